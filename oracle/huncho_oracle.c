@@ -1,0 +1,680 @@
+/*
+ * huncho_oracle.c - CPU restatement of Huncho's Qwen3.5 (Kev) scoring-forward path.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity oracle and timed CPU baseline); see huncho_oracle.h.
+ * Compiled with -ffp-contract=off so every product and sum rounds separately, as in the
+ * reference's scalar loops (delta_cpu.rs:1-5). The dense projection lives in ho_gemm.c.
+ *
+ * Citations are to grafuls/huncho, relative to the repository root:
+ *   crates/huncho-backend/src/qwen3_5.rs       (model, norms, RoPE, GDN, MLP)
+ *   crates/huncho-backend/src/qwen3_5/attention.rs, qwen3_5/kv_pages.rs
+ *   crates/huncho-backend/src/delta_cpu.rs, conv_cpu.rs, gate_cpu.rs, kev.rs
+ *   crates/huncho-core/src/calibration.rs
+ */
+#include "huncho_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------- */
+/* numeric helpers                                                            */
+/* ------------------------------------------------------------------------- */
+
+uint16_t ho_f32_to_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+    uint32_t rounding = 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)((u + rounding) >> 16);
+}
+
+float ho_bf16_to_f32(uint16_t x) {
+    uint32_t u = (uint32_t)x << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static inline float rb(float x) { return ho_bf16_to_f32(ho_f32_to_bf16(x)); }
+
+void ho_round_bf16(float* x, size_t n) {
+    for (size_t i = 0; i < n; ++i) x[i] = rb(x[i]);
+}
+void ho_to_bf16(const float* x, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = ho_f32_to_bf16(x[i]);
+}
+void ho_from_bf16(const uint16_t* x, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = ho_bf16_to_f32(x[i]);
+}
+
+/* splitmix64 (Steele, Lea, Flood 2014; Vigna's constants). */
+static inline uint64_t splitmix64(uint64_t* s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+static inline uint64_t stream_state(uint64_t seed, uint64_t stream) {
+    return seed ^ (stream * 0xD1B54A32D192ED03ull);
+}
+
+void ho_normal_fill(uint64_t seed, uint64_t stream, float* out, size_t n, float mean, float std) {
+    /* Each 64-bit draw gives two 24-bit uniforms; Box-Muller in double precision. */
+    uint64_t s = stream_state(seed, stream);
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i += 2) {
+        uint64_t z = splitmix64(&s);
+        double u1 = ((double)(z >> 40) + 0.5) * (1.0 / 16777216.0);
+        double u2 = (double)((z >> 16) & 0xFFFFFFull) * (1.0 / 16777216.0);
+        double r = sqrt(-2.0 * log(u1));
+        out[i] = (float)(mean + std * (r * cos(two_pi * u2)));
+        if (i + 1 < n) out[i + 1] = (float)(mean + std * (r * sin(two_pi * u2)));
+    }
+}
+
+static uint64_t uniform_below(uint64_t* s, uint64_t range) {
+    uint64_t limit = UINT64_MAX - (UINT64_MAX % range);
+    uint64_t z;
+    do {
+        z = splitmix64(s);
+    } while (z >= limit);
+    return z % range;
+}
+
+void ho_uniform_int_fill(uint64_t seed, uint64_t stream, int32_t* out, size_t n, int32_t lo, int32_t hi) {
+    uint64_t s = stream_state(seed, stream);
+    uint64_t range = (uint64_t)((int64_t)hi - (int64_t)lo + 1);
+    for (size_t i = 0; i < n; ++i) out[i] = (int32_t)((int64_t)lo + (int64_t)uniform_below(&s, range));
+}
+
+void ho_permutation(uint64_t seed, uint64_t stream, int32_t* out, int32_t n) {
+    uint64_t s = stream_state(seed, stream);
+    for (int32_t i = 0; i < n; ++i) out[i] = i;
+    for (int32_t i = n - 1; i > 0; --i) {
+        int32_t j = (int32_t)uniform_below(&s, (uint64_t)i + 1);
+        int32_t t = out[i];
+        out[i] = out[j];
+        out[j] = t;
+    }
+}
+
+void ho_set_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+int ho_get_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+static inline float silu_f(float x) { return x / (1.0f + expf(-x)); }
+static inline float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* ------------------------------------------------------------------------- */
+/* norms                                                                     */
+/* ------------------------------------------------------------------------- */
+
+/* qwen3_5.rs:184-190: var = mean(x^2); y = x / sqrt(var + eps) * w_eff (fp32). */
+void ho_rms_norm_effective(const float* x, const float* w_eff, int rows, int width, float eps,
+                           float* y) {
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (size_t)r * width;
+        float ss = 0.0f;
+        for (int i = 0; i < width; ++i) ss += xr[i] * xr[i];
+        float var = ss / (float)width;
+        float denom = sqrtf(var + eps);
+        for (int i = 0; i < width; ++i) y[(size_t)r * width + i] = (xr[i] / denom) * w_eff[i];
+    }
+}
+
+/* qwen3_5.rs:193-201: rms_norm(x) * w * silu(z), plain weight (not 1 + w). */
+void ho_rms_norm_gated(const float* x, const float* z, const float* w, int rows, int width,
+                       float eps, float* y) {
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (size_t)r * width;
+        const float* zr = z + (size_t)r * width;
+        float ss = 0.0f;
+        for (int i = 0; i < width; ++i) ss += xr[i] * xr[i];
+        float denom = sqrtf(ss / (float)width + eps);
+        for (int i = 0; i < width; ++i)
+            y[(size_t)r * width + i] = ((xr[i] / denom) * w[i]) * silu_f(zr[i]);
+    }
+}
+
+/* qwen3_5.rs:204-210: x * (sum(x^2) + eps)^-1/2 (fp32). */
+void ho_l2norm(const float* x, int rows, int width, float eps, float* y) {
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (size_t)r * width;
+        float ss = 0.0f;
+        for (int i = 0; i < width; ++i) ss += xr[i] * xr[i];
+        float inv = 1.0f / sqrtf(ss + eps);
+        for (int i = 0; i < width; ++i) y[(size_t)r * width + i] = xr[i] * inv;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* rotary                                                                    */
+/* ------------------------------------------------------------------------- */
+
+/* qwen3_5.rs:168-171 */
+int ho_rotary_dim(int head_dim, double partial_rotary_factor) {
+    int d = (int)llround((double)head_dim * partial_rotary_factor);
+    if (d < 2) d = 2;
+    return d & ~1;
+}
+
+/* qwen3_5.rs:225-247: inv_freq_i = theta^(-2i/rd) in f32; freqs = pos * inv_freq;
+ * emb = [freqs, freqs]; cos/sin in f32, cast to the model dtype. */
+void ho_rope_cos_sin(int rd, double theta, const int32_t* positions, int n, int bf16_mode,
+                     float* cos_out, float* sin_out) {
+    int half = rd / 2;
+    for (int t = 0; t < n; ++t) {
+        float pos = (float)positions[t];
+        for (int i = 0; i < half; ++i) {
+            float inv = powf((float)theta, -(2.0f * (float)i) / (float)rd);
+            float f = pos * inv;
+            float c = cosf(f), s = sinf(f);
+            if (bf16_mode) {
+                c = rb(c);
+                s = rb(s);
+            }
+            cos_out[(size_t)t * rd + i] = c;
+            cos_out[(size_t)t * rd + half + i] = c;
+            sin_out[(size_t)t * rd + i] = s;
+            sin_out[(size_t)t * rd + half + i] = s;
+        }
+    }
+}
+
+/* qwen3_5.rs:249-283: x_rot*cos + rotate_half(x_rot)*sin on the first rd dims. */
+void ho_apply_rope(float* x, int n, int heads, int head_dim, int rd, const float* cos_t,
+                   const float* sin_t) {
+    int half = rd / 2;
+    float tmp[1024];
+    for (int t = 0; t < n; ++t)
+        for (int h = 0; h < heads; ++h) {
+            float* xh = x + ((size_t)t * heads + h) * head_dim;
+            const float* c = cos_t + (size_t)t * rd;
+            const float* s = sin_t + (size_t)t * rd;
+            for (int i = 0; i < rd; ++i) {
+                float rot = i < half ? -xh[i + half] : xh[i - half];
+                float a = xh[i] * c[i];
+                float b = rot * s[i];
+                tmp[i] = a + b;
+            }
+            for (int i = 0; i < rd; ++i) xh[i] = tmp[i];
+        }
+}
+
+/* ------------------------------------------------------------------------- */
+/* paged KV                                                                  */
+/* ------------------------------------------------------------------------- */
+
+/* kv_pages.rs:307-341 appends rows to the tail page, then whole pages, in token order;
+ * materialize (63-98) concatenates pages in list order. With an explicit block table
+ * the page list of a sequence is block_tables[s][0..], so token j sits at
+ * (block_tables[s][j / P], j % P). */
+int ho_paged_kv_write(const void* k, const void* v, int elem_bytes, const int32_t* cu_seqlens,
+                      const int32_t* positions, int n_seqs, int kv_heads, int head_dim,
+                      int page_size, const int32_t* block_tables, int bt_stride, int num_pages,
+                      void* k_pool, void* v_pool) {
+    size_t row = (size_t)head_dim * elem_bytes;
+    for (int s = 0; s < n_seqs; ++s) {
+        for (int t = cu_seqlens[s]; t < cu_seqlens[s + 1]; ++t) {
+            int pos = positions[t];
+            if (pos < 0 || pos / page_size >= bt_stride) return -1;
+            int page = block_tables[(size_t)s * bt_stride + pos / page_size];
+            if (page < 0 || page >= num_pages) return -1;
+            int slot = pos % page_size;
+            for (int h = 0; h < kv_heads; ++h) {
+                size_t src = ((size_t)t * kv_heads + h) * row;
+                size_t dst = (((size_t)page * kv_heads + h) * page_size + slot) * row;
+                memcpy((char*)k_pool + dst, (const char*)k + src, row);
+                memcpy((char*)v_pool + dst, (const char*)v + src, row);
+            }
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* attention                                                                 */
+/* ------------------------------------------------------------------------- */
+
+/* One query row against keys 0..last through the block table. Follows the dense path
+ * qwen3_5.rs:697-701: scores = (q.k) * scale; + causal mask (future keys are -inf and
+ * contribute exp(-inf) = 0, so they are skipped); softmax = exp(s - max) / sum (in key
+ * order); o = sum_j p_j v_j in key order. */
+static void attend_row(const float* qrow, int last, const int32_t* table, int kvh, int kv_heads,
+                       int head_dim, int page_size, float scale, const void* k_pool,
+                       const void* v_pool, int is_bf16, float* scores, float* orow) {
+    float m = -INFINITY;
+    for (int j = 0; j <= last; ++j) {
+        int page = table[j / page_size], slot = j % page_size;
+        size_t off = (((size_t)page * kv_heads + kvh) * page_size + slot) * head_dim;
+        float dot = 0.0f;
+        if (is_bf16) {
+            const uint16_t* kr = (const uint16_t*)k_pool + off;
+            for (int i = 0; i < head_dim; ++i) dot += qrow[i] * ho_bf16_to_f32(kr[i]);
+        } else {
+            const float* kr = (const float*)k_pool + off;
+            for (int i = 0; i < head_dim; ++i) dot += qrow[i] * kr[i];
+        }
+        scores[j] = dot * scale;
+        if (scores[j] > m) m = scores[j];
+    }
+    float sum = 0.0f;
+    for (int j = 0; j <= last; ++j) {
+        scores[j] = expf(scores[j] - m);
+        sum += scores[j];
+    }
+    for (int i = 0; i < head_dim; ++i) orow[i] = 0.0f;
+    for (int j = 0; j <= last; ++j) {
+        float p = scores[j] / sum;
+        int page = table[j / page_size], slot = j % page_size;
+        size_t off = (((size_t)page * kv_heads + kvh) * page_size + slot) * head_dim;
+        if (is_bf16) {
+            const uint16_t* vr = (const uint16_t*)v_pool + off;
+            for (int i = 0; i < head_dim; ++i) orow[i] += p * ho_bf16_to_f32(vr[i]);
+        } else {
+            const float* vr = (const float*)v_pool + off;
+            for (int i = 0; i < head_dim; ++i) orow[i] += p * vr[i];
+        }
+    }
+}
+
+static int paged_attention(const void* q, int q_is_bf16, const void* k_pool, const void* v_pool,
+                           const int32_t* block_tables, int bt_stride, const int32_t* cu_seqlens_q,
+                           const int32_t* context_lens, int n_seqs, int q_heads, int kv_heads,
+                           int head_dim, int page_size, float scale, float* o) {
+    if (kv_heads <= 0 || q_heads % kv_heads != 0 || head_dim > 1024) return -1;
+    int group = q_heads / kv_heads;
+    for (int s = 0; s < n_seqs; ++s) {
+        int ql = cu_seqlens_q[s + 1] - cu_seqlens_q[s];
+        if (ql < 0 || context_lens[s] < ql || (context_lens[s] + page_size - 1) / page_size > bt_stride)
+            return -1;
+    }
+    int max_ctx = 0;
+    for (int s = 0; s < n_seqs; ++s)
+        if (context_lens[s] > max_ctx) max_ctx = context_lens[s];
+    int total_q = cu_seqlens_q[n_seqs];
+#pragma omp parallel
+    {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)(max_ctx > 0 ? max_ctx : 1));
+        float qrow[1024];
+#pragma omp for schedule(dynamic, 4)
+        for (long idx = 0; idx < (long)total_q * q_heads; ++idx) {
+            int t = (int)(idx / q_heads), h = (int)(idx % q_heads);
+            int s = 0;
+            while (cu_seqlens_q[s + 1] <= t) ++s;
+            int ql = cu_seqlens_q[s + 1] - cu_seqlens_q[s];
+            int pos = context_lens[s] - ql + (t - cu_seqlens_q[s]);
+            size_t qoff = ((size_t)t * q_heads + h) * head_dim;
+            for (int i = 0; i < head_dim; ++i)
+                qrow[i] = q_is_bf16 ? ho_bf16_to_f32(((const uint16_t*)q)[qoff + i])
+                                    : ((const float*)q)[qoff + i];
+            attend_row(qrow, pos, block_tables + (size_t)s * bt_stride, h / group, kv_heads, head_dim,
+                       page_size, scale, k_pool, v_pool, q_is_bf16, scores, o + qoff);
+        }
+        free(scores);
+    }
+    return 0;
+}
+
+int ho_paged_attention_f32(const float* q, const float* k_pool, const float* v_pool,
+                           const int32_t* block_tables, int bt_stride, const int32_t* cu_seqlens_q,
+                           const int32_t* context_lens, int n_seqs, int q_heads, int kv_heads,
+                           int head_dim, int page_size, float scale, float* o) {
+    return paged_attention(q, 0, k_pool, v_pool, block_tables, bt_stride, cu_seqlens_q, context_lens,
+                           n_seqs, q_heads, kv_heads, head_dim, page_size, scale, o);
+}
+
+int ho_paged_attention_bf16(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                            const int32_t* block_tables, int bt_stride,
+                            const int32_t* cu_seqlens_q, const int32_t* context_lens, int n_seqs,
+                            int q_heads, int kv_heads, int head_dim, int page_size, float scale,
+                            float* o) {
+    return paged_attention(q, 1, k_pool, v_pool, block_tables, bt_stride, cu_seqlens_q, context_lens,
+                           n_seqs, q_heads, kv_heads, head_dim, page_size, scale, o);
+}
+
+/* ------------------------------------------------------------------------- */
+/* gated delta rule                                                          */
+/* ------------------------------------------------------------------------- */
+
+/* delta_cpu.rs:95-131: per token, decay = exp(g); one pass does cell *= decay and
+ * memory += cell*k_i (i over dk outer, j over dv inner); delta = (v - memory) * beta;
+ * a second pass does cell += k_i*delta_j and out_j += cell*q_i. */
+int ho_gated_delta_rule(const float* q, const float* k, const float* v, const float* g,
+                        const float* beta, const int32_t* cu_seqlens, int n_seqs, int heads,
+                        int dk, int dv, const float* initial_state, float* o, float* final_state) {
+    if (n_seqs <= 0 || heads <= 0 || dk <= 0 || dv <= 0 || dv > 4096) return -1;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+    for (int s = 0; s < n_seqs; ++s)
+        for (int h = 0; h < heads; ++h) {
+            size_t msz = (size_t)dk * dv;
+            float* state = (float*)malloc(sizeof(float) * msz);
+            float delta[4096];
+            if (initial_state)
+                memcpy(state, initial_state + ((size_t)s * heads + h) * msz, sizeof(float) * msz);
+            else
+                memset(state, 0, sizeof(float) * msz);
+            for (int t = cu_seqlens[s]; t < cu_seqlens[s + 1]; ++t) {
+                const float* qt = q + ((size_t)t * heads + h) * dk;
+                const float* kt = k + ((size_t)t * heads + h) * dk;
+                const float* vt = v + ((size_t)t * heads + h) * dv;
+                float decay = expf(g[(size_t)t * heads + h]);
+                float b = beta[(size_t)t * heads + h];
+                float* out = o + ((size_t)t * heads + h) * dv;
+                for (int j = 0; j < dv; ++j) delta[j] = 0.0f;
+                for (int i = 0; i < dk; ++i) {
+                    float ki = kt[i];
+                    float* row = state + (size_t)i * dv;
+                    for (int j = 0; j < dv; ++j) {
+                        row[j] *= decay;
+                        delta[j] += row[j] * ki;
+                    }
+                }
+                for (int j = 0; j < dv; ++j) delta[j] = (vt[j] - delta[j]) * b;
+                for (int j = 0; j < dv; ++j) out[j] = 0.0f;
+                for (int i = 0; i < dk; ++i) {
+                    float ki = kt[i], qi = qt[i];
+                    float* row = state + (size_t)i * dv;
+                    for (int j = 0; j < dv; ++j) {
+                        row[j] += ki * delta[j];
+                        out[j] += row[j] * qi;
+                    }
+                }
+            }
+            if (final_state) memcpy(final_state + ((size_t)s * heads + h) * msz, state, sizeof(float) * msz);
+            free(state);
+        }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* causal conv                                                               */
+/* ------------------------------------------------------------------------- */
+
+/* conv_cpu.rs:34-48 over the history-prepended sequence (qwen3_5.rs:851-870):
+ * out[c][t] = sum over taps in ascending order of w[c][tap] * x[c][t-(K-1)+tap],
+ * accumulated from 0 (taps before the start are skipped); then SiLU in fp32. */
+void ho_causal_conv1d_silu(const float* x, int T, int C, const float* w, int K,
+                           const float* history, float* out, float* tail_out) {
+    int H = history ? K - 1 : 0;
+#pragma omp parallel for schedule(static)
+    for (int c = 0; c < C; ++c) {
+        for (int t = 0; t < T; ++t) {
+            float acc = 0.0f;
+            int tt = t + H; /* index in the concatenated [history, x] sequence */
+            for (int tap = 0; tap < K; ++tap) {
+                int shift = K - 1 - tap;
+                if (tt - shift < 0) continue;
+                int src = tt - shift;
+                float xv = src < H ? history[(size_t)c * (K - 1) + src] : x[(size_t)(src - H) * C + c];
+                acc += w[(size_t)c * K + tap] * xv;
+            }
+            out[(size_t)t * C + c] = silu_f(acc);
+        }
+        if (tail_out) {
+            /* The last K-1 inputs of the concatenated sequence (qwen3_5.rs:856-868). */
+            int total = T + H;
+            for (int i = 0; i < K - 1; ++i) {
+                int src = total - (K - 1) + i;
+                float xv = 0.0f;
+                if (src >= 0) xv = src < H ? history[(size_t)c * (K - 1) + src] : x[(size_t)(src - H) * C + c];
+                tail_out[(size_t)c * (K - 1) + i] = xv;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Qwen3.5 model                                                              */
+/* ------------------------------------------------------------------------- */
+
+static void round_if(float* x, size_t n, int on) {
+    if (on) ho_round_bf16(x, n);
+}
+
+/* Attention::forward, qwen3_5.rs:586-726 (fresh cache, dense path). */
+static void full_attention(const ho_qwen_cfg* c, const ho_qwen_layer* L, const float* x, int T,
+                           int bf, float* out /* [T][hidden] */) {
+    int Hq = c->n_heads, Hkv = c->n_kv_heads, d = c->head_dim, hid = c->hidden;
+    float* qg = (float*)malloc(sizeof(float) * (size_t)T * 2 * Hq * d);
+    float* q = (float*)malloc(sizeof(float) * (size_t)T * Hq * d);
+    float* gate = (float*)malloc(sizeof(float) * (size_t)T * Hq * d);
+    float* kk = (float*)malloc(sizeof(float) * (size_t)T * Hkv * d);
+    float* vv = (float*)malloc(sizeof(float) * (size_t)T * Hkv * d);
+    float* att = (float*)malloc(sizeof(float) * (size_t)T * Hq * d);
+    float* cs = (float*)malloc(sizeof(float) * (size_t)T * c->rotary_dim);
+    float* sn = (float*)malloc(sizeof(float) * (size_t)T * c->rotary_dim);
+    int32_t* pos = (int32_t*)malloc(sizeof(int32_t) * (size_t)T);
+    ho_linear(x, L->q_proj, NULL, T, hid, 2 * Hq * d, qg);
+    round_if(qg, (size_t)T * 2 * Hq * d, bf);
+    /* per-head [q | gate] split (596-599) */
+    for (int t = 0; t < T; ++t)
+        for (int h = 0; h < Hq; ++h) {
+            memcpy(q + ((size_t)t * Hq + h) * d, qg + ((size_t)t * Hq + h) * 2 * d, sizeof(float) * d);
+            memcpy(gate + ((size_t)t * Hq + h) * d, qg + ((size_t)t * Hq + h) * 2 * d + d, sizeof(float) * d);
+        }
+    ho_rms_norm_effective(q, L->q_norm_eff, T * Hq, d, c->eps, q);
+    round_if(q, (size_t)T * Hq * d, bf);
+    ho_linear(x, L->k_proj, NULL, T, hid, Hkv * d, kk);
+    round_if(kk, (size_t)T * Hkv * d, bf);
+    ho_rms_norm_effective(kk, L->k_norm_eff, T * Hkv, d, c->eps, kk);
+    round_if(kk, (size_t)T * Hkv * d, bf);
+    ho_linear(x, L->v_proj, NULL, T, hid, Hkv * d, vv);
+    round_if(vv, (size_t)T * Hkv * d, bf);
+    for (int t = 0; t < T; ++t) pos[t] = t;
+    ho_rope_cos_sin(c->rotary_dim, c->rope_theta, pos, T, bf, cs, sn);
+    ho_apply_rope(q, T, Hq, d, c->rotary_dim, cs, sn);
+    round_if(q, (size_t)T * Hq * d, bf);
+    ho_apply_rope(kk, T, Hkv, d, c->rotary_dim, cs, sn);
+    round_if(kk, (size_t)T * Hkv * d, bf);
+    /* Dense causal softmax attention: one page of T rows ([Hkv][T][d]) with table {0}
+     * is exactly the materialized K/V of the reference's default path. */
+    int32_t cu[2] = {0, T}, ctx[1] = {T}, table[1] = {0};
+    {
+        float* kp = (float*)malloc(sizeof(float) * (size_t)T * Hkv * d);
+        float* vp = (float*)malloc(sizeof(float) * (size_t)T * Hkv * d);
+        for (int t = 0; t < T; ++t)
+            for (int h = 0; h < Hkv; ++h) {
+                memcpy(kp + ((size_t)h * T + t) * d, kk + ((size_t)t * Hkv + h) * d, sizeof(float) * d);
+                memcpy(vp + ((size_t)h * T + t) * d, vv + ((size_t)t * Hkv + h) * d, sizeof(float) * d);
+            }
+        ho_paged_attention_f32(q, kp, vp, table, 1, cu, ctx, 1, Hq, Hkv, d, T, (float)(1.0 / sqrt((double)d)), att);
+        free(kp);
+        free(vp);
+    }
+    round_if(att, (size_t)T * Hq * d, bf);
+    /* output gate (706-714): sigmoid in fp32, cast, multiply in the activation dtype */
+    for (size_t i = 0; i < (size_t)T * Hq * d; ++i) {
+        float gt = sigmoid_f(gate[i]);
+        if (bf) gt = rb(gt);
+        float a = att[i] * gt;
+        att[i] = bf ? rb(a) : a;
+    }
+    ho_linear(att, L->o_proj, NULL, T, Hq * d, hid, out);
+    round_if(out, (size_t)T * hid, bf);
+    free(qg); free(q); free(gate); free(kk); free(vv); free(att); free(cs); free(sn); free(pos);
+}
+
+/* LinearAttn::forward, qwen3_5.rs:846-946 (fresh cache). */
+static void linear_attention(const ho_qwen_cfg* c, const ho_qwen_layer* L, const float* x, int T,
+                             int bf, float* out) {
+    int hid = c->hidden, Hk = c->lin_n_k_heads, Hv = c->lin_n_v_heads, dk = c->lin_key_dim,
+        dv = c->lin_v_dim, K = c->conv_k;
+    int key_dim = Hk * dk, value_dim = Hv * dv, conv_dim = 2 * key_dim + value_dim;
+    float* mixed = (float*)malloc(sizeof(float) * (size_t)T * conv_dim);
+    float* conv = (float*)malloc(sizeof(float) * (size_t)T * conv_dim);
+    float* z = (float*)malloc(sizeof(float) * (size_t)T * value_dim);
+    float* bproj = (float*)malloc(sizeof(float) * (size_t)T * Hv);
+    float* aproj = (float*)malloc(sizeof(float) * (size_t)T * Hv);
+    float* q = (float*)malloc(sizeof(float) * (size_t)T * Hv * dk);
+    float* k = (float*)malloc(sizeof(float) * (size_t)T * Hv * dk);
+    float* v = (float*)malloc(sizeof(float) * (size_t)T * Hv * dv);
+    float* g = (float*)malloc(sizeof(float) * (size_t)T * Hv);
+    float* beta = (float*)malloc(sizeof(float) * (size_t)T * Hv);
+    float* o = (float*)malloc(sizeof(float) * (size_t)T * Hv * dv);
+    float* normed = (float*)malloc(sizeof(float) * (size_t)T * value_dim);
+    ho_linear(x, L->in_qkv, NULL, T, hid, conv_dim, mixed);
+    round_if(mixed, (size_t)T * conv_dim, bf);
+    ho_causal_conv1d_silu(mixed, T, conv_dim, L->conv_w, K, NULL, conv, NULL);
+    round_if(conv, (size_t)T * conv_dim, bf); /* silu(out).to_dtype(x.dtype()) (843) */
+    ho_linear(x, L->in_z, NULL, T, hid, value_dim, z);
+    round_if(z, (size_t)T * value_dim, bf);
+    ho_linear(x, L->in_b, NULL, T, hid, Hv, bproj);
+    round_if(bproj, (size_t)T * Hv, bf);
+    ho_linear(x, L->in_a, NULL, T, hid, Hv, aproj);
+    round_if(aproj, (size_t)T * Hv, bf);
+    int n_rep = (Hv % Hk == 0) ? Hv / Hk : 1;
+    float scale = (float)(1.0 / sqrt((double)dk));
+    for (int t = 0; t < T; ++t) {
+        const float* row = conv + (size_t)t * conv_dim;
+        for (int h = 0; h < Hv; ++h) {
+            int kh = h / n_rep; /* repeat_interleave_head (285-296, 901-915) */
+            float* qd = q + ((size_t)t * Hv + h) * dk;
+            float* kd = k + ((size_t)t * Hv + h) * dk;
+            ho_l2norm(row + (size_t)kh * dk, 1, dk, 1e-6f, qd);
+            for (int i = 0; i < dk; ++i) qd[i] = qd[i] * scale; /* affine(scale, 0) (923) */
+            ho_l2norm(row + key_dim + (size_t)kh * dk, 1, dk, 1e-6f, kd);
+            memcpy(v + ((size_t)t * Hv + h) * dv, row + 2 * key_dim + (size_t)h * dv, sizeof(float) * dv);
+            /* beta = sigmoid(b) in the activation dtype (893); g = -exp(A_log) * softplus(a + dt_bias) (894-899) */
+            float bt = sigmoid_f(bproj[(size_t)t * Hv + h]);
+            beta[(size_t)t * Hv + h] = bf ? rb(bt) : bt;
+            float base_g = -expf(L->a_log[h]);
+            float sp = logf(expf(aproj[(size_t)t * Hv + h] + L->dt_bias[h]) + 1.0f);
+            g[(size_t)t * Hv + h] = base_g * sp;
+        }
+    }
+    int32_t cu[2] = {0, T};
+    ho_gated_delta_rule(q, k, v, g, beta, cu, 1, Hv, dk, dv, NULL, o, NULL);
+    round_if(o, (size_t)T * Hv * dv, bf); /* out.to_dtype(self.dtype) (936) */
+    ho_rms_norm_gated(o, z, L->norm_w, T * Hv, dv, c->eps, normed);
+    round_if(normed, (size_t)T * value_dim, bf);
+    ho_linear(normed, L->out_proj, NULL, T, value_dim, hid, out);
+    round_if(out, (size_t)T * hid, bf);
+    free(mixed); free(conv); free(z); free(bproj); free(aproj); free(q); free(k); free(v);
+    free(g); free(beta); free(o); free(normed);
+}
+
+/* Mlp::forward, qwen3_5.rs:1020-1031: down(silu(gate(x)) * up(x)). */
+static void mlp(const ho_qwen_cfg* c, const ho_qwen_layer* L, const float* x, int T, int bf, float* out) {
+    int hid = c->hidden, I = c->intermediate;
+    float* ga = (float*)malloc(sizeof(float) * (size_t)T * I);
+    float* up = (float*)malloc(sizeof(float) * (size_t)T * I);
+    ho_linear(x, L->gate_proj, NULL, T, hid, I, ga);
+    round_if(ga, (size_t)T * I, bf);
+    ho_linear(x, L->up_proj, NULL, T, hid, I, up);
+    round_if(up, (size_t)T * I, bf);
+    for (size_t i = 0; i < (size_t)T * I; ++i) {
+        float s = silu_f(ga[i]);
+        if (bf) s = rb(s);
+        float p = s * up[i];
+        ga[i] = bf ? rb(p) : p;
+    }
+    ho_linear(ga, L->down_proj, NULL, T, I, hid, out);
+    round_if(out, (size_t)T * hid, bf);
+    free(ga);
+    free(up);
+}
+
+/* Model::forward_inner (1533-1553) and DecoderLayer::forward (1083-1104). */
+int ho_qwen_forward(const ho_qwen_cfg* cfg, const ho_qwen_layer* layers, const float* embed,
+                    const float* final_norm_eff, const int32_t* ids, int T, int bf16_mode,
+                    float* hidden_out) {
+    int hid = cfg->hidden;
+    if (T <= 0) return -1;
+    for (int t = 0; t < T; ++t)
+        if (ids[t] < 0 || ids[t] >= cfg->vocab) return -1;
+    float* x = (float*)malloc(sizeof(float) * (size_t)T * hid);
+    float* h = (float*)malloc(sizeof(float) * (size_t)T * hid);
+    float* y = (float*)malloc(sizeof(float) * (size_t)T * hid);
+    for (int t = 0; t < T; ++t) memcpy(x + (size_t)t * hid, embed + (size_t)ids[t] * hid, sizeof(float) * hid);
+    for (int l = 0; l < cfg->n_layers; ++l) {
+        const ho_qwen_layer* L = layers + l;
+        ho_rms_norm_effective(x, L->input_norm_eff, T, hid, cfg->eps, h);
+        round_if(h, (size_t)T * hid, bf16_mode);
+        if (cfg->layer_types[l] == 1)
+            full_attention(cfg, L, h, T, bf16_mode, y);
+        else
+            linear_attention(cfg, L, h, T, bf16_mode, y);
+        for (size_t i = 0; i < (size_t)T * hid; ++i) {
+            float s = y[i] + x[i];
+            x[i] = bf16_mode ? rb(s) : s; /* h = mixer + residual */
+        }
+        ho_rms_norm_effective(x, L->post_norm_eff, T, hid, cfg->eps, h);
+        round_if(h, (size_t)T * hid, bf16_mode);
+        mlp(cfg, L, h, T, bf16_mode, y);
+        for (size_t i = 0; i < (size_t)T * hid; ++i) {
+            float s = y[i] + x[i];
+            x[i] = bf16_mode ? rb(s) : s;
+        }
+    }
+    ho_rms_norm_effective(x, final_norm_eff, T, hid, cfg->eps, hidden_out);
+    round_if(hidden_out, (size_t)T * hid, bf16_mode);
+    free(x);
+    free(h);
+    free(y);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* readout and calibration                                                   */
+/* ------------------------------------------------------------------------- */
+
+void ho_pointer_head(const float* hidden, int hidden_size, int T, const int32_t* positions,
+                     int n_pos, const float* wq, const float* bq, const float* wk,
+                     const float* bk, int head_dim, float* scores) {
+    float q[1024], kv[1024];
+    const float* last = hidden + (size_t)(T - 1) * hidden_size;
+    for (int o = 0; o < head_dim; ++o) {
+        float acc = 0.0f;
+        for (int i = 0; i < hidden_size; ++i) acc += last[i] * wq[(size_t)o * hidden_size + i];
+        q[o] = acc + bq[o];
+    }
+    float scale = (float)(1.0 / sqrt((double)head_dim));
+    for (int p = 0; p < n_pos; ++p) {
+        const float* hp = hidden + (size_t)positions[p] * hidden_size;
+        for (int o = 0; o < head_dim; ++o) {
+            float acc = 0.0f;
+            for (int i = 0; i < hidden_size; ++i) acc += hp[i] * wk[(size_t)o * hidden_size + i];
+            kv[o] = acc + bk[o];
+        }
+        float dot = 0.0f;
+        for (int o = 0; o < head_dim; ++o) dot += kv[o] * q[o];
+        scores[p] = dot * scale;
+    }
+}
+
+int ho_calibrate(const float* logits, int n, float temperature, float* probs) {
+    if (!(temperature > 0.0f) || !isfinite(temperature)) return -1;
+    for (int i = 0; i < n; ++i)
+        if (!isfinite(logits[i])) return -1;
+    if (n == 0) return 0;
+    float inv_t = 1.0f / temperature;
+    float m = -INFINITY;
+    for (int i = 0; i < n; ++i) m = logits[i] > m ? logits[i] : m;
+    double sum = 0.0;
+    for (int i = 0; i < n; ++i) {
+        float e = expf((logits[i] - m) * inv_t);
+        probs[i] = e;
+        sum += (double)e;
+    }
+    for (int i = 0; i < n; ++i) {
+        probs[i] = (float)((double)probs[i] / sum);
+        if (!isfinite(probs[i])) return -1;
+    }
+    return 0;
+}

@@ -1,0 +1,444 @@
+"""ctypes wrapper over the C oracle (oracle/huncho_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the parity checker and the timed CPU baseline. Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, and only
+as the checker; the product (huncho_amd, libhuncho_rocm) never does.
+
+Besides the C entry points this module restates, in numpy, the two load-time steps the
+full-model oracle needs:
+  * Config::from_value (crates/huncho-backend/src/qwen3_5.rs:77-166), and
+  * merge_lora_into_map (qwen3_5.rs:1597-1640): W' = W + (alpha/r) * (B @ A) in fp32.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import math
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "libhuncho_oracle.so"
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"oracle library not built: {LIB_PATH} (run `make -C oracle`)")
+        L = C.CDLL(str(LIB_PATH))
+        L.ho_f32_to_bf16.restype = C.c_uint16
+        L.ho_f32_to_bf16.argtypes = [C.c_float]
+        L.ho_normal_fill.argtypes = [C.c_uint64, C.c_uint64, _f32p, C.c_size_t, C.c_float, C.c_float]
+        L.ho_uniform_int_fill.argtypes = [C.c_uint64, C.c_uint64, _i32p, C.c_size_t, C.c_int32, C.c_int32]
+        L.ho_permutation.argtypes = [C.c_uint64, C.c_uint64, _i32p, C.c_int32]
+        L.ho_round_bf16.argtypes = [_f32p, C.c_size_t]
+        L.ho_set_threads.argtypes = [C.c_int]
+        L.ho_get_threads.restype = C.c_int
+        L.ho_rms_norm_effective.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_float, _f32p]
+        L.ho_rms_norm_gated.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_float, _f32p]
+        L.ho_l2norm.argtypes = [_f32p, C.c_int, C.c_int, C.c_float, _f32p]
+        L.ho_rotary_dim.restype = C.c_int
+        L.ho_rotary_dim.argtypes = [C.c_int, C.c_double]
+        L.ho_rope_cos_sin.argtypes = [C.c_int, C.c_double, _i32p, C.c_int, C.c_int, _f32p, _f32p]
+        L.ho_apply_rope.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, _f32p]
+        L.ho_paged_kv_write.restype = C.c_int
+        L.ho_paged_kv_write.argtypes = [C.c_void_p, C.c_void_p, C.c_int, _i32p, _i32p, C.c_int, C.c_int,
+                                        C.c_int, C.c_int, _i32p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        L.ho_paged_attention_f32.restype = C.c_int
+        L.ho_paged_attention_f32.argtypes = [_f32p, _f32p, _f32p, _i32p, C.c_int, _i32p, _i32p, C.c_int,
+                                             C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _f32p]
+        L.ho_paged_attention_bf16.restype = C.c_int
+        L.ho_paged_attention_bf16.argtypes = [_u16p, _u16p, _u16p, _i32p, C.c_int, _i32p, _i32p, C.c_int,
+                                              C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _f32p]
+        L.ho_gated_delta_rule.restype = C.c_int
+        L.ho_gated_delta_rule.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i32p, C.c_int, C.c_int,
+                                          C.c_int, C.c_int, C.c_void_p, _f32p, C.c_void_p]
+        L.ho_causal_conv1d_silu.argtypes = [_f32p, C.c_int, C.c_int, _f32p, C.c_int, C.c_void_p, _f32p,
+                                            C.c_void_p]
+        L.ho_linear.argtypes = [_f32p, _f32p, C.c_void_p, C.c_int, C.c_int, C.c_int, _f32p]
+        L.ho_pointer_head.argtypes = [_f32p, C.c_int, C.c_int, _i32p, C.c_int, _f32p, _f32p, _f32p, _f32p,
+                                      C.c_int, _f32p]
+        L.ho_calibrate.restype = C.c_int
+        L.ho_calibrate.argtypes = [_f32p, C.c_int, C.c_float, _f32p]
+        L.ho_qwen_forward.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def i32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------------------
+# numeric helpers
+# ---------------------------------------------------------------------------
+
+def bf16_bits(x) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round-to-nearest-even (vectorised restatement of
+    ho_f32_to_bf16)."""
+    x = f32(x)
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    return (np.ascontiguousarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x) -> np.ndarray:
+    return bf16_to_f32(bf16_bits(x))
+
+
+def normal(seed: int, stream: int, shape, mean=0.0, std=1.0) -> np.ndarray:
+    out = np.empty(int(np.prod(shape)), dtype=np.float32)
+    lib().ho_normal_fill(seed, stream, out, out.size, mean, std)
+    return out.reshape(shape)
+
+
+def uniform_int(seed: int, stream: int, n: int, lo: int, hi: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().ho_uniform_int_fill(seed, stream, out, n, lo, hi)
+    return out
+
+
+def permutation(seed: int, stream: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().ho_permutation(seed, stream, out, n)
+    return out
+
+
+def set_threads(n: int) -> None:
+    lib().ho_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().ho_get_threads())
+
+
+# ---------------------------------------------------------------------------
+# kernels
+# ---------------------------------------------------------------------------
+
+def rms_norm_effective(x, w_eff, eps):
+    x = f32(x)
+    y = np.empty_like(x)
+    width = x.shape[-1]
+    lib().ho_rms_norm_effective(x, f32(w_eff), x.size // width, width, eps, y)
+    return y
+
+
+def rms_norm_gated(x, z, w, eps):
+    x = f32(x)
+    y = np.empty_like(x)
+    width = x.shape[-1]
+    lib().ho_rms_norm_gated(x, f32(z), f32(w), x.size // width, width, eps, y)
+    return y
+
+
+def l2norm(x, eps=1e-6):
+    x = f32(x)
+    y = np.empty_like(x)
+    lib().ho_l2norm(x, x.size // x.shape[-1], x.shape[-1], eps, y)
+    return y
+
+
+def rotary_dim(head_dim, prf):
+    return int(lib().ho_rotary_dim(head_dim, prf))
+
+
+def rope_cos_sin(rd, theta, positions, bf16_mode=False):
+    positions = i32(positions)
+    n = positions.size
+    c = np.empty((n, rd), np.float32)
+    s = np.empty((n, rd), np.float32)
+    lib().ho_rope_cos_sin(rd, theta, positions, n, int(bf16_mode), c, s)
+    return c, s
+
+
+def apply_rope(x, rd, cos_t, sin_t):
+    """x [n, heads, d] -> rotated copy."""
+    y = f32(x).copy()
+    n, heads, d = y.shape
+    lib().ho_apply_rope(y, n, heads, d, rd, f32(cos_t), f32(sin_t))
+    return y
+
+
+def paged_kv_write(k, v, cu_seqlens, positions, block_tables, page_size, k_pool, v_pool):
+    """k,v [tokens, Hkv, d] (float32 or uint16 bf16 bits); pools [pages, Hkv, P, d] (same
+    dtype, updated in place)."""
+    assert k.dtype == v.dtype == k_pool.dtype == v_pool.dtype
+    assert k.flags.c_contiguous and k_pool.flags.c_contiguous
+    bt = i32(block_tables)
+    rc = lib().ho_paged_kv_write(_ptr(k), _ptr(v), k.dtype.itemsize, i32(cu_seqlens), i32(positions),
+                                 len(cu_seqlens) - 1, k.shape[1], k.shape[2], page_size, bt,
+                                 bt.shape[1], k_pool.shape[0], _ptr(k_pool), _ptr(v_pool))
+    if rc != 0:
+        raise ValueError("oracle paged_kv_write rejected its inputs")
+
+
+def paged_attention(q, k_pool, v_pool, block_tables, cu_seqlens_q, context_lens, page_size, scale):
+    """GQA causal attention through block tables. q [tokens, Hq, d]; returns fp32 o."""
+    bt = i32(block_tables)
+    tokens, hq, d = q.shape
+    hkv = k_pool.shape[1]
+    o = np.zeros((tokens, hq, d), np.float32)
+    n = len(cu_seqlens_q) - 1
+    if q.dtype == np.uint16:
+        rc = lib().ho_paged_attention_bf16(np.ascontiguousarray(q), np.ascontiguousarray(k_pool),
+                                           np.ascontiguousarray(v_pool), bt, bt.shape[1],
+                                           i32(cu_seqlens_q), i32(context_lens), n, hq, hkv, d,
+                                           page_size, scale, o)
+    else:
+        rc = lib().ho_paged_attention_f32(f32(q), f32(k_pool), f32(v_pool), bt, bt.shape[1],
+                                          i32(cu_seqlens_q), i32(context_lens), n, hq, hkv, d,
+                                          page_size, scale, o)
+    if rc != 0:
+        raise ValueError("oracle paged_attention rejected its inputs")
+    return o
+
+
+def gated_delta_rule(q, k, v, g, beta, cu_seqlens, initial_state=None, want_state=True):
+    """q,k [tokens,H,dk], v [tokens,H,dv], g,beta [tokens,H] (fp32). Returns (o, state)."""
+    q, k, v, g, beta = map(f32, (q, k, v, g, beta))
+    tokens, heads, dk = q.shape
+    dv = v.shape[2]
+    n = len(cu_seqlens) - 1
+    o = np.zeros((tokens, heads, dv), np.float32)
+    st = np.zeros((n, heads, dk, dv), np.float32) if want_state else None
+    init = None if initial_state is None else f32(initial_state)
+    rc = lib().ho_gated_delta_rule(q, k, v, g, beta, i32(cu_seqlens), n, heads, dk, dv, _ptr(init), o,
+                                   _ptr(st))
+    if rc != 0:
+        raise ValueError("oracle gated_delta_rule rejected its inputs")
+    return o, st
+
+
+def causal_conv1d_silu(x, w, history=None, want_tail=False):
+    """x [T, C] fp32 (one sequence), w [C, K]; returns (out [T, C], tail [C, K-1] | None)."""
+    x = f32(x)
+    T, Cc = x.shape
+    w = f32(w)
+    K = w.shape[1]
+    out = np.empty_like(x)
+    tail = np.empty((Cc, K - 1), np.float32) if want_tail else None
+    hist = None if history is None else f32(history)
+    lib().ho_causal_conv1d_silu(x, T, Cc, w, K, _ptr(hist), out, _ptr(tail))
+    return out, tail
+
+
+def linear(x, w, b=None):
+    x = f32(x)
+    w = f32(w)
+    n = x.size // x.shape[-1]
+    y = np.empty(x.shape[:-1] + (w.shape[0],), np.float32)
+    bb = None if b is None else f32(b)
+    lib().ho_linear(x, w, _ptr(bb), n, w.shape[1], w.shape[0], y)
+    return y
+
+
+def calibrate(logits, temperature):
+    """calibration.rs:170-173 (fp32 exp, fp64 ordered sum/divide)."""
+    x = f32(logits)
+    p = np.empty_like(x)
+    if lib().ho_calibrate(x, x.size, float(temperature), p) != 0:
+        raise ValueError("calibration rejected non-finite logits or temperature")
+    return p
+
+
+def pointer_head(hidden, positions, head):
+    """kev.rs:161-165 on final hidden states [T, hidden]."""
+    hidden = f32(hidden)
+    T, hs = hidden.shape
+    pos = i32(positions)
+    scores = np.empty(pos.size, np.float32)
+    lib().ho_pointer_head(hidden, hs, T, pos, pos.size, f32(head["q_weight"]), f32(head["q_bias"]),
+                          f32(head["k_weight"]), f32(head["k_bias"]), int(head["head_dim"]), scores)
+    return scores
+
+
+# ---------------------------------------------------------------------------
+# Qwen3.5 model
+# ---------------------------------------------------------------------------
+
+@dataclass
+class QwenConfig:
+    hidden_size: int
+    num_hidden_layers: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    head_dim: int
+    intermediate_size: int
+    vocab_size: int
+    rms_norm_eps: float
+    layer_types: list
+    linear_conv_kernel_dim: int = 4
+    linear_key_head_dim: int = 128
+    linear_num_key_heads: int = 16
+    linear_num_value_heads: int = 32
+    linear_value_head_dim: int = 128
+    rope_theta: float = 10000.0
+    partial_rotary_factor: float = 1.0
+
+    @property
+    def rotary_dim(self) -> int:
+        return rotary_dim(self.head_dim, self.partial_rotary_factor)
+
+    @staticmethod
+    def from_json(v: dict) -> "QwenConfig":
+        """qwen3_5.rs:77-166 (defaults included)."""
+        t = v.get("text_config", v)
+        hs = t.get("hidden_size", 4096)
+        n_layers = t.get("num_hidden_layers", 32)
+        n_heads = t.get("num_attention_heads", 16)
+        if "layer_types" in t:
+            lts = [1 if "full_attention" in s else 0 for s in t["layer_types"]]
+        else:
+            interval = max(t.get("full_attention_interval", 4), 1)
+            lts = [1 if (i + 1) % interval == 0 else 0 for i in range(n_layers)]
+        rp = t.get("rope_parameters") or {}
+        theta = rp.get("rope_theta", t.get("rope_theta", 10000.0))
+        prf = rp.get("partial_rotary_factor", t.get("partial_rotary_factor", 1.0))
+        return QwenConfig(
+            hidden_size=hs, num_hidden_layers=n_layers, num_attention_heads=n_heads,
+            num_key_value_heads=t.get("num_key_value_heads", 4),
+            head_dim=t.get("head_dim", hs // n_heads),
+            intermediate_size=t.get("intermediate_size", 12288),
+            vocab_size=t.get("vocab_size", 248320),
+            rms_norm_eps=float(t.get("rms_norm_eps", 1e-6)), layer_types=lts,
+            linear_conv_kernel_dim=t.get("linear_conv_kernel_dim", 4),
+            linear_key_head_dim=t.get("linear_key_head_dim", 128),
+            linear_num_key_heads=t.get("linear_num_key_heads", 16),
+            linear_num_value_heads=t.get("linear_num_value_heads", 32),
+            linear_value_head_dim=t.get("linear_value_head_dim", 128),
+            rope_theta=float(theta), partial_rotary_factor=float(prf))
+
+
+class _Cfg(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("n_layers", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("intermediate", C.c_int), ("vocab", C.c_int), ("eps", C.c_float),
+                ("rope_theta", C.c_double), ("rotary_dim", C.c_int), ("conv_k", C.c_int),
+                ("lin_key_dim", C.c_int), ("lin_n_k_heads", C.c_int), ("lin_n_v_heads", C.c_int),
+                ("lin_v_dim", C.c_int), ("layer_types", C.POINTER(C.c_int32))]
+
+
+_LAYER_FIELDS = ["input_norm_eff", "post_norm_eff", "gate_proj", "up_proj", "down_proj", "in_qkv", "in_z",
+                 "in_b", "in_a", "out_proj", "conv_w", "norm_w", "a_log", "dt_bias", "q_proj", "k_proj",
+                 "v_proj", "o_proj", "q_norm_eff", "k_norm_eff"]
+
+
+class _Layer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in _LAYER_FIELDS]
+
+
+# checkpoint names (qwen3_5.rs:536-584, 758-813, 1003-1018, 1044-1079)
+_NAME = {
+    "input_norm_eff": "input_layernorm.weight", "post_norm_eff": "post_attention_layernorm.weight",
+    "gate_proj": "mlp.gate_proj.weight", "up_proj": "mlp.up_proj.weight", "down_proj": "mlp.down_proj.weight",
+    "in_qkv": "linear_attn.in_proj_qkv.weight", "in_z": "linear_attn.in_proj_z.weight",
+    "in_b": "linear_attn.in_proj_b.weight", "in_a": "linear_attn.in_proj_a.weight",
+    "out_proj": "linear_attn.out_proj.weight", "conv_w": "linear_attn.conv1d.weight",
+    "norm_w": "linear_attn.norm.weight", "a_log": "linear_attn.A_log", "dt_bias": "linear_attn.dt_bias",
+    "q_proj": "self_attn.q_proj.weight", "k_proj": "self_attn.k_proj.weight",
+    "v_proj": "self_attn.v_proj.weight", "o_proj": "self_attn.o_proj.weight",
+    "q_norm_eff": "self_attn.q_norm.weight", "k_norm_eff": "self_attn.k_norm.weight",
+}
+_EFFECTIVE = {"input_norm_eff", "post_norm_eff", "q_norm_eff", "k_norm_eff"}
+
+PREFIX = "model.language_model."
+
+
+def merge_lora(weights: dict, lora: dict, scale: float) -> dict:
+    """qwen3_5.rs:1597-1640 + canonical_weight_name (2496-2512): W += scale * (B @ A), fp32."""
+    out = dict(weights)
+    targets = sorted({k[len("base_model.model."):-len(".lora_A.weight")] for k in lora
+                      if k.startswith("base_model.model.") and k.endswith(".lora_A.weight")})
+    for t in targets:
+        a = f32(lora[f"base_model.model.{t}.lora_A.weight"])
+        b = f32(lora[f"base_model.model.{t}.lora_B.weight"])
+        name = t + ".weight"
+        if not name.startswith(PREFIX):
+            name = PREFIX + (name[len("model."):] if name.startswith("model.") else name)
+        delta = (b @ a).astype(np.float32) * np.float32(scale)
+        out[name] = (f32(out[name]) + delta).astype(np.float32)
+    return out
+
+
+class QwenModel:
+    """Holds fp32 weights (already rounded to the model dtype when bf16) and runs the
+    C oracle forward (ho_qwen_forward)."""
+
+    def __init__(self, cfg: QwenConfig, weights: dict, bf16: bool):
+        self.cfg = cfg
+        self.bf16 = bf16
+        self.keep = []
+        rnd = round_bf16 if bf16 else f32
+        self.embed = rnd(weights[PREFIX + "embed_tokens.weight"])
+        self.final_norm = f32(rnd(weights[PREFIX + "norm.weight"])) + np.float32(1.0)
+        self.layer_types = i32(cfg.layer_types)
+        layers = (_Layer * cfg.num_hidden_layers)()
+        for i in range(cfg.num_hidden_layers):
+            for f in _LAYER_FIELDS:
+                key = f"{PREFIX}layers.{i}.{_NAME[f]}"
+                if key not in weights:
+                    continue
+                # dtype conversion at load (qwen3_5.rs:2479); norm offsets become 1 + w in fp32 (180-182)
+                a = rnd(weights[key])
+                if f in _EFFECTIVE:
+                    a = f32(a) + np.float32(1.0)
+                a = f32(a).reshape(a.shape[0], -1) if f == "conv_w" else f32(a)
+                self.keep.append(a)
+                setattr(layers[i], f, a.ctypes.data_as(C.c_void_p).value)
+        self.layers = layers
+        self.ccfg = _Cfg(cfg.hidden_size, cfg.num_hidden_layers, cfg.num_attention_heads,
+                         cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size, cfg.vocab_size,
+                         cfg.rms_norm_eps, cfg.rope_theta, cfg.rotary_dim, cfg.linear_conv_kernel_dim,
+                         cfg.linear_key_head_dim, cfg.linear_num_key_heads, cfg.linear_num_value_heads,
+                         cfg.linear_value_head_dim,
+                         self.layer_types.ctypes.data_as(C.POINTER(C.c_int32)))
+
+    def forward(self, ids) -> np.ndarray:
+        ids = i32(ids)
+        T = ids.size
+        out = np.empty((T, self.cfg.hidden_size), np.float32)
+        L = lib()
+        rc = L.ho_qwen_forward(C.byref(self.ccfg), self.layers, self.embed.ctypes.data_as(C.c_void_p),
+                               self.final_norm.ctypes.data_as(C.c_void_p), ids.ctypes.data_as(C.c_void_p),
+                               C.c_int(T), C.c_int(int(self.bf16)), out.ctypes.data_as(C.c_void_p))
+        if rc != 0:
+            raise ValueError("oracle forward rejected its inputs (token outside the vocabulary?)")
+        return out
+
+
+def load_tiny_kev(root: Path):
+    """The reference's tiny Kev fixture (qwen3_5.rs:2185-2348 load path) as fp32 arrays."""
+    from safetensors.numpy import load_file
+
+    cfg = QwenConfig.from_json(json.loads((root / "config.json").read_text()))
+    weights = load_file(str(root / "model.safetensors"))
+    lora = load_file(str(root / "adapter_model.safetensors"))
+    ac = json.loads((root / "adapter_config.json").read_text())
+    scale = ac["lora_alpha"] / ac["r"] if ac["r"] > 0 else 1.0
+    weights = merge_lora(weights, lora, scale)
+    head = json.loads((root / "head.json").read_text())
+    golden = json.loads((root / "golden.json").read_text())
+    return cfg, weights, head, golden
