@@ -1,0 +1,236 @@
+"""Kev-shaped hybrid prefill benchmark on one MI355X.
+
+Workload: the Kev/Qwen3.5 hybrid scoring forward (hidden 1024, 24 layers = 3 Gated DeltaNet :
+1 gated GQA attention, attention 16/8 heads x 128, GDN 16 heads x 128, SwiGLU 3584,
+vocab 151936, decision head over 8 choices) on a batch of 64 sequences x 512 seeded token
+ids, random-init weights N(0, 0.02) in the model dtype, KV pages of 16 tokens from a seeded
+permutation of the pool. One step = one full forward of the 32,768 tokens (every layer,
+every token) plus the decision logits; inputs are resident in HBM before timing starts.
+
+Prints one JSON line: whole-job prefill tokens/s, the live-measured roofline of the attention
+kernel (MFMA-bound, bf16 dense peak 2.5 PFLOP/s) and of the delta-rule kernel (HBM-bound,
+8 TB/s), and the CPU oracle's forward timed on this host's cores as a reported baseline.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+SEED = 20261201
+MFMA_PEAK_BF16 = 2.5e15   # dense bf16 / fp16 MFMA, FLOP/s
+HBM_PEAK = 8.0e12         # bytes/s
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--batch", type=int, default=64)
+    p.add_argument("--seq-len", type=int, default=512)
+    p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
+    p.add_argument("--kernel-iters", type=int, default=20)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-threads", type=int, default=0)
+    return p.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_launches(fn, iters, stream):
+    """Average duration (s) of `fn` launches measured with events on the launch stream."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / 1e3 / iters
+
+
+def kernel_rooflines(ctx, shape, n_seqs, seq_len, dtype, iters):
+    """Times the attention and delta-rule kernels alone on inputs of the forward's shapes and
+    layouts (fused-projection q/gate strides, paged pools, token-major GDN inputs)."""
+    import numpy as np
+    import torch
+
+    from huncho_amd import abi
+    from huncho_amd.ops import gated_delta_chunked, paged_prefill_attention, qk_norm_rope_kv_write
+
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    n = n_seqs * seq_len
+    hq, hkv, d, P = shape.n_heads, shape.n_kv_heads, shape.head_dim, shape.page_size
+    rows = 2 * hq * d + 2 * hkv * d
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    qkv = torch.randn((n, rows), generator=g, device=dev, dtype=torch.float32).to(dtype)
+    cu = torch.arange(0, n + 1, seq_len, dtype=torch.int32, device=dev)
+    lens = torch.full((n_seqs,), seq_len, dtype=torch.int32, device=dev)
+    pages_per = seq_len // P
+    perm = abi.synth_permutation(SEED, 5, n_seqs * pages_per)
+    bt = torch.from_numpy(perm.reshape(n_seqs, pages_per).copy()).to(dev)
+    kp = torch.zeros((n_seqs * pages_per, hkv, P, d), dtype=dtype, device=dev)
+    vp = torch.zeros_like(kp)
+    cs, sn = abi.rope_table(d, shape.rope_theta, seq_len, True)
+    w1 = torch.ones(d, device=dev)
+    q = qkv[:, : 2 * hq * d].view(n, hq, 2 * d)[:, :, :d]
+    gate = qkv[:, : 2 * hq * d].view(n, hq, 2 * d)[:, :, d:]
+    k_in = qkv[:, 2 * hq * d: 2 * hq * d + hkv * d].view(n, hkv, d)
+    v_in = qkv[:, 2 * hq * d + hkv * d:].view(n, hkv, d)
+    qk_norm_rope_kv_write(ctx, q, k_in, v_in, w1, w1, shape.eps, torch.from_numpy(cs).to(dev),
+                          torch.from_numpy(sn).to(dev), d, cu, lens, bt, kp, vp, q)
+    out = torch.empty((n, hq, d), dtype=dtype, device=dev)
+    t_attn = time_launches(lambda: paged_prefill_attention(ctx, q, kp, vp, bt, cu, lens, seq_len, gate=gate,
+                                                           out=out), iters, stream)
+    attn_flops = 4.0 * hq * d * seq_len * (seq_len + 1) / 2 * n_seqs
+    attn_bytes = n * (2 * hq + 2 * hkv) * d * 2
+
+    H = shape.lin_n_v_heads
+    qg = torch.nn.functional.normalize(torch.randn((n, shape.lin_n_k_heads, 128), generator=g, device=dev),
+                                       dim=-1)
+    kg = torch.nn.functional.normalize(torch.randn((n, shape.lin_n_k_heads, 128), generator=g, device=dev),
+                                       dim=-1).to(dtype)
+    qg = (qg * 128 ** -0.5).to(dtype)
+    vg = torch.randn((n, H, 128), generator=g, device=dev).to(dtype)
+    gg = -torch.nn.functional.softplus(torch.randn((n, H), generator=g, device=dev)) * 0.5
+    bb = torch.sigmoid(torch.randn((n, H), generator=g, device=dev))
+    og = torch.empty_like(vg)
+    t_gdn = time_launches(lambda: gated_delta_chunked(ctx, qg, kg, vg, gg, bb, cu, out=og), iters, stream)
+    gdn_bytes = n * H * (4 * 128 * 2 + 8)
+    chunks = math.ceil(seq_len / 64) * n_seqs * H
+    gdn_flops = chunks * 11.71e6
+    torch.cuda.synchronize()
+    return {
+        "attention": {"seconds": t_attn, "flops": attn_flops, "bytes": attn_bytes},
+        "delta_rule": {"seconds": t_gdn, "flops": gdn_flops, "bytes": gdn_bytes},
+    }
+
+
+def cpu_baseline(shape, weights, seq_len, threads):
+    """The CPU oracle's fp32 forward of one sequence of the same model on this host."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import numpy as np
+
+    from oracle import oracle as O
+
+    O.set_threads(threads)
+    cfg = O.QwenConfig(hidden_size=shape.hidden, num_hidden_layers=shape.n_layers,
+                       num_attention_heads=shape.n_heads, num_key_value_heads=shape.n_kv_heads,
+                       head_dim=shape.head_dim, intermediate_size=shape.intermediate, vocab_size=shape.vocab,
+                       rms_norm_eps=shape.eps, layer_types=shape.layer_types, linear_conv_kernel_dim=shape.conv_k,
+                       linear_key_head_dim=shape.lin_key_dim, linear_num_key_heads=shape.lin_n_k_heads,
+                       linear_num_value_heads=shape.lin_n_v_heads, linear_value_head_dim=shape.lin_v_dim,
+                       rope_theta=shape.rope_theta, partial_rotary_factor=shape.rotary_dim / shape.head_dim)
+    f = {k: O.bf16_to_f32(v).reshape(v.shape) for k, v in weights.items()}
+    model = O.QwenModel(cfg, f, bf16=False)
+    from huncho_amd import abi
+
+    ids = abi.synth_uniform_int(SEED, 900, seq_len, 0, shape.vocab - 1)
+    t0 = time.perf_counter()
+    h = model.forward(ids)
+    _ = h[-1] @ f["decision_head.weight"].T
+    dt = time.perf_counter() - t0
+    return {"value": round(seq_len / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"1 sequence x {seq_len} tokens of the same Kev-shaped model (all 24 layers + head), "
+                      f"fp32 CPU oracle forward, {threads} OpenMP threads, {dt:.2f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: every GPU host here has one, and this path shards by "
+              f"independent sequences with no collectives (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from huncho_amd import abi
+    from huncho_amd.kev import KevModel, KevShape, synthetic_weights
+    from huncho_amd.ops import context_for_torch
+
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    shape = KevShape()
+    t0 = time.perf_counter()
+    weights = synthetic_weights(shape, SEED)
+    log(f"synthetic weights in {time.perf_counter() - t0:.1f} s")
+    ctx = context_for_torch(0)
+    info = ctx.device_info()
+    model = KevModel(ctx, shape, weights, dtype)
+    lengths = [args.seq_len] * args.batch
+    batch = model.prepare(lengths, seed=SEED)
+    ids_np = abi.synth_uniform_int(SEED, 901, sum(lengths), 0, shape.vocab - 1)
+    ids = torch.from_numpy(ids_np).to("cuda")
+    n_tokens = sum(lengths)
+    log(f"model ready on {info.name.decode()} ({info.compute_units} CUs); warmup {args.warmup}")
+    for _ in range(args.warmup):
+        model.forward_ids(ids, batch)
+    torch.cuda.synchronize()
+    if ctx.take_faults():
+        raise RuntimeError("device faults during warmup")
+    log(f"timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        model.forward_ids(ids, batch)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    logits = batch["logits"].cpu().numpy()
+    probs = abi.calibrate(logits[0], 1.3)
+    log(f"{ms:.2f} ms/step; first row calibrated probabilities {np.round(probs, 4).tolist()}")
+
+    kr = kernel_rooflines(ctx, shape, args.batch, args.seq_len, dtype, args.kernel_iters)
+    a, gd = kr["attention"], kr["delta_rule"]
+    attn_achieved = a["flops"] / a["seconds"] / 1e12
+    gdn_achieved = gd["bytes"] / gd["seconds"] / 1e9
+    log(f"attention {a['seconds'] * 1e6:.1f} us/launch, delta rule {gd['seconds'] * 1e6:.1f} us/launch")
+    line = {
+        "metric": "prefill tokens/s (Kev-shaped 64x512 bf16); attn TFLOP/s as % of MFMA peak",
+        "value": round(n_tokens / (elapsed / args.steps), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic (seeded token ids, random-init N(0,0.02) weights)",
+        "config": {"workload": "kev_hybrid_scoring_prefill", "batch": args.batch, "seq_len": args.seq_len,
+                   "tokens_per_step": n_tokens, "layers": shape.n_layers, "hidden": shape.hidden,
+                   "layer_pattern": "3 gated-delta-rule : 1 gated GQA attention", "attn_heads": "16q/8kv x 128",
+                   "gdn_heads": "16 x 128", "mlp": "SwiGLU 3584", "vocab": shape.vocab, "page_size": shape.page_size,
+                   "decision_head": shape.n_out},
+        "roofline": {"kernel": "paged_prefill_attn", "bound": "mfma", "achieved": round(attn_achieved, 2),
+                     "peak": MFMA_PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                     "frac": round(attn_achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": None,
+                     "us_per_launch": round(a["seconds"] * 1e6, 2), "flops_per_launch": a["flops"],
+                     "hbm_frac": round(a["bytes"] / a["seconds"] / HBM_PEAK, 4)},
+        "roofline_delta_rule": {"kernel": "gdn_chunk", "bound": "hbm", "achieved": round(gdn_achieved, 1),
+                                "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                                "frac": round(gd["bytes"] / gd["seconds"] / HBM_PEAK, 4), "traffic": None,
+                                "us_per_launch": round(gd["seconds"] * 1e6, 2), "bytes_per_launch": gd["bytes"],
+                                "tflops": round(gd["flops"] / gd["seconds"] / 1e12, 2)},
+        "device": {"name": info.name.decode(), "cus": info.compute_units, "clock_mhz": info.clock_khz // 1000},
+    }
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        log(f"CPU baseline with {threads} threads")
+        line["cpu_baseline"] = cpu_baseline(shape, weights, args.seq_len, threads)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,215 @@
+"""ctypes binding of libhuncho_rocm (include/huncho_rocm.h).
+
+This is the Python counterpart of the `extern "C"` block a Rust `huncho-rocm-sys` crate
+would declare: the same symbols, plain pointers and sizes. `HkError` carries the status
+code and the context's last error string; the Rust side maps HK_ERR_UNSUPPORTED to
+`Error::Unsupported` and the rest to `Error::Backend`
+(crates/huncho-core/src/error.rs:11-38).
+
+The library is loaded from the package's _build/ directory. Importing this module fails
+with an ImportError if it has not been built: there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_build" / "libhuncho_rocm.so"
+
+HK_OK, HK_ERR_INVALID, HK_ERR_UNSUPPORTED, HK_ERR_DEVICE, HK_ERR_NOMEM = 0, 1, 2, 3, 4
+HK_F32, HK_BF16 = 0, 1
+HK_FAULT_SEQLENS, HK_FAULT_PAGE, HK_FAULT_ROPE, HK_FAULT_TOKEN = 1, 2, 4, 8
+
+vp = C.c_void_p
+i32p = C.POINTER(C.c_int32)
+f32p = C.POINTER(C.c_float)
+L, I, F, D, SZ, U64 = C.c_long, C.c_int, C.c_float, C.c_double, C.c_size_t, C.c_uint64
+
+
+class HkError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"huncho_rocm error {code}: {message}")
+        self.code = code
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("compute_units", I), ("clock_khz", I), ("mem_clock_khz", I),
+                ("mem_bus_width", I), ("total_mem", SZ), ("lds_per_block", SZ), ("l2_bytes", I)]
+
+
+class KevConfig(C.Structure):
+    _fields_ = [("hidden", I), ("n_layers", I), ("n_heads", I), ("n_kv_heads", I), ("head_dim", I),
+                ("intermediate", I), ("vocab", I), ("eps", F), ("rope_theta", D), ("rotary_dim", I),
+                ("conv_k", I), ("lin_key_dim", I), ("lin_n_k_heads", I), ("lin_n_v_heads", I), ("lin_v_dim", I),
+                ("page_size", I), ("max_context", I), ("n_out", I), ("layer_types_host", i32p)]
+
+
+LAYER_FIELDS = ["input_norm", "post_norm", "gate_proj", "up_proj", "down_proj", "in_qkv", "in_z", "in_b", "in_a",
+                "out_proj", "conv_w", "norm_w", "a_log", "dt_bias", "q_proj", "k_proj", "v_proj", "o_proj",
+                "q_norm", "k_norm"]
+
+
+class KevLayerWeights(C.Structure):
+    _fields_ = [(n, vp) for n in LAYER_FIELDS]
+
+
+# name -> (restype, argtypes); every function declared in include/huncho_rocm.h
+SIGNATURES = {
+    "hk_device_count": (I, [C.POINTER(I)]),
+    "hk_version": (C.c_char_p, []),
+    "hk_ctx_create": (I, [I, C.POINTER(vp)]),
+    "hk_ctx_destroy": (I, [vp]),
+    "hk_ctx_set_stream": (I, [vp, vp]),
+    "hk_ctx_stream": (vp, [vp]),
+    "hk_ctx_own_stream": (vp, [vp]),
+    "hk_ctx_synchronize": (I, [vp]),
+    "hk_ctx_last_error": (C.c_char_p, [vp]),
+    "hk_ctx_device_info": (I, [vp, C.POINTER(DeviceInfo)]),
+    "hk_ctx_take_faults": (I, [vp, C.POINTER(I)]),
+    "hk_rope_fill_table": (I, [I, D, I, I, vp, vp]),
+    "hk_qk_norm_rope_kv_write": (I, [vp, I, vp, L, L, vp, L, vp, L, vp, vp, F, vp, vp, I, I, vp, vp, I, I, vp, I,
+                                     I, I, I, I, I, vp, L, L, vp, vp]),
+    "hk_paged_kv_write": (I, [vp, I, vp, vp, vp, vp, I, I, vp, I, I, I, I, I, vp, vp]),
+    "hk_paged_prefill_attention": (I, [vp, I, vp, L, L, vp, vp, I, I, vp, I, vp, vp, I, I, I, I, I, I, F, vp, L,
+                                       L, vp, L, L]),
+    "hk_gated_delta_chunked": (I, [vp, I, vp, L, vp, L, vp, L, vp, vp, vp, I, I, I, I, I, I, vp, vp, vp, L]),
+    "hk_gdn_prep": (I, [vp, I, vp, L, vp, I, vp, vp, L, I, I, vp, vp, vp, I, I, I, I, vp, vp, vp, vp, vp, vp]),
+    "hk_rms_norm": (I, [vp, I, vp, L, vp, F, I, I, vp, L]),
+    "hk_gated_rms_norm": (I, [vp, I, vp, vp, L, I, vp, F, I, I, vp]),
+    "hk_swiglu": (I, [vp, I, vp, L, L, I, I, vp]),
+    "hk_kev_model_create": (I, [vp, I, C.POINTER(KevConfig), C.POINTER(KevLayerWeights), vp, vp, vp, vp,
+                                C.POINTER(vp)]),
+    "hk_kev_model_destroy": (I, [vp]),
+    "hk_kev_workspace_size": (I, [vp, I, I, C.POINTER(SZ)]),
+    "hk_kev_forward": (I, [vp, vp, vp, i32p, I, vp, I, I, vp, SZ, vp, vp]),
+    "hk_calibrate": (I, [f32p, I, F, f32p]),
+    "hk_synth_normal": (I, [U64, U64, vp, SZ, F, F]),
+    "hk_synth_normal_bf16": (I, [U64, U64, vp, SZ, F, F]),
+    "hk_synth_uniform_int": (I, [U64, U64, vp, SZ, C.c_int32, C.c_int32]),
+    "hk_synth_permutation": (I, [U64, U64, vp, C.c_int32]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(f"libhuncho_rocm is not built ({LIB_PATH}); run `python -m huncho_amd.build`")
+        L_ = C.CDLL(str(LIB_PATH), mode=C.RTLD_GLOBAL)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L_, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L_
+    return _lib
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    lib().hk_device_count(C.byref(n))
+    return n.value
+
+
+class Context:
+    """A device context (hk_ctx). One thread at a time, like the engine's backend mutex."""
+
+    def __init__(self, device: int = 0, stream=None):
+        h = vp()
+        rc = lib().hk_ctx_create(device, C.byref(h))
+        if rc != HK_OK:
+            raise HkError(rc, "no gfx950 GPU available" if rc == HK_ERR_UNSUPPORTED else "context creation failed")
+        self.h = h
+        if stream is not None:
+            self.set_stream(stream)
+
+    def set_stream(self, stream) -> None:
+        """stream: a raw hipStream_t value (int; 0 is the null stream), e.g.
+        torch.cuda.current_stream().cuda_stream."""
+        self.check(lib().hk_ctx_set_stream(self.h, vp(stream) if stream else None))
+
+    def check(self, rc: int) -> None:
+        if rc != HK_OK:
+            raise HkError(rc, lib().hk_ctx_last_error(self.h).decode())
+
+    def synchronize(self) -> None:
+        self.check(lib().hk_ctx_synchronize(self.h))
+
+    def take_faults(self) -> int:
+        f = C.c_int(0)
+        self.check(lib().hk_ctx_take_faults(self.h, C.byref(f)))
+        return f.value
+
+    def device_info(self) -> DeviceInfo:
+        info = DeviceInfo()
+        self.check(lib().hk_ctx_device_info(self.h, C.byref(info)))
+        return info
+
+    def close(self) -> None:
+        if self.h:
+            lib().hk_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def rope_table(rotary_dim: int, theta: float, max_pos: int, round_bf16: bool):
+    """Host cos/sin tables [max_pos][rd/2] (float32 numpy arrays)."""
+    import numpy as np
+
+    cs = np.empty((max_pos, rotary_dim // 2), np.float32)
+    sn = np.empty_like(cs)
+    rc = lib().hk_rope_fill_table(rotary_dim, theta, max_pos, int(round_bf16), cs.ctypes.data, sn.ctypes.data)
+    if rc != HK_OK:
+        raise HkError(rc, "bad rope table arguments")
+    return cs, sn
+
+
+def calibrate(logits, temperature: float):
+    import numpy as np
+
+    x = np.ascontiguousarray(logits, np.float32)
+    p = np.empty_like(x)
+    rc = lib().hk_calibrate(x.ctypes.data_as(f32p), x.size, float(temperature), p.ctypes.data_as(f32p))
+    if rc != HK_OK:
+        raise HkError(rc, "calibration rejected non-finite logits or temperature")
+    return p
+
+
+def synth_normal(seed: int, stream: int, n: int, mean=0.0, std=1.0):
+    import numpy as np
+
+    out = np.empty(n, np.float32)
+    lib().hk_synth_normal(seed, stream, out.ctypes.data, n, mean, std)
+    return out
+
+
+def synth_normal_bf16(seed: int, stream: int, n: int, mean=0.0, std=1.0):
+    """bf16 bit patterns (uint16) of the same normal stream."""
+    import numpy as np
+
+    out = np.empty(n, np.uint16)
+    lib().hk_synth_normal_bf16(seed, stream, out.ctypes.data, n, mean, std)
+    return out
+
+
+def synth_uniform_int(seed: int, stream: int, n: int, lo: int, hi: int):
+    import numpy as np
+
+    out = np.empty(n, np.int32)
+    lib().hk_synth_uniform_int(seed, stream, out.ctypes.data, n, lo, hi)
+    return out
+
+
+def synth_permutation(seed: int, stream: int, n: int):
+    import numpy as np
+
+    out = np.empty(n, np.int32)
+    lib().hk_synth_permutation(seed, stream, out.ctypes.data, n)
+    return out

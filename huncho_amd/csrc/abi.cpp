@@ -1,0 +1,439 @@
+// abi.cpp - host side of the libhuncho_rocm C ABI: context, error model, argument
+// validation and launch of the gfx950 kernels. See include/huncho_rocm.h.
+#include "abi_internal.hpp"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+// ---------------------------------------------------------------------------
+// context and errors
+// ---------------------------------------------------------------------------
+
+int hk_fail(hk_ctx* ctx, int code, const char* fmt, ...) {
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        ctx->last_error = buf;
+    }
+    return code;
+}
+
+int hk_check_hip(hk_ctx* ctx, hipError_t e, const char* what) {
+    if (e == hipSuccess) return HK_OK;
+    return hk_fail(ctx, HK_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+extern "C" int hk_device_count(int* out) {
+    if (!out) return HK_ERR_INVALID;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *out = n;
+    return HK_OK;
+}
+
+extern "C" const char* hk_version(void) { return "huncho_rocm 0.1 (gfx950)"; }
+
+extern "C" int hk_ctx_create(int device_ordinal, hk_ctx** out) {
+    if (!out) return HK_ERR_INVALID;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return HK_ERR_UNSUPPORTED;
+    if (device_ordinal < 0 || device_ordinal >= n) return HK_ERR_INVALID;
+    if (hipSetDevice(device_ordinal) != hipSuccess) return HK_ERR_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device_ordinal) != hipSuccess) return HK_ERR_DEVICE;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return HK_ERR_UNSUPPORTED;
+    hk_ctx* ctx = new hk_ctx();
+    ctx->device = device_ordinal;
+    ctx->prop = prop;
+    if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return HK_ERR_DEVICE;
+    }
+    ctx->stream = ctx->own_stream;
+    if (hipMalloc(&ctx->fault_dev, 256) != hipSuccess) {
+        hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return HK_ERR_NOMEM;
+    }
+    if (hipMemset(ctx->fault_dev, 0, 256) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hipFree(ctx->fault_dev);
+        hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return HK_ERR_DEVICE;
+    }
+    *out = ctx;
+    return HK_OK;
+}
+
+extern "C" int hk_ctx_destroy(hk_ctx* ctx) {
+    if (!ctx) return HK_ERR_INVALID;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    hk_blas_release(ctx);
+    if (ctx->fault_dev) hipFree(ctx->fault_dev);
+    if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return HK_OK;
+}
+
+extern "C" int hk_ctx_set_stream(hk_ctx* ctx, void* hip_stream) {
+    if (!ctx) return HK_ERR_INVALID;
+    ctx->stream = (hipStream_t)hip_stream;  // NULL is HIP's null stream
+    return HK_OK;
+}
+
+extern "C" void* hk_ctx_own_stream(hk_ctx* ctx) { return ctx ? (void*)ctx->own_stream : nullptr; }
+
+extern "C" void* hk_ctx_stream(hk_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+extern "C" int hk_ctx_synchronize(hk_ctx* ctx) {
+    if (!ctx) return HK_ERR_INVALID;
+    hipSetDevice(ctx->device);
+    return hk_check_hip(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+extern "C" const char* hk_ctx_last_error(hk_ctx* ctx) { return ctx ? ctx->last_error.c_str() : "no context"; }
+
+extern "C" int hk_ctx_device_info(hk_ctx* ctx, hk_device_info_t* out) {
+    if (!ctx || !out) return HK_ERR_INVALID;
+    memset(out, 0, sizeof(*out));
+    snprintf(out->name, sizeof(out->name), "%s", ctx->prop.gcnArchName);
+    out->compute_units = ctx->prop.multiProcessorCount;
+    out->clock_khz = ctx->prop.clockRate;
+    out->mem_clock_khz = ctx->prop.memoryClockRate;
+    out->mem_bus_width = ctx->prop.memoryBusWidth;
+    out->total_mem = ctx->prop.totalGlobalMem;
+    out->lds_per_block = ctx->prop.sharedMemPerBlock;
+    out->l2_bytes = ctx->prop.l2CacheSize;
+    return HK_OK;
+}
+
+extern "C" int hk_ctx_take_faults(hk_ctx* ctx, int* faults_out) {
+    if (!ctx || !faults_out) return HK_ERR_INVALID;
+    hipSetDevice(ctx->device);
+    int f = 0;
+    int rc = hk_check_hip(ctx, hipMemcpyAsync(&f, ctx->fault_dev, sizeof(int), hipMemcpyDeviceToHost, ctx->stream),
+                          "fault flag read");
+    if (rc) return rc;
+    rc = hk_check_hip(ctx, hipStreamSynchronize(ctx->stream), "fault flag sync");
+    if (rc) return rc;
+    *faults_out = f;
+    if (f) {
+        int zero = 0;
+        rc = hk_check_hip(ctx, hipMemcpyAsync(ctx->fault_dev, &zero, sizeof(int), hipMemcpyHostToDevice, ctx->stream),
+                          "fault flag clear");
+        if (rc) return rc;
+        rc = hk_check_hip(ctx, hipStreamSynchronize(ctx->stream), "fault flag clear sync");
+    }
+    return rc;
+}
+
+// ---------------------------------------------------------------------------
+// host helpers: rope table, calibration, synthetic inputs
+// ---------------------------------------------------------------------------
+
+static inline uint16_t f32_to_bf16_bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+static inline float bf16_bits_to_f32(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+extern "C" int hk_rope_fill_table(int rd, double theta, int max_pos, int round_bf16, float* cos_host, float* sin_host) {
+    if (rd < 2 || (rd & 1) || max_pos < 0 || !cos_host || !sin_host || !(theta > 0)) return HK_ERR_INVALID;
+    const int half = rd / 2;
+    for (int p = 0; p < max_pos; ++p)
+        for (int i = 0; i < half; ++i) {
+            // qwen3_5.rs:229-244: inv_freq in f32, pos * inv_freq in f32, cos/sin in f32
+            float inv = powf((float)theta, -(2.0f * (float)i) / (float)rd);
+            float f = (float)p * inv;
+            float c = cosf(f), s = sinf(f);
+            if (round_bf16) {
+                c = bf16_bits_to_f32(f32_to_bf16_bits(c));
+                s = bf16_bits_to_f32(f32_to_bf16_bits(s));
+            }
+            cos_host[(size_t)p * half + i] = c;
+            sin_host[(size_t)p * half + i] = s;
+        }
+    return HK_OK;
+}
+
+extern "C" int hk_calibrate(const float* logits, int n, float temperature, float* probs) {
+    if (n < 0 || (n > 0 && (!logits || !probs))) return HK_ERR_INVALID;
+    if (!(temperature > 0.0f) || !isfinite(temperature)) return HK_ERR_INVALID;
+    for (int i = 0; i < n; ++i)
+        if (!isfinite(logits[i])) return HK_ERR_INVALID;
+    if (n == 0) return HK_OK;
+    const float inv_t = 1.0f / temperature;
+    float m = -INFINITY;
+    for (int i = 0; i < n; ++i) m = logits[i] > m ? logits[i] : m;
+    double sum = 0.0;
+    for (int i = 0; i < n; ++i) {
+        float e = expf((logits[i] - m) * inv_t);
+        probs[i] = e;
+        sum += (double)e;
+    }
+    for (int i = 0; i < n; ++i) {
+        probs[i] = (float)((double)probs[i] / sum);
+        if (!isfinite(probs[i])) return HK_ERR_INVALID;
+    }
+    return HK_OK;
+}
+
+static inline uint64_t splitmix64(uint64_t* s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+static inline uint64_t stream_state(uint64_t seed, uint64_t stream) { return seed ^ (stream * 0xD1B54A32D192ED03ull); }
+
+template <typename F>
+static void normal_stream(uint64_t seed, uint64_t stream, size_t n, float mean, float std, F&& put) {
+    uint64_t s = stream_state(seed, stream);
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i += 2) {
+        uint64_t z = splitmix64(&s);
+        double u1 = ((double)(z >> 40) + 0.5) * (1.0 / 16777216.0);
+        double u2 = (double)((z >> 16) & 0xFFFFFFull) * (1.0 / 16777216.0);
+        double r = sqrt(-2.0 * log(u1));
+        put(i, (float)(mean + std * (r * cos(two_pi * u2))));
+        if (i + 1 < n) put(i + 1, (float)(mean + std * (r * sin(two_pi * u2))));
+    }
+}
+
+extern "C" int hk_synth_normal(uint64_t seed, uint64_t stream, float* out, size_t n, float mean, float std) {
+    if (!out && n) return HK_ERR_INVALID;
+    normal_stream(seed, stream, n, mean, std, [&](size_t i, float v) { out[i] = v; });
+    return HK_OK;
+}
+
+extern "C" int hk_synth_normal_bf16(uint64_t seed, uint64_t stream, uint16_t* out, size_t n, float mean, float std) {
+    if (!out && n) return HK_ERR_INVALID;
+    normal_stream(seed, stream, n, mean, std, [&](size_t i, float v) { out[i] = f32_to_bf16_bits(v); });
+    return HK_OK;
+}
+
+static uint64_t uniform_below(uint64_t* s, uint64_t range) {
+    uint64_t limit = UINT64_MAX - (UINT64_MAX % range);
+    uint64_t z;
+    do {
+        z = splitmix64(s);
+    } while (z >= limit);
+    return z % range;
+}
+
+extern "C" int hk_synth_uniform_int(uint64_t seed, uint64_t stream, int32_t* out, size_t n, int32_t lo, int32_t hi) {
+    if ((!out && n) || hi < lo) return HK_ERR_INVALID;
+    uint64_t s = stream_state(seed, stream);
+    uint64_t range = (uint64_t)((int64_t)hi - (int64_t)lo + 1);
+    for (size_t i = 0; i < n; ++i) out[i] = (int32_t)((int64_t)lo + (int64_t)uniform_below(&s, range));
+    return HK_OK;
+}
+
+extern "C" int hk_synth_permutation(uint64_t seed, uint64_t stream, int32_t* out, int32_t n) {
+    if (n < 0 || (!out && n)) return HK_ERR_INVALID;
+    uint64_t s = stream_state(seed, stream);
+    for (int32_t i = 0; i < n; ++i) out[i] = i;
+    for (int32_t i = n - 1; i > 0; --i) {
+        int32_t j = (int32_t)uniform_below(&s, (uint64_t)i + 1);
+        int32_t t = out[i];
+        out[i] = out[j];
+        out[j] = t;
+    }
+    return HK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// validated ops
+// ---------------------------------------------------------------------------
+
+static int log2_exact(int v) {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int s = 0;
+    while ((1 << s) < v) ++s;
+    return s;
+}
+
+#define REQUIRE(cond, ...)                                              \
+    do {                                                                \
+        if (!(cond)) return hk_fail(ctx, HK_ERR_INVALID, __VA_ARGS__); \
+    } while (0)
+
+static int check_dtype(hk_ctx* ctx, int dtype) {
+    if (dtype != HK_F32 && dtype != HK_BF16) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d is not supported", dtype);
+    return HK_OK;
+}
+
+int hk_qk_norm_rope_kv_write_impl(hk_ctx* ctx, int dtype, const void* q_in, long q_in_tok, long q_in_head,
+                                  const void* k_in, long k_in_tok, const void* v_in, long v_in_tok, const float* q_norm,
+                                  const float* k_norm, float eps, const float* rope_cos, const float* rope_sin, int rd,
+                                  int rope_max_pos, const int32_t* cu, const int32_t* ctxl, int n_seqs, int n_tokens,
+                                  const int32_t* bt, int bt_stride, int num_pages, int page_size, int q_heads,
+                                  int kv_heads, int head_dim, void* q_out, long q_out_tok, long q_out_head,
+                                  void* k_pool, void* v_pool) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = check_dtype(ctx, dtype)) return rc;
+    if (head_dim != 128) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "head_dim %d: only 128 is implemented", head_dim);
+    const int shift = log2_exact(page_size);
+    REQUIRE(shift >= 4 && shift <= 8, "page_size %d must be a power of two in 16..256", page_size);
+    REQUIRE(n_seqs > 0 && n_tokens >= 0 && q_heads >= 0 && kv_heads > 0, "bad batch/head counts");
+    REQUIRE(bt_stride > 0 && num_pages > 0, "bad block table geometry");
+    REQUIRE(cu && ctxl && bt && k_in && v_in && k_pool && v_pool, "null pointer argument");
+    REQUIRE(q_heads == 0 || (q_in && q_out), "null q pointer");
+    REQUIRE(!rope_cos || (rope_sin && rd >= 2 && rd % 2 == 0 && rd <= head_dim && rope_max_pos > 0),
+            "bad rope table arguments");
+    REQUIRE(k_in_tok >= (long)kv_heads * head_dim && v_in_tok >= (long)kv_heads * head_dim, "k/v token stride too small");
+    hipSetDevice(ctx->device);
+    hk::KvArgs a{q_in, q_in_tok, q_in_head, k_in, k_in_tok, v_in, v_in_tok, q_norm, k_norm, eps, rope_cos, rope_sin,
+                 rd, rope_max_pos, cu, ctxl, n_seqs, n_tokens, bt, bt_stride, num_pages, shift, q_heads, kv_heads,
+                 q_out, q_out_tok, q_out_head, k_pool, v_pool, ctx->fault_dev};
+    int rc = hk_launch_qk_norm_rope_kv_write(dtype == HK_BF16, &a, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "qk_norm_rope_kv_write launch failed") : HK_OK;
+}
+
+extern "C" int hk_qk_norm_rope_kv_write(hk_ctx* ctx, int dtype, const void* q_in, long q_in_tok, long q_in_head,
+                                        const void* k_in, long k_in_tok, const void* v_in, long v_in_tok,
+                                        const float* q_norm, const float* k_norm, float eps, const float* rope_cos,
+                                        const float* rope_sin, int rd, int rope_max_pos, const int32_t* cu,
+                                        const int32_t* ctxl, int n_seqs, int n_tokens, const int32_t* bt,
+                                        int bt_stride, int num_pages, int page_size, int q_heads, int kv_heads,
+                                        int head_dim, void* q_out, long q_out_tok, long q_out_head, void* k_pool,
+                                        void* v_pool) {
+    return hk_qk_norm_rope_kv_write_impl(ctx, dtype, q_in, q_in_tok, q_in_head, k_in, k_in_tok, v_in, v_in_tok, q_norm,
+                                         k_norm, eps, rope_cos, rope_sin, rd, rope_max_pos, cu, ctxl, n_seqs, n_tokens,
+                                         bt, bt_stride, num_pages, page_size, q_heads, kv_heads, head_dim, q_out,
+                                         q_out_tok, q_out_head, k_pool, v_pool);
+}
+
+extern "C" int hk_paged_kv_write(hk_ctx* ctx, int dtype, const void* k, const void* v, const int32_t* cu,
+                                 const int32_t* ctxl, int n_seqs, int n_tokens, const int32_t* bt, int bt_stride,
+                                 int num_pages, int page_size, int kv_heads, int head_dim, void* k_pool, void* v_pool) {
+    return hk_qk_norm_rope_kv_write_impl(ctx, dtype, nullptr, 0, 0, k, (long)kv_heads * head_dim, v,
+                                         (long)kv_heads * head_dim, nullptr, nullptr, 0.f, nullptr, nullptr, 0, 0, cu,
+                                         ctxl, n_seqs, n_tokens, bt, bt_stride, num_pages, page_size, 0, kv_heads,
+                                         head_dim, nullptr, 0, 0, k_pool, v_pool);
+}
+
+extern "C" int hk_paged_prefill_attention(hk_ctx* ctx, int dtype, const void* q, long q_tok, long q_head,
+                                          const void* k_pool, const void* v_pool, int num_pages, int page_size,
+                                          const int32_t* bt, int bt_stride, const int32_t* cu, const int32_t* ctxl,
+                                          int n_seqs, int n_tokens, int max_q_len, int q_heads, int kv_heads,
+                                          int head_dim, float scale, const void* gate, long gate_tok, long gate_head,
+                                          void* o, long o_tok, long o_head) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = check_dtype(ctx, dtype)) return rc;
+    if (head_dim != 128) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "head_dim %d: only 128 is implemented", head_dim);
+    REQUIRE(kv_heads > 0 && q_heads > 0 && q_heads % kv_heads == 0, "q_heads %d not a multiple of kv_heads %d", q_heads,
+            kv_heads);
+    const int group = q_heads / kv_heads;
+    if (group != 1 && group != 2 && group != 4 && group != 8)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "GQA group %d: 1, 2, 4 or 8 are implemented", group);
+    const int shift = log2_exact(page_size);
+    REQUIRE(shift >= 4 && shift <= 8, "page_size %d must be a power of two in 16..256", page_size);
+    REQUIRE(n_seqs > 0 && n_tokens >= 0 && max_q_len >= 0 && bt_stride > 0 && num_pages > 0, "bad batch geometry");
+    REQUIRE(q && k_pool && v_pool && bt && cu && ctxl && o, "null pointer argument");
+    REQUIRE(q_head >= head_dim && q_tok >= (long)q_heads * q_head - (q_head - head_dim), "q strides overlap heads");
+    REQUIRE(o_head >= head_dim && o_tok >= (long)q_heads * o_head - (o_head - head_dim), "o strides overlap heads");
+    REQUIRE(!gate || gate_head >= head_dim, "gate stride too small");
+    REQUIRE(scale > 0 && isfinite(scale), "scale must be positive and finite");
+    if (max_q_len == 0 || n_tokens == 0) return HK_OK;
+    const int pos_per_block = 128 / group;
+    const int n_qblocks = (max_q_len + pos_per_block - 1) / pos_per_block;
+    REQUIRE(n_qblocks <= 65535, "max_q_len too large");
+    hipSetDevice(ctx->device);
+    hk::AttnArgs a{q, q_tok, q_head, k_pool, v_pool, shift, bt, bt_stride, cu, ctxl, q_heads, kv_heads, group,
+                   pos_per_block, scale * 1.4426950408889634f, gate, gate_tok, gate_head, o, o_tok, o_head,
+                   num_pages, n_tokens, ctx->fault_dev};
+    int rc = hk_launch_paged_prefill_attention(dtype == HK_BF16, &a, n_seqs, n_qblocks, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "attention launch failed") : HK_OK;
+}
+
+extern "C" int hk_gated_delta_chunked(hk_ctx* ctx, int dtype, const void* q, long q_tok, const void* k, long k_tok,
+                                      const void* v, long v_tok, const float* g, const float* beta, const int32_t* cu,
+                                      int n_seqs, int n_tokens, int heads, int k_heads, int dk, int dv,
+                                      const float* initial_state, float* final_state, void* o, long o_tok) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = check_dtype(ctx, dtype)) return rc;
+    if (dk != 128 || dv != 128) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dk=%d dv=%d: only 128x128 is implemented", dk, dv);
+    REQUIRE(heads > 0 && k_heads > 0 && heads % k_heads == 0, "heads %d not a multiple of k_heads %d", heads, k_heads);
+    REQUIRE(n_seqs > 0 && n_seqs <= 65535 && n_tokens >= 0, "bad batch geometry");
+    REQUIRE(q && k && v && g && beta && cu && o, "null pointer argument");
+    REQUIRE(q_tok >= (long)k_heads * dk && k_tok >= (long)k_heads * dk && v_tok >= (long)heads * dv &&
+                o_tok >= (long)heads * dv,
+            "token strides too small");
+    hipSetDevice(ctx->device);
+    hk::GdnArgs a{q, k, v, q_tok, k_tok, v_tok, heads / k_heads, g, beta, (long)heads, cu, initial_state,
+                  final_state, o, o_tok, heads, n_tokens, ctx->fault_dev};
+    int rc = hk_launch_gated_delta_chunked(dtype == HK_BF16, &a, n_seqs, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "gated delta launch failed") : HK_OK;
+}
+
+extern "C" int hk_gdn_prep(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
+                           const void* conv_hist, const void* ba, long ba_tok, int b_col, int a_col, const float* base_g,
+                           const float* dt_bias, const int32_t* cu, int n_seqs, int n_tokens, int heads, int k_heads,
+                           void* q_out, void* k_out, void* v_out, float* g_out, float* beta_out, void* conv_tail_out) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = check_dtype(ctx, dtype)) return rc;
+    REQUIRE(heads > 0 && k_heads > 0 && heads % k_heads == 0, "heads %d not a multiple of k_heads %d", heads, k_heads);
+    REQUIRE(conv_k >= 1 && conv_k <= 16, "conv kernel %d outside 1..16", conv_k);
+    REQUIRE(n_seqs > 0 && n_tokens >= 0, "bad batch geometry");
+    REQUIRE(mixed && conv_w && ba && base_g && dt_bias && cu && q_out && k_out && v_out && g_out && beta_out,
+            "null pointer argument");
+    const long conv_dim = (2L * k_heads + heads) * 128;
+    REQUIRE(mixed_tok >= conv_dim, "mixed token stride %ld < conv_dim %ld", mixed_tok, conv_dim);
+    REQUIRE(b_col >= 0 && a_col >= 0 && b_col + heads <= ba_tok && a_col + heads <= ba_tok, "b/a columns outside a row");
+    hipSetDevice(ctx->device);
+    hk::PrepArgs a{mixed, mixed_tok, conv_w, conv_k, conv_hist, ba, ba_tok, b_col, a_col, base_g, dt_bias, cu, n_seqs,
+                   n_tokens, k_heads, heads, 1.0f / sqrtf(128.0f), q_out, k_out, v_out, g_out, beta_out,
+                   ctx->fault_dev};
+    int rc = hk_launch_gdn_prep(dtype == HK_BF16, &a, conv_tail_out, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "gdn_prep launch failed") : HK_OK;
+}
+
+extern "C" int hk_rms_norm(hk_ctx* ctx, int dtype, const void* x, long x_tok, const float* w, float eps, int rows,
+                           int width, void* y, long y_tok) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = check_dtype(ctx, dtype)) return rc;
+    REQUIRE(x && w && y && rows >= 0 && width > 0 && x_tok >= width && y_tok >= width, "bad rms_norm arguments");
+    hipSetDevice(ctx->device);
+    hk::NormArgs a{x, x_tok, w, eps, rows, width, y, y_tok};
+    int rc = hk_launch_rms_norm(dtype == HK_BF16, &a, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "rms_norm launch failed") : HK_OK;
+}
+
+extern "C" int hk_gated_rms_norm(hk_ctx* ctx, int dtype, const void* x, const void* z, long z_tok, int heads,
+                                 const float* w, float eps, int rows, int width, void* y) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = check_dtype(ctx, dtype)) return rc;
+    REQUIRE(x && z && w && y && rows >= 0 && width > 0 && heads > 0 && rows % heads == 0 && z_tok >= (long)heads * width,
+            "bad gated_rms_norm arguments");
+    hipSetDevice(ctx->device);
+    hk::GatedNormArgs a{x, z, z_tok, heads, w, eps, rows, width, y};
+    int rc = hk_launch_gated_rms_norm(dtype == HK_BF16, &a, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "gated_rms_norm launch failed") : HK_OK;
+}
+
+extern "C" int hk_swiglu(hk_ctx* ctx, int dtype, const void* gu, long gu_tok, long up_off, int rows, int width, void* y) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = check_dtype(ctx, dtype)) return rc;
+    REQUIRE(gu && y && rows >= 0 && width > 0 && up_off >= width && gu_tok >= up_off + width, "bad swiglu arguments");
+    hipSetDevice(ctx->device);
+    hk::SwigluArgs a{gu, gu_tok, up_off, rows, width, y};
+    int rc = hk_launch_swiglu(dtype == HK_BF16, &a, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "swiglu launch failed") : HK_OK;
+}

@@ -1,0 +1,30 @@
+// abi_internal.hpp - context object and helpers shared by the host-side ABI files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/huncho_rocm.h"
+#include "kernel_args.hpp"
+
+struct hk_blas;  // GEMM state (hipBLASLt), created lazily per context
+
+struct hk_ctx {
+    int device = 0;
+    hipDeviceProp_t prop{};
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    int* fault_dev = nullptr;
+    std::string last_error;
+    hk_blas* blas = nullptr;
+};
+
+int hk_fail(hk_ctx* ctx, int code, const char* fmt, ...);
+int hk_check_hip(hk_ctx* ctx, hipError_t e, const char* what);
+void hk_blas_release(hk_ctx* ctx);
+
+// Row-major Y[n][out] = alpha * X[n][in] . W[out][in]^T + beta * C (C may alias Y or be null).
+// dtype HK_BF16: bf16 in/out, fp32 accumulation; HK_F32: fp32.
+int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, long ldx, const void* w, long ldw,
+                void* y, long ldy, const void* c, long ldc, float alpha, float beta);

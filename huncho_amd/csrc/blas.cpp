@@ -1,0 +1,123 @@
+// blas.cpp - dense projections (candle Linear, qwen3_5.rs:306-515) on hipBLASLt.
+//
+// Row-major Y[n][out] = alpha * X[n][in] . W[out][in]^T + beta * C is the column-major
+// product Y^T = W . X^T: m = out, n = n, k = in, op(A) = T on the weight, op(B) = N on the
+// activations. bf16 operands with fp32 accumulation (HIPBLAS_COMPUTE_32F), or fp32.
+// Plans (descriptors + heuristic algorithm) are cached per shape; the workspace is owned
+// by the context and allocated on the first GEMM.
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <tuple>
+
+#include "abi_internal.hpp"
+
+namespace {
+
+struct Plan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr, d = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    size_t ws = 0;
+};
+
+typedef std::tuple<int, int, int, int, long, long, long, long, int> Key;
+
+}  // namespace
+
+struct hk_blas {
+    hipblasLtHandle_t handle = nullptr;
+    void* workspace = nullptr;
+    size_t ws_bytes = 0;
+    std::map<Key, Plan> plans;
+};
+
+static const size_t kWorkspace = 128ull << 20;
+
+void hk_blas_release(hk_ctx* ctx) {
+    if (!ctx || !ctx->blas) return;
+    hk_blas* b = ctx->blas;
+    for (auto& kv : b->plans) {
+        Plan& p = kv.second;
+        if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
+        if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
+        if (p.c) hipblasLtMatrixLayoutDestroy(p.c);
+        if (p.d) hipblasLtMatrixLayoutDestroy(p.d);
+        if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+    }
+    if (b->workspace) hipFree(b->workspace);
+    if (b->handle) hipblasLtDestroy(b->handle);
+    delete b;
+    ctx->blas = nullptr;
+}
+
+static int blas_init(hk_ctx* ctx) {
+    if (ctx->blas) return HK_OK;
+    hk_blas* b = new hk_blas();
+    if (hipblasLtCreate(&b->handle) != HIPBLAS_STATUS_SUCCESS) {
+        delete b;
+        return hk_fail(ctx, HK_ERR_DEVICE, "hipblasLtCreate failed");
+    }
+    if (hipMalloc(&b->workspace, kWorkspace) != hipSuccess) {
+        hipblasLtDestroy(b->handle);
+        delete b;
+        return hk_fail(ctx, HK_ERR_NOMEM, "GEMM workspace allocation failed");
+    }
+    b->ws_bytes = kWorkspace;
+    ctx->blas = b;
+    return HK_OK;
+}
+
+int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, long ldx, const void* w, long ldw,
+                void* y, long ldy, const void* c, long ldc, float alpha, float beta) {
+    if (n == 0 || out == 0) return HK_OK;
+    if (int rc = blas_init(ctx)) return rc;
+    hk_blas* B = ctx->blas;
+    const bool has_c = c != nullptr && beta != 0.0f;
+    if (!has_c) {
+        c = y;
+        ldc = ldy;
+    }
+    Key key{dtype, out, n, in, ldw, ldx, ldy, ldc, has_c ? 1 : 0};
+    auto it = B->plans.find(key);
+    if (it == B->plans.end()) {
+        Plan p;
+        const hipDataType t = dtype == HK_BF16 ? HIP_R_16BF : HIP_R_32F;
+        bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+        hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
+        ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)) ==
+                       HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)) ==
+                       HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&p.a, t, in, out, ldw) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&p.b, t, in, n, ldx) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&p.c, t, out, n, ldc) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&p.d, t, out, n, ldy) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulPreference_t pref = nullptr;
+        ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+        uint64_t wsmax = B->ws_bytes;
+        ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax,
+                                                         sizeof(wsmax)) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulHeuristicResult_t res[4];
+        int returned = 0;
+        ok = ok && hipblasLtMatmulAlgoGetHeuristic(B->handle, p.desc, p.a, p.b, p.c, p.d, pref, 4, res, &returned) ==
+                       HIPBLAS_STATUS_SUCCESS;
+        if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+        if (!ok || returned == 0) {
+            if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
+            if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
+            if (p.c) hipblasLtMatrixLayoutDestroy(p.c);
+            if (p.d) hipblasLtMatrixLayoutDestroy(p.d);
+            if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+            return hk_fail(ctx, HK_ERR_UNSUPPORTED, "no hipBLASLt algorithm for %dx%dx%d", out, n, in);
+        }
+        p.algo = res[0].algo;
+        p.ws = res[0].workspaceSize;
+        it = B->plans.emplace(key, p).first;
+    }
+    Plan& p = it->second;
+    hipblasStatus_t st = hipblasLtMatmul(B->handle, p.desc, &alpha, w, p.a, x, p.b, &beta, c, p.c, y, p.d, &p.algo,
+                                         B->workspace, p.ws, ctx->stream);
+    if (st != HIPBLAS_STATUS_SUCCESS) return hk_fail(ctx, HK_ERR_DEVICE, "hipblasLtMatmul failed (%d)", (int)st);
+    return HK_OK;
+}

@@ -1,0 +1,49 @@
+// common.hpp - shared device/host helpers for the gfx950 kernels of libhuncho_rocm.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace hk {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Accumulator layout of v_mfma_f32_32x32x{16 bf16, 2 f32} (checked on gfx950): lane l
+// holds column l % 32 and, in element j, row (j / 4) * 8 + (l / 32) * 4 + j % 4.
+__device__ __forceinline__ int acc_row(int j, int g) { return (j >> 2) * 8 + g * 4 + (j & 3); }
+
+__device__ __forceinline__ f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float to_f(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f(float x) { return x; }
+template <typename T> __device__ __forceinline__ T from_f(float x);
+template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) { return (bf16)x; }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float wave_max32(float v) {
+    // combine the two 32-lane halves (lane l and l ^ 32)
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+
+}  // namespace hk
+
+// Status codes shared with include/huncho_rocm.h.
+#define HK_OK 0
+#define HK_ERR_INVALID 1
+#define HK_ERR_UNSUPPORTED 2
+#define HK_ERR_DEVICE 3
+#define HK_ERR_NOMEM 4

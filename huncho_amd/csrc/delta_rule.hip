@@ -1,0 +1,577 @@
+// delta_rule.hip - chunked gated delta rule (Gated DeltaNet recurrence) for gfx950.
+//
+// Computes exactly the reference's per-token recurrence (crates/huncho-backend/src/
+// delta_cpu.rs:95-131, == qwen3_5.rs:950-987): for each token t of a sequence and head,
+//   S <- S * exp(g_t);  m = S^T k_t;  delta_t = (v_t - m) * beta_t;  S <- S + k_t delta_t^T;
+//   o_t = S^T q_t
+// with S [dk, dv] fp32, in the algebraically equal chunked form (chunk C = 64). With
+// G_t = sum_{s<=t} g_s inside a chunk and S0 the state entering it:
+//   A[t,s]   = beta_t exp(G_t - G_s) (k_t . k_s)        s < t   (strictly lower)
+//   T        = (I + A)^-1                              (forward substitution, fp32)
+//   delta    = T [ beta * (V - exp(G) * (K S0)) ]
+//   O        = exp(G) * (Q S0) + Aqk delta,  Aqk[t,s] = exp(G_t - G_s) (q_t . k_s), s <= t
+//   S_next   = exp(G_last) S0 + K^T [exp(G_last - G) * delta]
+// Only decay ratios exp(G_t - G_s) with t >= s (each <= 1) are formed.
+//
+// One workgroup = one (sequence, head); 4 waves; wave w owns value columns 32w..32w+31 of
+// the state, held as four 32x32 MFMA accumulators for the whole sequence, so the state
+// never leaves registers between chunks and is read/written in HBM only at the start (an
+// optional initial state) and the end (the optional final state). Every intermediate
+// (K S, R, delta) stays in accumulator layout and feeds the next MFMA as its B operand:
+// the reduction index of each product is permuted to match the accumulator's row order
+// instead of transposing the data. Inputs stream from HBM once: q, k, v, g, beta in, o out.
+//
+// Two variants: fp32 inputs on v_mfma_f32_32x32x2_f32 (fp32 model path), and bf16 q/k/v/o
+// on v_mfma_f32_32x32x16_bf16 with fp32 accumulation, fp32 state and an fp32 solve (bf16
+// model path).
+#include "common.hpp"
+#include "kernel_args.hpp"
+
+namespace hk {
+
+constexpr int CH = 64;
+constexpr int DK = 128;
+constexpr int DV = 128;
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_incl_scan(float x, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        float y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
+// 16x16 fp32 tiles on v_mfma_f32_16x16x4_f32: operand lane l holds row/column l % 16 and
+// reduction index l / 16; accumulator lane l holds column l % 16, rows (l / 16) * 4 + j.
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// D = X[16][K] . Y[K][16] from fp32 LDS tiles (K a multiple of 4).
+__device__ __forceinline__ f32x4 tile16_mm(const float* X, int ldx, const float* Y, int ldy, int K, int lane) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const int r = lane & 15, kq = lane >> 4;
+    for (int k = 0; k < K; k += 4) acc = mfma16(X[r * ldx + k + kq], Y[(k + kq) * ldy + r], acc);
+    return acc;
+}
+
+// D = -W[16][16] . Xacc where Xacc is a 16x16 accumulator tile: the reduction index of
+// step j is paired with the accumulator row 4 * (l / 16) + j the lane already holds.
+__device__ __forceinline__ f32x4 tile16_neg_mm_acc(const float* W, int ldw, f32x4 xacc, int lane) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const int r = lane & 15, kq = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = mfma16(-W[r * ldw + 4 * kq + j], xacc[j], acc);
+    return acc;
+}
+
+__device__ __forceinline__ void tile16_store(float* D, int ldd, f32x4 acc, int lane) {
+    const int c = lane & 15, r0 = (lane >> 4) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) D[(r0 + j) * ldd + c] = acc[j];
+}
+
+// T = (I + A)^-1 for strictly lower A [64][lda] (fp32, LDS), all 4 waves, blocked:
+//   1. wave w inverts the unit-lower diagonal block w (16x16) by forward substitution;
+//   2. T[1][0] = -T11 A10 T00 and T[3][2] = -T33 A32 T22 (16 -> 32);
+//   3. T[2:4][0:2] = -T[2:4][2:4] A[2:4][0:2] T[0:2][0:2] (32 -> 64), one 16x16 tile per wave.
+// T is written to Tf [64][lda] with its upper triangle zeroed; Xs is a [32][ldx] scratch.
+// Contains __syncthreads(): every thread of the workgroup must call it.
+__device__ void invert_unit_lower(const float* Am, float* Tf, int lda, float* Xs, int ldx, int wave, int lane) {
+    {
+        const int b = wave * 16;
+        if (lane < 16) {
+            float x[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float acc = (i == lane) ? 1.0f : 0.0f;
+                const float* row = Am + (b + i) * lda + b;
+#pragma unroll
+                for (int k = 0; k < i; ++k) acc -= row[k] * x[k];
+                x[i] = acc;
+                Tf[(b + i) * lda + b + lane] = acc;
+            }
+        }
+        // zero the blocks right of the diagonal in this block row
+        for (int idx = lane; idx < 16 * (48 - b); idx += 64) {
+            const int i = idx / (48 - b), j = idx % (48 - b);
+            Tf[(b + i) * lda + b + 16 + j] = 0.0f;
+        }
+    }
+    __syncthreads();
+    if (wave < 2) {
+        const int b = wave * 32;  // diagonal 32-block: [b, b+32)
+        f32x4 x = tile16_mm(Am + (b + 16) * lda + b, lda, Tf + b * lda + b, lda, 16, lane);
+        f32x4 t = tile16_neg_mm_acc(Tf + (b + 16) * lda + b + 16, lda, x, lane);
+        tile16_store(Tf + (b + 16) * lda + b, lda, t, lane);
+    }
+    __syncthreads();
+    {
+        const int rt = wave >> 1, ct = wave & 1;
+        f32x4 x = tile16_mm(Am + (32 + 16 * rt) * lda, lda, Tf + 16 * ct, lda, 32, lane);
+        tile16_store(Xs + 16 * rt * ldx + 16 * ct, ldx, x, lane);
+    }
+    __syncthreads();
+    {
+        const int rt = wave >> 1, ct = wave & 1;
+        f32x4 t = tile16_mm(Tf + (32 + 16 * rt) * lda + 32, lda, Xs + 16 * ct, ldx, 32, lane);
+        t = -t;
+        tile16_store(Tf + (32 + 16 * rt) * lda + 16 * ct, lda, t, lane);
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// fp32 variant
+// ---------------------------------------------------------------------------
+constexpr int F_KSTR = DK + 4;  // fp32 row stride of Kc/Qc
+constexpr int F_ASTR = CH + 4;  // fp32 row stride of A/T and Aqk
+constexpr int XSTR = 32 + 4;    // fp32 row stride of the inversion scratch
+constexpr size_t GDN_F32_LDS = sizeof(float) * (2 * CH * F_KSTR + 3 * CH * F_ASTR + 32 * XSTR + 2 * CH);
+
+__global__ __launch_bounds__(256, 1) void gdn_chunk_f32(GdnArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float smem_f[];
+    float* Kc = smem_f;
+    float* Qc = Kc + CH * F_KSTR;
+    float* Am = Qc + CH * F_KSTR;
+    float* Aq = Am + CH * F_ASTR;
+    float* Tf = Aq + CH * F_ASTR;
+    float* Xs = Tf + CH * F_ASTR;
+    float* Gs = Xs + 32 * XSTR;
+    float* Bs = Gs + CH;
+
+    const int h = blockIdx.x, seq = blockIdx.y, H = a.H;
+    const int t0 = a.cu_seqlens[seq];
+    const int T = a.cu_seqlens[seq + 1] - t0;
+    if (t0 < 0 || T < 0 || t0 + T > a.n_tokens) {
+        if (threadIdx.x == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, col = lane & 31;
+    const int dvc = wave * 32 + col;  // this lane's value column
+    const int kh = h / a.qk_rep;
+    const float* qg = (const float*)a.q + (long)kh * DK;
+    const float* kg = (const float*)a.k + (long)kh * DK;
+    const float* vg = (const float*)a.v + (long)h * DV;
+    float* og = (float*)a.o + (long)h * DV;
+    const long sbase = ((long)seq * H + h) * DK * DV;
+
+    f32x16 S[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            S[rb][j] = a.initial_state ? a.initial_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] : 0.0f;
+
+    for (int c0 = 0; c0 < T; c0 += CH) {
+        const int Lc = min(CH, T - c0);
+        __syncthreads();
+        // q, k chunk -> LDS (zero rows past the end); g, beta -> registers of wave 0
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            int idx = tid + 256 * i, r = idx >> 5, c4 = (idx & 31) * 4;
+            f32x4 qv = {0.f, 0.f, 0.f, 0.f}, kv = {0.f, 0.f, 0.f, 0.f};
+            if (r < Lc) {
+                qv = *(const f32x4*)(qg + (long)(t0 + c0 + r) * a.q_tok + c4);
+                kv = *(const f32x4*)(kg + (long)(t0 + c0 + r) * a.k_tok + c4);
+            }
+            *(f32x4*)(Qc + r * F_KSTR + c4) = qv;
+            *(f32x4*)(Kc + r * F_KSTR + c4) = kv;
+        }
+        if (wave == 0) {
+            float gv = 0.f, bv = 0.f;
+            if (lane < Lc) {
+                gv = a.g[(long)(t0 + c0 + lane) * a.gb_tok + h];
+                bv = a.beta[(long)(t0 + c0 + lane) * a.gb_tok + h];
+            }
+            Gs[lane] = wave_incl_scan(gv, lane);
+            Bs[lane] = bv;
+        }
+        __syncthreads();
+        // A (strictly lower, beta and decay folded in) and Aqk (lower incl. diagonal)
+        if (wave < 3) {
+            const int tb = wave == 0 ? 0 : 1, sb = wave == 2 ? 1 : 0;
+            f32x16 kk = f32x16{}, qk = f32x16{};
+            const float* ka = Kc + (tb * 32 + col) * F_KSTR + 2 * g;
+            const float* qa = Qc + (tb * 32 + col) * F_KSTR + 2 * g;
+            const float* kbp = Kc + (sb * 32 + col) * F_KSTR + 2 * g;
+#pragma unroll 8
+            for (int u = 0; u < 32; ++u) {
+                f32x2 av = *(const f32x2*)(ka + 4 * u);
+                f32x2 qv = *(const f32x2*)(qa + 4 * u);
+                f32x2 bv = *(const f32x2*)(kbp + 4 * u);
+                kk = mfma_f32(av[0], bv[0], kk);
+                kk = mfma_f32(av[1], bv[1], kk);
+                qk = mfma_f32(qv[0], bv[0], qk);
+                qk = mfma_f32(qv[1], bv[1], qk);
+            }
+            const int s = sb * 32 + col;
+            const float Gs_s = Gs[s];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = tb * 32 + acc_row(j, g);
+                const float dec = s <= t ? __expf(Gs[t] - Gs_s) : 0.0f;
+                Am[t * F_ASTR + s] = s < t ? Bs[t] * dec * kk[j] : 0.0f;
+                Aq[t * F_ASTR + s] = s <= t ? dec * qk[j] : 0.0f;
+            }
+        } else {
+            for (int idx = lane; idx < 32 * 32; idx += 64) {
+                const int t = idx >> 5, s = 32 + (idx & 31);
+                Am[t * F_ASTR + s] = 0.0f;
+                Aq[t * F_ASTR + s] = 0.0f;
+            }
+        }
+        __syncthreads();
+        invert_unit_lower(Am, Tf, F_ASTR, Xs, XSTR, wave, lane);
+        // K S0 and Q S0 for this wave's value columns
+        f32x16 ks[2], qs[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            ks[tb] = f32x16{};
+            qs[tb] = f32x16{};
+            const float* kr = Kc + (tb * 32 + col) * F_KSTR + g * 4;
+            const float* qr = Qc + (tb * 32 + col) * F_KSTR + g * 4;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    f32x4 kv = *(const f32x4*)(kr + rb * 32 + jj * 8);
+                    f32x4 qv = *(const f32x4*)(qr + rb * 32 + jj * 8);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        ks[tb] = mfma_f32(kv[e], S[rb][jj * 4 + e], ks[tb]);
+                        qs[tb] = mfma_f32(qv[e], S[rb][jj * 4 + e], qs[tb]);
+                    }
+                }
+        }
+        // R = beta * (V - exp(G) K S0); O starts as exp(G) Q S0
+        f32x16 R[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = tb * 32 + acc_row(j, g);
+                const float eg = __expf(Gs[t]);
+                const float vv = t < Lc ? vg[(long)(t0 + c0 + t) * a.v_tok + dvc] : 0.0f;
+                R[tb][j] = Bs[t] * (vv - eg * ks[tb][j]);
+                qs[tb][j] *= eg;
+            }
+        // delta = T R
+        f32x16 dl[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            dl[tb] = f32x16{};
+            const float* tr = Tf + (tb * 32 + col) * F_ASTR + g * 4;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    f32x4 tv = *(const f32x4*)(tr + sb * 32 + jj * 8);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dl[tb] = mfma_f32(tv[e], R[sb][jj * 4 + e], dl[tb]);
+                }
+        }
+        // O = exp(G) Q S0 + Aqk delta -> HBM
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            const float* ar = Aq + (tb * 32 + col) * F_ASTR + g * 4;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    f32x4 av = *(const f32x4*)(ar + sb * 32 + jj * 8);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) qs[tb] = mfma_f32(av[e], dl[sb][jj * 4 + e], qs[tb]);
+                }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = tb * 32 + acc_row(j, g);
+                if (t < Lc) og[(long)(t0 + c0 + t) * a.o_tok + dvc] = qs[tb][j];
+            }
+        }
+        // S = exp(G_last) S + K^T (exp(G_last - G) delta)
+        const float glast = Gs[CH - 1];
+        const float eglast = __expf(glast);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) dl[tb][j] *= __expf(glast - Gs[tb * 32 + acc_row(j, g)]);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) S[rb][j] *= eglast;
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    S[rb] = mfma_f32(Kc[(tb * 32 + acc_row(j, g)) * F_KSTR + rb * 32 + col], dl[tb][j], S[rb]);
+        }
+    }
+    if (a.final_state) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a.final_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] = S[rb][j];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 variant
+// ---------------------------------------------------------------------------
+constexpr int B_KSTR = DK + 8;  // bf16 row stride of Kc/Qc
+constexpr int B_TSTR = CH + 8;  // bf16 row stride of Kt (transposed k), T and Aqk
+constexpr int B_ASTR = CH + 4;  // fp32 row stride of A (aliased by T afterwards)
+constexpr size_t GDN_BF16_LDS =
+    2 * CH * B_KSTR * 2 + DK * B_TSTR * 2 + 2 * CH * B_ASTR * 4 + CH * B_TSTR * 2 + 32 * XSTR * 4 + 2 * CH * 4;
+
+// 8 bf16 operands whose reduction index g*8+i maps to accumulator rows acc_row(hh*8+i, g)
+// of a 32-block starting at column `base`: two runs of 4 (base+16hh+4g, base+16hh+8+4g).
+__device__ __forceinline__ bf16x8 ld_perm8(const bf16* row, int base, int hh, int g) {
+    bf16x4 lo = *(const bf16x4*)(row + base + 16 * hh + 4 * g);
+    bf16x4 hi = *(const bf16x4*)(row + base + 16 * hh + 8 + 4 * g);
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+__device__ __forceinline__ bf16x8 pack8(const f32x16& v, int hh) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (bf16)v[hh * 8 + i];
+    return r;
+}
+
+__global__ __launch_bounds__(256, 1) void gdn_chunk_bf16(GdnArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char smem_b[];
+    bf16* Kc = (bf16*)smem_b;                   // [64][136]
+    bf16* Qc = Kc + CH * B_KSTR;                // [64][136]
+    bf16* Kt = Qc + CH * B_KSTR;                // [128][72]
+    float* Am = (float*)(Kt + DK * B_TSTR);     // [64][68] fp32; bf16 T [64][72] reuses it
+    bf16* Tm = (bf16*)Am;
+    float* Tf = Am + CH * B_ASTR;               // [64][68] fp32 inverse
+    bf16* Aq = (bf16*)(Tf + CH * B_ASTR);       // [64][72]
+    float* Xs = (float*)(Aq + CH * B_TSTR);     // [32][36]
+    float* Gs = Xs + 32 * XSTR;
+    float* Bs = Gs + CH;
+
+    const int h = blockIdx.x, seq = blockIdx.y, H = a.H;
+    const int t0 = a.cu_seqlens[seq];
+    const int T = a.cu_seqlens[seq + 1] - t0;
+    if (t0 < 0 || T < 0 || t0 + T > a.n_tokens) {
+        if (threadIdx.x == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, col = lane & 31;
+    const int dvc = wave * 32 + col;
+    const int kh = h / a.qk_rep;
+    const bf16* qg = (const bf16*)a.q + (long)kh * DK;
+    const bf16* kg = (const bf16*)a.k + (long)kh * DK;
+    const bf16* vg = (const bf16*)a.v + (long)h * DV;
+    bf16* og = (bf16*)a.o + (long)h * DV;
+    const long sbase = ((long)seq * H + h) * DK * DV;
+
+    f32x16 S[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            S[rb][j] = a.initial_state ? a.initial_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] : 0.0f;
+
+    for (int c0 = 0; c0 < T; c0 += CH) {
+        const int Lc = min(CH, T - c0);
+        __syncthreads();
+        // q rows -> Qc; k rows -> Kc and transposed into Kt. Thread t handles rows
+        // 4*(t/16)+i (i = 0..3) and the 8 dims (t%16)*8.
+        {
+            const int rbase = 4 * (tid >> 4), d0 = (tid & 15) * 8;
+            uint4 kr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = rbase + i;
+                uint4 qv = {0, 0, 0, 0}, kv = {0, 0, 0, 0};
+                if (r < Lc) {
+                    qv = *(const uint4*)(qg + (long)(t0 + c0 + r) * a.q_tok + d0);
+                    kv = *(const uint4*)(kg + (long)(t0 + c0 + r) * a.k_tok + d0);
+                }
+                *(uint4*)(Qc + r * B_KSTR + d0) = qv;
+                *(uint4*)(Kc + r * B_KSTR + d0) = kv;
+                kr[i] = kv;
+            }
+            const bf16* k0 = (const bf16*)&kr[0];
+            const bf16* k1 = (const bf16*)&kr[1];
+            const bf16* k2 = (const bf16*)&kr[2];
+            const bf16* k3 = (const bf16*)&kr[3];
+#pragma unroll
+            for (int dd = 0; dd < 8; ++dd) {
+                bf16x4 w = {k0[dd], k1[dd], k2[dd], k3[dd]};
+                *(bf16x4*)(Kt + (d0 + dd) * B_TSTR + rbase) = w;
+            }
+        }
+        if (wave == 0) {
+            float gv = 0.f, bv = 0.f;
+            if (lane < Lc) {
+                gv = a.g[(long)(t0 + c0 + lane) * a.gb_tok + h];
+                bv = a.beta[(long)(t0 + c0 + lane) * a.gb_tok + h];
+            }
+            Gs[lane] = wave_incl_scan(gv, lane);
+            Bs[lane] = bv;
+        }
+        __syncthreads();
+        if (wave < 3) {
+            const int tb = wave == 0 ? 0 : 1, sb = wave == 2 ? 1 : 0;
+            f32x16 kk = f32x16{}, qk = f32x16{};
+            const bf16* ka = Kc + (tb * 32 + col) * B_KSTR + g * 8;
+            const bf16* qa = Qc + (tb * 32 + col) * B_KSTR + g * 8;
+            const bf16* kbp = Kc + (sb * 32 + col) * B_KSTR + g * 8;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                bf16x8 bv = *(const bf16x8*)(kbp + ks * 16);
+                kk = mfma_bf16(*(const bf16x8*)(ka + ks * 16), bv, kk);
+                qk = mfma_bf16(*(const bf16x8*)(qa + ks * 16), bv, qk);
+            }
+            const int s = sb * 32 + col;
+            const float Gs_s = Gs[s];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = tb * 32 + acc_row(j, g);
+                const float dec = s <= t ? __expf(Gs[t] - Gs_s) : 0.0f;
+                Am[t * B_ASTR + s] = s < t ? Bs[t] * dec * kk[j] : 0.0f;
+                Aq[t * B_TSTR + s] = (bf16)(s <= t ? dec * qk[j] : 0.0f);
+            }
+        } else {
+            for (int idx = lane; idx < 32 * 32; idx += 64) {
+                const int t = idx >> 5, s = 32 + (idx & 31);
+                Am[t * B_ASTR + s] = 0.0f;
+                Aq[t * B_TSTR + s] = (bf16)0.0f;
+            }
+        }
+        __syncthreads();
+        invert_unit_lower(Am, Tf, B_ASTR, Xs, XSTR, wave, lane);
+        // A is dead: round T to bf16 into its space
+        for (int idx = tid; idx < CH * CH; idx += 256) {
+            const int i = idx >> 6, j = idx & 63;
+            Tm[i * B_TSTR + j] = (bf16)Tf[i * B_ASTR + j];
+        }
+        // K S0 and Q S0 (S0 rounded to bf16 as the B operand)
+        bf16x8 Sb[4][2];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            Sb[rb][0] = pack8(S[rb], 0);
+            Sb[rb][1] = pack8(S[rb], 1);
+        }
+        f32x16 ks[2], qs[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            ks[tb] = f32x16{};
+            qs[tb] = f32x16{};
+            const bf16* kr = Kc + (tb * 32 + col) * B_KSTR;
+            const bf16* qr = Qc + (tb * 32 + col) * B_KSTR;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    ks[tb] = mfma_bf16(ld_perm8(kr, rb * 32, hh, g), Sb[rb][hh], ks[tb]);
+                    qs[tb] = mfma_bf16(ld_perm8(qr, rb * 32, hh, g), Sb[rb][hh], qs[tb]);
+                }
+        }
+        f32x16 R[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = tb * 32 + acc_row(j, g);
+                const float eg = __expf(Gs[t]);
+                const float vv = t < Lc ? (float)vg[(long)(t0 + c0 + t) * a.v_tok + dvc] : 0.0f;
+                R[tb][j] = Bs[t] * (vv - eg * ks[tb][j]);
+                qs[tb][j] *= eg;
+            }
+        __syncthreads();  // bf16 T ready
+        bf16x8 Rb[2][2];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            Rb[sb][0] = pack8(R[sb], 0);
+            Rb[sb][1] = pack8(R[sb], 1);
+        }
+        f32x16 dl[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            dl[tb] = f32x16{};
+            const bf16* tr = Tm + (tb * 32 + col) * B_TSTR;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) dl[tb] = mfma_bf16(ld_perm8(tr, sb * 32, hh, g), Rb[sb][hh], dl[tb]);
+        }
+        bf16x8 Db[2][2];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            Db[sb][0] = pack8(dl[sb], 0);
+            Db[sb][1] = pack8(dl[sb], 1);
+        }
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            const bf16* ar = Aq + (tb * 32 + col) * B_TSTR;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) qs[tb] = mfma_bf16(ld_perm8(ar, sb * 32, hh, g), Db[sb][hh], qs[tb]);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = tb * 32 + acc_row(j, g);
+                if (t < Lc) og[(long)(t0 + c0 + t) * a.o_tok + dvc] = (bf16)qs[tb][j];
+            }
+        }
+        const float glast = Gs[CH - 1];
+        const float eglast = __expf(glast);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) dl[tb][j] *= __expf(glast - Gs[tb * 32 + acc_row(j, g)]);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            Db[tb][0] = pack8(dl[tb], 0);
+            Db[tb][1] = pack8(dl[tb], 1);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) S[rb][j] *= eglast;
+            const bf16* ktr = Kt + (rb * 32 + col) * B_TSTR;
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) S[rb] = mfma_bf16(ld_perm8(ktr, tb * 32, hh, g), Db[tb][hh], S[rb]);
+        }
+    }
+    if (a.final_state) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a.final_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] = S[rb][j];
+    }
+}
+
+}  // namespace hk
+
+extern "C" int hk_launch_gated_delta_chunked(int is_bf16, const hk::GdnArgs* args, int n_seqs, hipStream_t stream) {
+    dim3 grid(args->H, n_seqs);
+    if (is_bf16) {
+        static bool configured = false;
+        if (!configured) {
+            if (hipFuncSetAttribute((const void*)hk::gdn_chunk_bf16, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)hk::GDN_BF16_LDS) != hipSuccess)
+                return HK_ERR_DEVICE;
+            configured = true;
+        }
+        hipLaunchKernelGGL(hk::gdn_chunk_bf16, grid, dim3(256), hk::GDN_BF16_LDS, stream, *args);
+    } else {
+        static bool configured = false;
+        if (!configured) {
+            if (hipFuncSetAttribute((const void*)hk::gdn_chunk_f32, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)hk::GDN_F32_LDS) != hipSuccess)
+                return HK_ERR_DEVICE;
+            configured = true;
+        }
+        hipLaunchKernelGGL(hk::gdn_chunk_f32, grid, dim3(256), hk::GDN_F32_LDS, stream, *args);
+    }
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}

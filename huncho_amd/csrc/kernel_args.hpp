@@ -1,0 +1,143 @@
+// kernel_args.hpp - argument blocks passed by value to the gfx950 kernels, and the
+// launcher entry points the host side of the ABI calls after validation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace hk {
+
+struct AttnArgs {
+    const void* q;
+    long q_tok, q_head;
+    const void* k_pool;
+    const void* v_pool;
+    int page_shift;  // log2(page_size)
+    const int* block_tables;
+    int bt_stride;
+    const int* cu_seqlens_q;
+    const int* context_lens;
+    int q_heads, kv_heads, group, pos_per_block;
+    float scale_log2;  // softmax scale * log2(e)
+    const void* gate;
+    long g_tok, g_head;
+    void* o;
+    long o_tok, o_head;
+    int num_pages;
+    int n_tokens;
+    int* fault;
+};
+
+struct GdnArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    long q_tok, k_tok, v_tok;  // token strides (elements); head stride is dk (q,k) / dv (v)
+    int qk_rep;                // value heads per key head
+    const float* g;
+    const float* beta;
+    long gb_tok;
+    const int* cu_seqlens;
+    const float* initial_state;  // [n_seqs][H][dk][dv] or null
+    float* final_state;          // [n_seqs][H][dk][dv] or null
+    void* o;
+    long o_tok;
+    int H;
+    int n_tokens;
+    int* fault;
+};
+
+struct KvArgs {
+    const void* q_in;
+    long q_in_tok, q_in_head;
+    const void* k_in;
+    long k_in_tok;
+    const void* v_in;
+    long v_in_tok;
+    const float* q_norm;  // (1 + w) or null
+    const float* k_norm;
+    float eps;
+    const float* rope_cos;  // [max_pos][rd/2] or null
+    const float* rope_sin;
+    int rd, rope_max_pos;
+    const int* cu_seqlens_q;
+    const int* context_lens;
+    int n_seqs, n_tokens;
+    const int* block_tables;
+    int bt_stride, num_pages, page_shift;
+    int q_heads, kv_heads;
+    void* q_out;
+    long q_out_tok, q_out_head;
+    void* k_pool;
+    void* v_pool;
+    int* fault;
+};
+
+struct PrepArgs {
+    const void* mixed;
+    long mixed_tok;
+    const float* conv_w;  // [conv_dim][K]
+    int K;
+    const void* hist;  // [n_seqs][conv_dim][K-1] or null
+    const void* ba;    // b at col b_col, a at col a_col of each token row
+    long ba_tok;
+    int b_col, a_col;
+    const float* base_g;   // -exp(A_log) [Hv]
+    const float* dt_bias;  // [Hv]
+    const int* cu_seqlens;
+    int n_seqs, n_tokens;
+    int Hk, Hv;
+    float scale;
+    void* q_out;
+    void* k_out;
+    void* v_out;
+    float* g_out;
+    float* beta_out;
+    int* fault;
+};
+
+struct NormArgs {
+    const void* x;
+    long x_tok;
+    const float* w;
+    float eps;
+    int rows, width;
+    void* y;
+    long y_tok;
+};
+
+struct GatedNormArgs {
+    const void* x;  // [rows][width] contiguous (rows = tokens * heads)
+    const void* z;  // token-strided: z[t * z_tok + h * width + i]
+    long z_tok;
+    int heads;
+    const float* w;
+    float eps;
+    int rows, width;
+    void* y;  // [rows][width]
+};
+
+struct SwigluArgs {
+    const void* gu;  // gate at [t * gu_tok + i], up at [t * gu_tok + up_off + i]
+    long gu_tok, up_off;
+    int rows, width;
+    void* y;
+};
+
+}  // namespace hk
+
+extern "C" {
+int hk_launch_paged_prefill_attention(int is_bf16, const hk::AttnArgs* args, int n_seqs, int n_qblocks,
+                                      hipStream_t stream);
+int hk_launch_gated_delta_chunked(int is_bf16, const hk::GdnArgs* args, int n_seqs, hipStream_t stream);
+int hk_launch_qk_norm_rope_kv_write(int is_bf16, const hk::KvArgs* args, hipStream_t stream);
+int hk_launch_gdn_prep(int is_bf16, const hk::PrepArgs* a, void* tail_out, hipStream_t st);
+int hk_launch_rms_norm(int is_bf16, const hk::NormArgs* a, hipStream_t st);
+int hk_launch_gated_rms_norm(int is_bf16, const hk::GatedNormArgs* a, hipStream_t st);
+int hk_launch_swiglu(int is_bf16, const hk::SwigluArgs* a, hipStream_t st);
+int hk_launch_embed(int is_bf16, const int* ids, int n, const void* table, int vocab, int width, void* out, int* fault,
+                    hipStream_t st);
+int hk_launch_final_norm_head(int is_bf16, const void* x, long x_tok, const int* cu, int n_seqs, const float* w_eff,
+                              float eps, int width, const void* head_w, const float* head_b, int n_out, float* logits,
+                              void* h_out, hipStream_t st);
+int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st);
+}

@@ -1,0 +1,363 @@
+// kev_model.cpp - the Kev/Qwen3.5 hybrid scoring forward on one MI355X.
+//
+// Mirrors Model::forward_inner / DecoderLayer::forward (crates/huncho-backend/src/
+// qwen3_5.rs:1083-1104, 1533-1553) for a fresh varlen batch (the native batch path,
+// forward_independent_batch 3138-3194, without right padding):
+//   x = embed(ids)
+//   per layer: h = rms(x) ; x += mixer(h) ; h = rms(x) ; x += down(silu(gate(h)) * up(h))
+//   mixer = Gated DeltaNet (LinearAttn::forward 846-946) or gated full attention
+//           (Attention::forward 586-726)
+//   final: rms of each sequence's last token, then the decision head (fp32).
+// Load-time layout work (done once, qwen3_5.rs:2185-2348 is the reference loader):
+//   * projections that read the same input are fused into one GEMM weight:
+//     GDN in_proj_qkv | in_proj_z | in_proj_b | in_proj_a, attention q_proj | k_proj |
+//     v_proj, MLP gate_proj | up_proj;
+//   * zero-centred norm weights become (1 + w) in fp32 (effective_norm_weight, 180-182),
+//     conv weights, the gated-norm weight and dt_bias become fp32, A_log becomes
+//     base_g = -exp(A_log) in fp32 (788-790);
+//   * a RoPE cos/sin table in the model dtype covers positions 0..max_context-1.
+// Residual adds are folded into the GEMM epilogue (beta = 1 onto the residual stream).
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+#include "abi_internal.hpp"
+
+namespace {
+
+struct Layer {
+    int type = 0;
+    float *in_norm = nullptr, *post_norm = nullptr;
+    void *w_gu = nullptr, *w_down = nullptr;
+    void *w_in = nullptr, *w_out = nullptr;
+    float *conv_w = nullptr, *norm_w = nullptr, *base_g = nullptr, *dt_bias = nullptr;
+    void *w_qkv = nullptr, *w_o = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr;
+};
+
+inline float bf16_to_f32(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+}  // namespace
+
+struct hk_kev_model {
+    hk_ctx* ctx = nullptr;
+    int dtype = HK_BF16;
+    size_t esz = 2;
+    hk_kev_config cfg{};
+    std::vector<int> layer_types;
+    std::vector<Layer> layers;
+    std::vector<void*> owned;
+    void* embed = nullptr;
+    float* final_norm = nullptr;
+    void* head_w = nullptr;
+    float* head_b = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    // derived sizes
+    int key_dim = 0, value_dim = 0, conv_dim = 0, gdn_rows = 0, attn_rows = 0;
+};
+
+static int dev_alloc(hk_kev_model* m, size_t bytes, void** out) {
+    if (hipMalloc(out, bytes) != hipSuccess) return hk_fail(m->ctx, HK_ERR_NOMEM, "model allocation of %zu bytes failed", bytes);
+    m->owned.push_back(*out);
+    return HK_OK;
+}
+
+// Reads `count` elements of the model dtype at src (device) into fp32 on the host.
+static int read_as_f32(hk_kev_model* m, const void* src, size_t count, std::vector<float>& out) {
+    out.resize(count);
+    if (m->dtype == HK_F32)
+        return hk_check_hip(m->ctx, hipMemcpy(out.data(), src, count * 4, hipMemcpyDeviceToHost), "weight read");
+    std::vector<uint16_t> tmp(count);
+    if (int rc = hk_check_hip(m->ctx, hipMemcpy(tmp.data(), src, count * 2, hipMemcpyDeviceToHost), "weight read"))
+        return rc;
+    for (size_t i = 0; i < count; ++i) out[i] = bf16_to_f32(tmp[i]);
+    return HK_OK;
+}
+
+static int upload_f32(hk_kev_model* m, const std::vector<float>& v, float** out) {
+    if (int rc = dev_alloc(m, v.size() * 4, (void**)out)) return rc;
+    return hk_check_hip(m->ctx, hipMemcpy(*out, v.data(), v.size() * 4, hipMemcpyHostToDevice), "weight upload");
+}
+
+// fp32 copy of a small weight, optionally transformed.
+template <typename F>
+static int small_f32(hk_kev_model* m, const void* src, size_t count, float** out, F&& f) {
+    if (!src) return hk_fail(m->ctx, HK_ERR_INVALID, "missing small weight");
+    std::vector<float> v;
+    if (int rc = read_as_f32(m, src, count, v)) return rc;
+    for (auto& x : v) x = f(x);
+    return upload_f32(m, v, out);
+}
+
+// Stacks row-major [rows_i][in] weights into one [sum rows][in] buffer.
+static int fuse_rows(hk_kev_model* m, std::initializer_list<std::pair<const void*, int>> parts, int in, void** out) {
+    size_t rows = 0;
+    for (auto& p : parts) {
+        if (!p.first) return hk_fail(m->ctx, HK_ERR_INVALID, "missing projection weight");
+        rows += p.second;
+    }
+    if (int rc = dev_alloc(m, rows * in * m->esz, out)) return rc;
+    size_t off = 0;
+    for (auto& p : parts) {
+        size_t bytes = (size_t)p.second * in * m->esz;
+        if (int rc = hk_check_hip(m->ctx, hipMemcpy((char*)*out + off, p.first, bytes, hipMemcpyDeviceToDevice),
+                                  "weight fuse"))
+            return rc;
+        off += bytes;
+    }
+    return HK_OK;
+}
+
+extern "C" int hk_kev_model_destroy(hk_kev_model* m) {
+    if (!m) return HK_ERR_INVALID;
+    hipSetDevice(m->ctx->device);
+    hipStreamSynchronize(m->ctx->stream);
+    for (void* p : m->owned) hipFree(p);
+    delete m;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* cfg, const hk_kev_layer_weights* lw,
+                                   const void* embed, const void* final_norm, const void* head_w, const float* head_b,
+                                   hk_kev_model** out) {
+    if (!ctx || !cfg || !lw || !embed || !final_norm || !out) return HK_ERR_INVALID;
+    *out = nullptr;
+    if (dtype != HK_BF16 && dtype != HK_F32) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d", dtype);
+    const hk_kev_config& c = *cfg;
+    if (c.head_dim != 128 || c.lin_key_dim != 128 || c.lin_v_dim != 128)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "head dims must be 128 (got %d/%d/%d)", c.head_dim, c.lin_key_dim,
+                       c.lin_v_dim);
+    if (c.hidden <= 0 || c.hidden % 8 || c.intermediate <= 0 || c.intermediate % 8 || c.n_layers <= 0 || c.vocab <= 0 ||
+        c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads || c.lin_n_k_heads <= 0 ||
+        c.lin_n_v_heads % c.lin_n_k_heads || c.conv_k < 1 || c.max_context <= 0 || c.n_out < 0 ||
+        !c.layer_types_host || c.rotary_dim < 2 || c.rotary_dim > c.head_dim || c.rotary_dim % 2)
+        return hk_fail(ctx, HK_ERR_INVALID, "invalid model configuration");
+    if (c.n_out > 0 && !head_w) return hk_fail(ctx, HK_ERR_INVALID, "missing decision head");
+    hipSetDevice(ctx->device);
+    hk_kev_model* m = new hk_kev_model();
+    m->ctx = ctx;
+    m->dtype = dtype;
+    m->esz = dtype == HK_BF16 ? 2 : 4;
+    m->cfg = c;
+    m->layer_types.assign(c.layer_types_host, c.layer_types_host + c.n_layers);
+    m->cfg.layer_types_host = m->layer_types.data();
+    m->key_dim = c.lin_n_k_heads * c.lin_key_dim;
+    m->value_dim = c.lin_n_v_heads * c.lin_v_dim;
+    m->conv_dim = 2 * m->key_dim + m->value_dim;
+    m->gdn_rows = m->conv_dim + m->value_dim + 2 * c.lin_n_v_heads;
+    m->attn_rows = 2 * c.n_heads * c.head_dim + 2 * c.n_kv_heads * c.head_dim;
+    const int H = c.hidden, I = c.intermediate;
+    int rc = HK_OK;
+    auto fail = [&](int code) {
+        hk_kev_model_destroy(m);
+        return code;
+    };
+    auto eff = [](float w) { return 1.0f + w; };
+    auto same = [](float w) { return w; };
+    auto negexp = [](float w) { return -expf(w); };
+    for (int l = 0; l < c.n_layers; ++l) {
+        const hk_kev_layer_weights& w = lw[l];
+        Layer L;
+        L.type = m->layer_types[l];
+        if ((rc = small_f32(m, w.input_norm, H, &L.in_norm, eff))) return fail(rc);
+        if ((rc = small_f32(m, w.post_norm, H, &L.post_norm, eff))) return fail(rc);
+        if ((rc = fuse_rows(m, {{w.gate_proj, I}, {w.up_proj, I}}, H, &L.w_gu))) return fail(rc);
+        if ((rc = fuse_rows(m, {{w.down_proj, H}}, I, &L.w_down))) return fail(rc);
+        if (L.type == 0) {
+            const int Hv = c.lin_n_v_heads;
+            if ((rc = fuse_rows(m, {{w.in_qkv, m->conv_dim}, {w.in_z, m->value_dim}, {w.in_b, Hv}, {w.in_a, Hv}}, H,
+                                &L.w_in)))
+                return fail(rc);
+            if ((rc = fuse_rows(m, {{w.out_proj, H}}, m->value_dim, &L.w_out))) return fail(rc);
+            if ((rc = small_f32(m, w.conv_w, (size_t)m->conv_dim * c.conv_k, &L.conv_w, same))) return fail(rc);
+            if ((rc = small_f32(m, w.norm_w, c.lin_v_dim, &L.norm_w, same))) return fail(rc);
+            if ((rc = small_f32(m, w.a_log, Hv, &L.base_g, negexp))) return fail(rc);
+            if ((rc = small_f32(m, w.dt_bias, Hv, &L.dt_bias, same))) return fail(rc);
+        } else {
+            const int hd = c.head_dim;
+            if ((rc = fuse_rows(m, {{w.q_proj, 2 * c.n_heads * hd}, {w.k_proj, c.n_kv_heads * hd}, {w.v_proj, c.n_kv_heads * hd}},
+                                H, &L.w_qkv)))
+                return fail(rc);
+            if ((rc = fuse_rows(m, {{w.o_proj, H}}, c.n_heads * hd, &L.w_o))) return fail(rc);
+            if ((rc = small_f32(m, w.q_norm, hd, &L.q_norm, eff))) return fail(rc);
+            if ((rc = small_f32(m, w.k_norm, hd, &L.k_norm, eff))) return fail(rc);
+        }
+        m->layers.push_back(L);
+    }
+    if ((rc = fuse_rows(m, {{embed, c.vocab}}, H, &m->embed))) return fail(rc);
+    if ((rc = small_f32(m, final_norm, H, &m->final_norm, eff))) return fail(rc);
+    if (c.n_out > 0) {
+        if ((rc = fuse_rows(m, {{head_w, c.n_out}}, H, &m->head_w))) return fail(rc);
+        if (head_b) {
+            std::vector<float> hb(c.n_out);
+            if ((rc = hk_check_hip(ctx, hipMemcpy(hb.data(), head_b, c.n_out * 4, hipMemcpyDeviceToHost), "head bias")))
+                return fail(rc);
+            if ((rc = upload_f32(m, hb, &m->head_b))) return fail(rc);
+        }
+    }
+    {
+        const int half = c.rotary_dim / 2;
+        std::vector<float> cs((size_t)c.max_context * half), sn((size_t)c.max_context * half);
+        hk_rope_fill_table(c.rotary_dim, c.rope_theta, c.max_context, dtype == HK_BF16, cs.data(), sn.data());
+        if ((rc = upload_f32(m, cs, &m->rope_cos)) || (rc = upload_f32(m, sn, &m->rope_sin))) return fail(rc);
+    }
+    *out = m;
+    return HK_OK;
+}
+
+namespace {
+
+struct Workspace {
+    size_t off = 0;
+    char* base = nullptr;
+    template <typename T>
+    T* take(size_t count) {
+        size_t bytes = (count * sizeof(T) + 255) & ~(size_t)255;
+        T* p = (T*)(base ? base + off : nullptr);
+        off += bytes;
+        return p;
+    }
+    void* take_bytes(size_t bytes) {
+        bytes = (bytes + 255) & ~(size_t)255;
+        void* p = base ? base + off : nullptr;
+        off += bytes;
+        return p;
+    }
+};
+
+struct Buffers {
+    void *x, *h, *big, *q, *k, *v, *o, *act, *k_pool, *v_pool;
+    float *g, *beta;
+    int* ctx_lens;
+    size_t pool_bytes;
+};
+
+Buffers carve(const hk_kev_model* m, Workspace& ws, int n, int n_seqs, int num_pages) {
+    const hk_kev_config& c = m->cfg;
+    Buffers b{};
+    const size_t e = m->esz;
+    int big_cols = m->gdn_rows;
+    if (m->attn_rows > big_cols) big_cols = m->attn_rows;
+    if (2 * c.intermediate > big_cols) big_cols = 2 * c.intermediate;
+    b.x = ws.take_bytes((size_t)n * c.hidden * e);
+    b.h = ws.take_bytes((size_t)n * c.hidden * e);
+    b.big = ws.take_bytes((size_t)n * big_cols * e);
+    b.q = ws.take_bytes((size_t)n * m->key_dim * e);
+    b.k = ws.take_bytes((size_t)n * m->key_dim * e);
+    b.v = ws.take_bytes((size_t)n * m->value_dim * e);
+    int o_cols = m->value_dim > c.n_heads * c.head_dim ? m->value_dim : c.n_heads * c.head_dim;
+    b.o = ws.take_bytes((size_t)n * o_cols * e);
+    b.act = ws.take_bytes((size_t)n * c.intermediate * e);
+    b.g = ws.take<float>((size_t)n * c.lin_n_v_heads);
+    b.beta = ws.take<float>((size_t)n * c.lin_n_v_heads);
+    b.ctx_lens = ws.take<int>((size_t)n_seqs);
+    b.pool_bytes = (size_t)num_pages * c.n_kv_heads * c.page_size * c.head_dim * e;
+    b.k_pool = ws.take_bytes(b.pool_bytes);
+    b.v_pool = ws.take_bytes(b.pool_bytes);
+    return b;
+}
+
+}  // namespace
+
+extern "C" int hk_kev_workspace_size(hk_kev_model* m, int n_tokens, int n_seqs, size_t* bytes_out) {
+    if (!m || !bytes_out || n_tokens < 0 || n_seqs <= 0) return HK_ERR_INVALID;
+    // pools sized for every sequence's pages; callers that share pages may pass fewer
+    const int P = m->cfg.page_size;
+    const int pages = (n_tokens + n_seqs * (P - 1)) / P + 1;
+    Workspace ws;
+    carve(m, ws, n_tokens, n_seqs, pages);
+    *bytes_out = ws.off;
+    return HK_OK;
+}
+
+#define RUN(expr)                  \
+    do {                           \
+        int rc__ = (expr);         \
+        if (rc__) return rc__;     \
+    } while (0)
+
+extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev, const int32_t* cu_host,
+                              int n_seqs, const int32_t* bt, int bt_stride, int num_pages, void* workspace,
+                              size_t workspace_bytes, float* logits, void* hidden_last) {
+    if (!m) return HK_ERR_INVALID;
+    hk_ctx* ctx = m->ctx;
+    const hk_kev_config& c = m->cfg;
+    if (!ids || !cu_dev || !cu_host || !bt || !workspace || n_seqs <= 0 || bt_stride <= 0 || num_pages <= 0)
+        return hk_fail(ctx, HK_ERR_INVALID, "invalid forward arguments");
+    if (c.n_out > 0 && !logits) return hk_fail(ctx, HK_ERR_INVALID, "logits output required");
+    if (cu_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "cu_seqlens[0] must be 0");
+    int max_len = 0;
+    for (int s = 0; s < n_seqs; ++s) {
+        const int len = cu_host[s + 1] - cu_host[s];
+        if (len <= 0) return hk_fail(ctx, HK_ERR_INVALID, "sequence %d is empty", s);
+        if (len > c.max_context) return hk_fail(ctx, HK_ERR_INVALID, "sequence length %d exceeds max_context %d", len, c.max_context);
+        if ((len + c.page_size - 1) / c.page_size > bt_stride)
+            return hk_fail(ctx, HK_ERR_INVALID, "sequence %d needs more pages than bt_stride", s);
+        if (len > max_len) max_len = len;
+    }
+    const int n = cu_host[n_seqs];
+    Workspace ws;
+    ws.base = (char*)workspace;
+    Buffers b = carve(m, ws, n, n_seqs, num_pages);
+    if (ws.off > workspace_bytes) return hk_fail(ctx, HK_ERR_INVALID, "workspace too small: %zu < %zu", workspace_bytes, ws.off);
+    hipSetDevice(ctx->device);
+    const int dt = m->dtype, isb = dt == HK_BF16;
+    const size_t e = m->esz;
+    const int H = c.hidden, I = c.intermediate, hd = c.head_dim;
+    const int Hq = c.n_heads, Hkv = c.n_kv_heads, Hv = c.lin_n_v_heads, Hk = c.lin_n_k_heads;
+
+    RUN(hk_launch_seq_lens(cu_dev, n_seqs, b.ctx_lens, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "seq_lens") : 0);
+    RUN(hk_launch_embed(isb, ids, n, m->embed, c.vocab, H, b.x, ctx->fault_dev, ctx->stream)
+            ? hk_fail(ctx, HK_ERR_DEVICE, "embed launch")
+            : 0);
+    for (int l = 0; l < c.n_layers; ++l) {
+        const Layer& L = m->layers[l];
+        RUN(hk_rms_norm(ctx, dt, b.x, H, L.in_norm, c.eps, n, H, b.h, H));
+        if (L.type == 0) {
+            const int rows = m->gdn_rows;
+            RUN(hk_gemm_xwt(ctx, dt, n, rows, H, b.h, H, L.w_in, H, b.big, rows, nullptr, 0, 1.0f, 0.0f));
+            RUN(hk_gdn_prep(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, b.big, rows,
+                            m->conv_dim + m->value_dim, m->conv_dim + m->value_dim + Hv, L.base_g, L.dt_bias, cu_dev,
+                            n_seqs, n, Hv, Hk, b.q, b.k, b.v, b.g, b.beta, nullptr));
+            RUN(hk_gated_delta_chunked(ctx, dt, b.q, (long)Hk * 128, b.k, (long)Hk * 128, b.v, (long)Hv * 128, b.g,
+                                       b.beta, cu_dev, n_seqs, n, Hv, Hk, 128, 128, nullptr, nullptr, b.o,
+                                       (long)Hv * 128));
+            RUN(hk_gated_rms_norm(ctx, dt, b.o, (char*)b.big + (size_t)m->conv_dim * e, rows, Hv, L.norm_w, c.eps,
+                                  n * Hv, 128, b.o));
+            RUN(hk_gemm_xwt(ctx, dt, n, H, m->value_dim, b.o, m->value_dim, L.w_out, m->value_dim, b.x, H, b.x, H, 1.0f,
+                            1.0f));
+        } else {
+            const int rows = m->attn_rows;
+            RUN(hk_gemm_xwt(ctx, dt, n, rows, H, b.h, H, L.w_qkv, H, b.big, rows, nullptr, 0, 1.0f, 0.0f));
+            char* qg = (char*)b.big;
+            char* kin = qg + (size_t)2 * Hq * hd * e;
+            char* vin = kin + (size_t)Hkv * hd * e;
+            RUN(hk_qk_norm_rope_kv_write(ctx, dt, qg, rows, 2 * hd, kin, rows, vin, rows, L.q_norm, L.k_norm, c.eps,
+                                         m->rope_cos, m->rope_sin, c.rotary_dim, c.max_context, cu_dev, b.ctx_lens,
+                                         n_seqs, n, bt, bt_stride, num_pages, c.page_size, Hq, Hkv, hd, qg, rows,
+                                         2 * hd, b.k_pool, b.v_pool));
+            RUN(hk_paged_prefill_attention(ctx, dt, qg, rows, 2 * hd, b.k_pool, b.v_pool, num_pages, c.page_size, bt,
+                                           bt_stride, cu_dev, b.ctx_lens, n_seqs, n, max_len, Hq, Hkv, hd,
+                                           (float)(1.0 / sqrt((double)hd)), qg + (size_t)hd * e, rows, 2 * hd, b.o,
+                                           (long)Hq * hd, hd));
+            RUN(hk_gemm_xwt(ctx, dt, n, H, Hq * hd, b.o, Hq * hd, L.w_o, Hq * hd, b.x, H, b.x, H, 1.0f, 1.0f));
+        }
+        RUN(hk_rms_norm(ctx, dt, b.x, H, L.post_norm, c.eps, n, H, b.h, H));
+        RUN(hk_gemm_xwt(ctx, dt, n, 2 * I, H, b.h, H, L.w_gu, H, b.big, 2 * I, nullptr, 0, 1.0f, 0.0f));
+        RUN(hk_swiglu(ctx, dt, b.big, 2 * I, I, n, I, b.act));
+        RUN(hk_gemm_xwt(ctx, dt, n, H, I, b.act, I, L.w_down, I, b.x, H, b.x, H, 1.0f, 1.0f));
+    }
+    if (c.n_out > 0 || hidden_last) {
+        RUN(hk_launch_final_norm_head(isb, b.x, H, cu_dev, n_seqs, m->final_norm, c.eps, H, m->head_w, m->head_b,
+                                      c.n_out, logits, hidden_last, ctx->stream)
+                ? hk_fail(ctx, HK_ERR_DEVICE, "final head launch")
+                : 0);
+    }
+    return HK_OK;
+}

@@ -1,0 +1,139 @@
+// kv_ops.hip - fused per-head RMSNorm (q_norm / k_norm) + partial RoPE + paged KV write.
+//
+// Reference semantics (crates/huncho-backend/src/qwen3_5.rs):
+//   * q/gate split per head [q(d) | gate(d)] (596-599); the gate is left in place and
+//     read by the attention epilogue;
+//   * q_norm / k_norm: zero-centred RMSNorm, x / sqrt(mean(x^2) + eps) * (1 + w), in fp32,
+//     stored in the activation dtype (184-190, 602-608);
+//   * partial NeoX RoPE on the first rd dims: x*cos + rotate_half(x)*sin with cos/sin
+//     tables in the activation dtype (220-283); in bf16 each of the two products and the
+//     sum is rounded, as the reference's bf16 tensor ops round;
+//   * paged append: token j of sequence s goes to page block_tables[s][j / P], slot j % P
+//     (qwen3_5/kv_pages.rs:307-341), pool layout [page][kv_head][P][d].
+// One workgroup per token; each wave processes one head row of 128 at a time with two
+// elements per lane (i and i + 64). Page indices are range-checked on the device: an
+// out-of-range entry skips the write and raises the context's fault flag.
+#include "common.hpp"
+#include "kernel_args.hpp"
+
+namespace hk {
+
+constexpr int HD = 128;
+
+__device__ __forceinline__ int find_seq(const int* cu, int n, int t) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ float rnd(float x) { return to_f(from_f<T>(x)); }
+
+// Normalise (optional) and rotate (optional) one 128-wide head row held as (x0 = elem lane,
+// x1 = elem lane + 64); result rounded to T at the reference's storage points.
+template <typename T>
+__device__ __forceinline__ void norm_rope(float& x0, float& x1, const float* w, float eps, const float* cs,
+                                          const float* sn, int rd, int lane) {
+    if (w) {
+        float ss = wave_sum(x0 * x0 + x1 * x1);
+        float denom = sqrtf(ss / (float)HD + eps);
+        x0 = rnd<T>((x0 / denom) * w[lane]);
+        x1 = rnd<T>((x1 / denom) * w[lane + 64]);
+    }
+    if (cs) {
+        // element e pairs with e + half (e < half) or e - half (half <= e < rd); the
+        // shuffles run on every lane, the selection afterwards
+        const int half = rd >> 1;
+        const int e0 = lane, e1 = lane + 64;
+        const int p0 = e0 < rd ? (e0 < half ? e0 + half : e0 - half) : e0;
+        const int p1 = e1 < rd ? (e1 < half ? e1 + half : e1 - half) : e1;
+        const float a0 = __shfl(x0, p0 & 63), b0 = __shfl(x1, p0 & 63);
+        const float a1 = __shfl(x0, p1 & 63), b1 = __shfl(x1, p1 & 63);
+        const float pv0 = p0 < 64 ? a0 : b0, pv1 = p1 < 64 ? a1 : b1;
+        if (e0 < rd) {
+            const int fi = e0 < half ? e0 : e0 - half;
+            const float rot = e0 < half ? -pv0 : pv0;
+            x0 = rnd<T>(rnd<T>(x0 * cs[fi]) + rnd<T>(rot * sn[fi]));
+        }
+        if (e1 < rd) {
+            const int fi = e1 < half ? e1 : e1 - half;
+            const float rot = e1 < half ? -pv1 : pv1;
+            x1 = rnd<T>(rnd<T>(x1 * cs[fi]) + rnd<T>(rot * sn[fi]));
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void qk_norm_rope_kv_write(KvArgs a) {
+    const int t = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int s = find_seq(a.cu_seqlens_q, a.n_seqs, t);
+    const int q0 = a.cu_seqlens_q[s];
+    const int q_len = a.cu_seqlens_q[s + 1] - q0;
+    const int ctx = a.context_lens[s];
+    const int pos = ctx - q_len + (t - q0);
+    if (pos < 0 || t - q0 >= q_len) {
+        if (threadIdx.x == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    const float* cs = nullptr;
+    const float* sn = nullptr;
+    if (a.rope_cos) {
+        if (pos >= a.rope_max_pos) {
+            if (threadIdx.x == 0) atomicOr(a.fault, 4);
+            return;
+        }
+        cs = a.rope_cos + (long)pos * (a.rd >> 1);
+        sn = a.rope_sin + (long)pos * (a.rd >> 1);
+    }
+    // queries
+    for (int h = wave; h < a.q_heads; h += 4) {
+        const T* src = (const T*)a.q_in + (long)t * a.q_in_tok + (long)h * a.q_in_head;
+        float x0 = to_f(src[lane]), x1 = to_f(src[lane + 64]);
+        norm_rope<T>(x0, x1, a.q_norm, a.eps, cs, sn, a.rd, lane);
+        T* dst = (T*)a.q_out + (long)t * a.q_out_tok + (long)h * a.q_out_head;
+        dst[lane] = from_f<T>(x0);
+        dst[lane + 64] = from_f<T>(x1);
+    }
+    // keys and values into the pool
+    const int pidx = pos >> a.page_shift;
+    int page = -1;
+    if (pidx < a.bt_stride) page = a.block_tables[(long)s * a.bt_stride + pidx];
+    if (page < 0 || page >= a.num_pages) {
+        if (threadIdx.x == 0) atomicOr(a.fault, 2);
+        return;
+    }
+    const long slot_base = ((long)page * a.kv_heads << a.page_shift) + (pos & ((1 << a.page_shift) - 1));
+    for (int h = wave; h < a.kv_heads; h += 4) {
+        const T* src = (const T*)a.k_in + (long)t * a.k_in_tok + (long)h * HD;
+        float x0 = to_f(src[lane]), x1 = to_f(src[lane + 64]);
+        norm_rope<T>(x0, x1, a.k_norm, a.eps, cs, sn, a.rd, lane);
+        T* dst = (T*)a.k_pool + (slot_base + ((long)h << a.page_shift)) * HD;
+        dst[lane] = from_f<T>(x0);
+        dst[lane + 64] = from_f<T>(x1);
+        const T* vs = (const T*)a.v_in + (long)t * a.v_in_tok + (long)h * HD;
+        T* vd = (T*)a.v_pool + (slot_base + ((long)h << a.page_shift)) * HD;
+        vd[lane] = vs[lane];
+        vd[lane + 64] = vs[lane + 64];
+    }
+}
+
+}  // namespace hk
+
+extern "C" int hk_launch_qk_norm_rope_kv_write(int is_bf16, const hk::KvArgs* args, hipStream_t stream) {
+    if (args->n_tokens == 0) return HK_OK;
+    if (is_bf16)
+        hipLaunchKernelGGL(hk::qk_norm_rope_kv_write<hk::bf16>, dim3(args->n_tokens), dim3(256), 0, stream, *args);
+    else
+        hipLaunchKernelGGL(hk::qk_norm_rope_kv_write<float>, dim3(args->n_tokens), dim3(256), 0, stream, *args);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}

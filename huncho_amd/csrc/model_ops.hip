@@ -1,0 +1,325 @@
+// model_ops.hip - the memory-bound elementwise ops of the Qwen3.5 (Kev) forward on gfx950.
+//
+//   gdn_prep            causal depthwise conv (K taps, ascending) + SiLU on the q|k|v
+//                       channels (qwen3_5.rs:817-870, conv_cpu.rs:34-48), then per head:
+//                       l2norm (204-210) of q and k, q * dk^-1/2 (923-924),
+//                       beta = sigmoid(b) (893), g = -exp(A_log) * softplus(a + dt_bias)
+//                       (889-899, softplus = log(exp(x) + 1), 212-214)
+//   conv_tail           the last K-1 raw conv inputs per sequence (cache tail, 851-868)
+//   rms_norm            zero-centred RMSNorm with (1 + w) pre-baked (178-190)
+//   gated_rms_norm      rms_norm(x) * w * silu(z) with plain w (193-201, 935-938)
+//   swiglu              silu(gate) * up in the activation dtype (1020-1031, gate_cpu.rs:8-47)
+//   embed_gather        token-id row gather (1537) with a range check
+//   final_norm_head     final RMSNorm of each sequence's last token (1548) and a linear
+//                       decision head in fp32 (the Kev readout runs its projections in
+//                       fp32, kev.rs:161-165)
+// All math is fp32 with rounding to the storage type T where the reference stores a
+// tensor of the activation dtype. One wave per 128-wide head row or per hidden row.
+#include "common.hpp"
+#include "kernel_args.hpp"
+
+namespace hk {
+
+__device__ __forceinline__ float wsum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+template <typename T>
+__device__ __forceinline__ float rndt(float x) { return to_f(from_f<T>(x)); }
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ int seq_of(const int* cu, int n, int t) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+constexpr int HW = 128;  // head width of the GDN heads
+
+template <typename T>
+__global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
+    const int t = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int s = seq_of(a.cu_seqlens, a.n_seqs, t);
+    const int start = a.cu_seqlens[s];
+    if (start < 0 || start > t || a.cu_seqlens[s + 1] > a.n_tokens) {
+        if (threadIdx.x == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    const int key_dim = a.Hk * HW;
+    const int conv_dim = 2 * key_dim + a.Hv * HW;
+    const int rows = 2 * a.Hk + a.Hv;
+    const int K = a.K;
+    for (int r = wave; r < rows; r += 4) {
+        float x[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int c = r * HW + lane + 64 * e;
+            float acc = 0.0f;
+            for (int tap = 0; tap < K; ++tap) {
+                const int tt = t - (K - 1) + tap;
+                float xv;
+                if (tt >= start) {
+                    xv = to_f(((const T*)a.mixed)[(long)tt * a.mixed_tok + c]);
+                } else if (a.hist) {
+                    xv = to_f(((const T*)a.hist)[((long)s * conv_dim + c) * (K - 1) + (tt - start + K - 1)]);
+                } else {
+                    continue;
+                }
+                acc += a.conv_w[(long)c * K + tap] * xv;
+            }
+            x[e] = rndt<T>(silu(acc));
+        }
+        if (r < 2 * a.Hk) {
+            const bool is_q = r < a.Hk;
+            const int hh = is_q ? r : r - a.Hk;
+            const float ss = wsum(x[0] * x[0] + x[1] * x[1]);
+            const float inv = 1.0f / sqrtf(ss + 1e-6f);
+            float y0 = x[0] * inv, y1 = x[1] * inv;
+            if (is_q) {
+                y0 *= a.scale;
+                y1 *= a.scale;
+            }
+            T* dst = (T*)(is_q ? a.q_out : a.k_out) + ((long)t * a.Hk + hh) * HW;
+            dst[lane] = from_f<T>(y0);
+            dst[lane + 64] = from_f<T>(y1);
+        } else {
+            const int hh = r - 2 * a.Hk;
+            T* dst = (T*)a.v_out + ((long)t * a.Hv + hh) * HW;
+            dst[lane] = from_f<T>(x[0]);
+            dst[lane + 64] = from_f<T>(x[1]);
+        }
+    }
+    if (threadIdx.x < a.Hv) {
+        const int h = threadIdx.x;
+        const T* row = (const T*)a.ba + (long)t * a.ba_tok;
+        const float b = to_f(row[a.b_col + h]);
+        const float av = to_f(row[a.a_col + h]);
+        a.beta_out[(long)t * a.Hv + h] = rndt<T>(1.0f / (1.0f + __expf(-b)));
+        a.g_out[(long)t * a.Hv + h] = a.base_g[h] * __logf(__expf(av + a.dt_bias[h]) + 1.0f);
+    }
+}
+
+// Tail of the concatenated [history, x] sequence: its last K-1 raw inputs per channel.
+template <typename T>
+__global__ void conv_tail(PrepArgs a, void* tail_out, int conv_dim) {
+    const int s = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= conv_dim) return;
+    const int start = a.cu_seqlens[s], len = a.cu_seqlens[s + 1] - start, K = a.K;
+    if (start < 0 || len < 0 || start + len > a.n_tokens) return;
+    for (int i = 0; i < K - 1; ++i) {
+        const int idx = len + (a.hist ? K - 1 : 0) - (K - 1) + i;  // index in [history, x]
+        T v = from_f<T>(0.0f);
+        if (idx >= 0) {
+            if (a.hist) {
+                v = idx < K - 1 ? ((const T*)a.hist)[((long)s * conv_dim + c) * (K - 1) + idx]
+                                : ((const T*)a.mixed)[(long)(start + idx - (K - 1)) * a.mixed_tok + c];
+            } else {
+                v = ((const T*)a.mixed)[(long)(start + idx) * a.mixed_tok + c];
+            }
+        }
+        ((T*)tail_out)[((long)s * conv_dim + c) * (K - 1) + i] = v;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rms_norm(NormArgs a) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= a.rows) return;
+    const T* x = (const T*)a.x + (long)row * a.x_tok;
+    T* y = (T*)a.y + (long)row * a.y_tok;
+    float ss = 0.0f;
+    for (int i = lane; i < a.width; i += 64) {
+        float v = to_f(x[i]);
+        ss += v * v;
+    }
+    ss = wsum(ss);
+    const float denom = sqrtf(ss / (float)a.width + a.eps);
+    for (int i = lane; i < a.width; i += 64) y[i] = from_f<T>((to_f(x[i]) / denom) * a.w[i]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void gated_rms_norm(GatedNormArgs a) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= a.rows) return;
+    const int t = row / a.heads, h = row % a.heads;
+    const T* x = (const T*)a.x + (long)row * a.width;
+    const T* z = (const T*)a.z + (long)t * a.z_tok + (long)h * a.width;
+    T* y = (T*)a.y + (long)row * a.width;
+    float ss = 0.0f;
+    for (int i = lane; i < a.width; i += 64) {
+        float v = to_f(x[i]);
+        ss += v * v;
+    }
+    ss = wsum(ss);
+    const float denom = sqrtf(ss / (float)a.width + a.eps);
+    for (int i = lane; i < a.width; i += 64)
+        y[i] = from_f<T>(((to_f(x[i]) / denom) * a.w[i]) * silu(to_f(z[i])));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu(SwigluArgs a) {
+    const long n = (long)a.rows * a.width;
+    for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
+        const long r = idx / a.width, i = idx % a.width;
+        const T* row = (const T*)a.gu + r * a.gu_tok;
+        const float sg = rndt<T>(silu(to_f(row[i])));
+        ((T*)a.y)[idx] = from_f<T>(sg * to_f(row[a.up_off + i]));
+    }
+}
+
+// bf16 fast path: 8 elements per thread with 16-byte accesses (width % 8 == 0).
+__global__ __launch_bounds__(256) void swiglu_bf16x8(SwigluArgs a) {
+    const int w8 = a.width >> 3;
+    const long n = (long)a.rows * w8;
+    for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
+        const long r = idx / w8, i = (idx % w8) * 8;
+        const bf16* row = (const bf16*)a.gu + r * a.gu_tok;
+        bf16x8 gv = *(const bf16x8*)(row + i);
+        bf16x8 uv = *(const bf16x8*)(row + a.up_off + i);
+        bf16x8 out;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] = (bf16)((float)(bf16)silu((float)gv[e]) * (float)uv[e]);
+        *(bf16x8*)((bf16*)a.y + r * a.width + i) = out;
+    }
+}
+
+template <typename T>
+__global__ void embed_gather(const int* ids, int n, const void* table, int vocab, int width, void* out, int* fault) {
+    const int t = blockIdx.x;
+    if (t >= n) return;
+    const int id = ids[t];
+    if (id < 0 || id >= vocab) {
+        if (threadIdx.x == 0) atomicOr(fault, 8);
+        return;
+    }
+    const T* src = (const T*)table + (long)id * width;
+    T* dst = (T*)out + (long)t * width;
+    for (int i = threadIdx.x; i < width; i += blockDim.x) dst[i] = src[i];
+}
+
+// One workgroup (one wave) per sequence: final RMSNorm of the last token, rounded to T,
+// then logits[c] = sum_i h[i] * W[c][i] (+ b[c]) in fp32.
+template <typename T>
+__global__ void final_norm_head(const void* x, long x_tok, const int* cu, const float* w_eff, float eps, int width,
+                                const void* head_w, const float* head_b, int n_out, float* logits, void* h_out) {
+    const int s = blockIdx.x, lane = threadIdx.x;
+    const int t = cu[s + 1] - 1;
+    const T* xr = (const T*)x + (long)t * x_tok;
+    float ss = 0.0f;
+    for (int i = lane; i < width; i += 64) {
+        float v = to_f(xr[i]);
+        ss += v * v;
+    }
+    ss = wsum(ss);
+    const float denom = sqrtf(ss / (float)width + eps);
+    for (int c = 0; c < n_out; ++c) {
+        float acc = 0.0f;
+        for (int i = lane; i < width; i += 64) {
+            float hv = rndt<T>((to_f(xr[i]) / denom) * w_eff[i]);
+            acc += hv * to_f(((const T*)head_w)[(long)c * width + i]);
+        }
+        acc = wsum(acc);
+        if (lane == 0) logits[(long)s * n_out + c] = head_b ? acc + head_b[c] : acc;
+    }
+    if (h_out)
+        for (int i = lane; i < width; i += 64)
+            ((T*)h_out)[(long)s * width + i] = from_f<T>((to_f(xr[i]) / denom) * w_eff[i]);
+}
+
+}  // namespace hk
+
+using namespace hk;
+
+extern "C" int hk_launch_gdn_prep(int is_bf16, const PrepArgs* a, void* tail_out, hipStream_t st) {
+    if (a->n_tokens > 0) {
+        if (is_bf16)
+            hipLaunchKernelGGL(gdn_prep<bf16>, dim3(a->n_tokens), dim3(256), 0, st, *a);
+        else
+            hipLaunchKernelGGL(gdn_prep<float>, dim3(a->n_tokens), dim3(256), 0, st, *a);
+    }
+    if (tail_out) {
+        const int conv_dim = (2 * a->Hk + a->Hv) * HW;
+        dim3 grid((conv_dim + 255) / 256, a->n_seqs);
+        if (is_bf16)
+            hipLaunchKernelGGL(conv_tail<bf16>, grid, dim3(256), 0, st, *a, tail_out, conv_dim);
+        else
+            hipLaunchKernelGGL(conv_tail<float>, grid, dim3(256), 0, st, *a, tail_out, conv_dim);
+    }
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+extern "C" int hk_launch_rms_norm(int is_bf16, const NormArgs* a, hipStream_t st) {
+    if (a->rows == 0) return HK_OK;
+    dim3 grid((a->rows + 3) / 4);
+    if (is_bf16)
+        hipLaunchKernelGGL(rms_norm<bf16>, grid, dim3(256), 0, st, *a);
+    else
+        hipLaunchKernelGGL(rms_norm<float>, grid, dim3(256), 0, st, *a);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+extern "C" int hk_launch_gated_rms_norm(int is_bf16, const GatedNormArgs* a, hipStream_t st) {
+    if (a->rows == 0) return HK_OK;
+    dim3 grid((a->rows + 3) / 4);
+    if (is_bf16)
+        hipLaunchKernelGGL(gated_rms_norm<bf16>, grid, dim3(256), 0, st, *a);
+    else
+        hipLaunchKernelGGL(gated_rms_norm<float>, grid, dim3(256), 0, st, *a);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+extern "C" int hk_launch_swiglu(int is_bf16, const SwigluArgs* a, hipStream_t st) {
+    if (a->rows == 0) return HK_OK;
+    const bool vec = is_bf16 && a->width % 8 == 0 && a->gu_tok % 8 == 0 && a->up_off % 8 == 0;
+    const long work = vec ? (long)a->rows * a->width / 8 : (long)a->rows * a->width;
+    const int blocks = (int)((work + 255) / 256 < 65536 ? (work + 255) / 256 : 65536);
+    if (vec)
+        hipLaunchKernelGGL(swiglu_bf16x8, dim3(blocks), dim3(256), 0, st, *a);
+    else if (is_bf16)
+        hipLaunchKernelGGL(swiglu<bf16>, dim3(blocks), dim3(256), 0, st, *a);
+    else
+        hipLaunchKernelGGL(swiglu<float>, dim3(blocks), dim3(256), 0, st, *a);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+extern "C" int hk_launch_embed(int is_bf16, const int* ids, int n, const void* table, int vocab, int width, void* out,
+                               int* fault, hipStream_t st) {
+    if (n == 0) return HK_OK;
+    if (is_bf16)
+        hipLaunchKernelGGL(embed_gather<bf16>, dim3(n), dim3(128), 0, st, ids, n, table, vocab, width, out, fault);
+    else
+        hipLaunchKernelGGL(embed_gather<float>, dim3(n), dim3(128), 0, st, ids, n, table, vocab, width, out, fault);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+extern "C" int hk_launch_final_norm_head(int is_bf16, const void* x, long x_tok, const int* cu, int n_seqs,
+                                         const float* w_eff, float eps, int width, const void* head_w,
+                                         const float* head_b, int n_out, float* logits, void* h_out, hipStream_t st) {
+    if (n_seqs == 0) return HK_OK;
+    if (is_bf16)
+        hipLaunchKernelGGL(final_norm_head<bf16>, dim3(n_seqs), dim3(64), 0, st, x, x_tok, cu, w_eff, eps, width,
+                           head_w, head_b, n_out, logits, h_out);
+    else
+        hipLaunchKernelGGL(final_norm_head<float>, dim3(n_seqs), dim3(64), 0, st, x, x_tok, cu, w_eff, eps, width,
+                           head_w, head_b, n_out, logits, h_out);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+namespace hk {
+__global__ void seq_lens_kernel(const int* cu, int n, int* out) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s < n) out[s] = cu[s + 1] - cu[s];
+}
+}  // namespace hk
+
+extern "C" int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st) {
+    if (n == 0) return HK_OK;
+    hipLaunchKernelGGL(hk::seq_lens_kernel, dim3((n + 255) / 256), dim3(256), 0, st, cu, n, out);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}

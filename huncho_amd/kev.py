@@ -1,0 +1,237 @@
+"""Kev/Qwen3.5 hybrid scoring model on libhuncho_rocm (host side, Python).
+
+Mirrors the parts of `Qwen3_5Backend` (crates/huncho-backend/src/qwen3_5.rs:2514-2935)
+that the scoring forward needs: weights under their checkpoint names
+(model.language_model.*, canonical_weight_name 2496-2512), a varlen native batch of
+independent rows (forward_batch / forward_independent_batch, 2759, 3138-3194; at most 64
+rows, backend.rs:107-119), validation before any work (2656-2725: vocabulary range,
+non-empty rows), and the calibrated decision readout (calibration.rs:170-173 through
+hk_calibrate). All numerics run in the C ABI; this module moves bytes and holds handles.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from concurrent.futures import ThreadPoolExecutor
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import abi
+from .abi import HK_BF16, HK_F32, KevConfig, KevLayerWeights
+
+PREFIX = "model.language_model."
+MAX_ROWS = 64  # BatchLimits { max_rows: 64 } (crates/huncho-core/src/backend.rs:107-119)
+
+
+@dataclass
+class KevShape:
+    """Architecture of a Kev-shaped Qwen3.5 hybrid model."""
+    hidden: int = 1024
+    n_layers: int = 24
+    n_heads: int = 16
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 3584
+    vocab: int = 151936
+    eps: float = 1e-6
+    rope_theta: float = 1e7
+    rotary_dim: int = 128
+    conv_k: int = 4
+    lin_key_dim: int = 128
+    lin_n_k_heads: int = 16
+    lin_n_v_heads: int = 16
+    lin_v_dim: int = 128
+    full_attention_interval: int = 4
+    page_size: int = 16
+    max_context: int = 8192
+    n_out: int = 8
+
+    @property
+    def layer_types(self):
+        # qwen3_5.rs:103-116: full attention at (i + 1) % interval == 0
+        return [1 if (i + 1) % self.full_attention_interval == 0 else 0 for i in range(self.n_layers)]
+
+    @property
+    def conv_dim(self):
+        return 2 * self.lin_n_k_heads * self.lin_key_dim + self.lin_n_v_heads * self.lin_v_dim
+
+    def weight_shapes(self) -> dict:
+        """Checkpoint tensor name -> shape, plus `decision_head.weight` [n_out, hidden]."""
+        H, I = self.hidden, self.intermediate
+        vd = self.lin_n_v_heads * self.lin_v_dim
+        shapes = {PREFIX + "embed_tokens.weight": (self.vocab, H), PREFIX + "norm.weight": (H,)}
+        for i, t in enumerate(self.layer_types):
+            p = f"{PREFIX}layers.{i}."
+            shapes.update({p + "input_layernorm.weight": (H,), p + "post_attention_layernorm.weight": (H,),
+                           p + "mlp.gate_proj.weight": (I, H), p + "mlp.up_proj.weight": (I, H),
+                           p + "mlp.down_proj.weight": (H, I)})
+            if t == 0:
+                la = p + "linear_attn."
+                shapes.update({la + "in_proj_qkv.weight": (self.conv_dim, H), la + "in_proj_z.weight": (vd, H),
+                               la + "in_proj_b.weight": (self.lin_n_v_heads, H),
+                               la + "in_proj_a.weight": (self.lin_n_v_heads, H), la + "out_proj.weight": (H, vd),
+                               la + "conv1d.weight": (self.conv_dim, 1, self.conv_k),
+                               la + "norm.weight": (self.lin_v_dim,), la + "A_log": (self.lin_n_v_heads,),
+                               la + "dt_bias": (self.lin_n_v_heads,)})
+            else:
+                sa = p + "self_attn."
+                d = self.head_dim
+                shapes.update({sa + "q_proj.weight": (2 * self.n_heads * d, H),
+                               sa + "k_proj.weight": (self.n_kv_heads * d, H),
+                               sa + "v_proj.weight": (self.n_kv_heads * d, H),
+                               sa + "o_proj.weight": (H, self.n_heads * d), sa + "q_norm.weight": (d,),
+                               sa + "k_norm.weight": (d,)})
+        if self.n_out:
+            shapes["decision_head.weight"] = (self.n_out, H)
+        return shapes
+
+
+def synthetic_weights(shape: KevShape, seed: int, std: float = 0.02, threads: int = 8) -> dict:
+    """Every tensor N(0, std) as bf16 bit patterns (uint16), one seeded stream per tensor in
+    sorted-name order (hk_synth_normal_bf16)."""
+    shapes = shape.weight_shapes()
+    names = sorted(shapes)
+
+    def make(item):
+        idx, name = item
+        n = int(np.prod(shapes[name]))
+        return name, abi.synth_normal_bf16(seed, 1000 + idx, n, 0.0, std).reshape(shapes[name])
+
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        return dict(ex.map(make, enumerate(names)))
+
+
+_LAYER_NAME = {
+    "input_norm": "input_layernorm.weight", "post_norm": "post_attention_layernorm.weight",
+    "gate_proj": "mlp.gate_proj.weight", "up_proj": "mlp.up_proj.weight", "down_proj": "mlp.down_proj.weight",
+    "in_qkv": "linear_attn.in_proj_qkv.weight", "in_z": "linear_attn.in_proj_z.weight",
+    "in_b": "linear_attn.in_proj_b.weight", "in_a": "linear_attn.in_proj_a.weight",
+    "out_proj": "linear_attn.out_proj.weight", "conv_w": "linear_attn.conv1d.weight",
+    "norm_w": "linear_attn.norm.weight", "a_log": "linear_attn.A_log", "dt_bias": "linear_attn.dt_bias",
+    "q_proj": "self_attn.q_proj.weight", "k_proj": "self_attn.k_proj.weight", "v_proj": "self_attn.v_proj.weight",
+    "o_proj": "self_attn.o_proj.weight", "q_norm": "self_attn.q_norm.weight", "k_norm": "self_attn.k_norm.weight",
+}
+
+
+def _to_device(a: np.ndarray, dtype: torch.dtype, device) -> torch.Tensor:
+    if a.dtype == np.uint16:
+        t = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+        if dtype == torch.float32:
+            t = t.float()
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(a, np.float32))
+        if dtype == torch.bfloat16:
+            t = t.to(torch.bfloat16)
+    return t.to(device).contiguous()
+
+
+class KevModel:
+    """hk_kev_model plus its workspace, for varlen batches of independent rows."""
+
+    def __init__(self, ctx: abi.Context, shape: KevShape, weights: dict, dtype: torch.dtype = torch.bfloat16,
+                 device=0):
+        self.ctx, self.shape, self.dtype = ctx, shape, dtype
+        self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        self.hk_dtype = HK_BF16 if dtype == torch.bfloat16 else HK_F32
+        staged = {k: _to_device(v, dtype, self.device) for k, v in weights.items()}
+        lts = (C.c_int32 * shape.n_layers)(*shape.layer_types)
+        cfg = KevConfig(shape.hidden, shape.n_layers, shape.n_heads, shape.n_kv_heads, shape.head_dim,
+                        shape.intermediate, shape.vocab, shape.eps, shape.rope_theta, shape.rotary_dim,
+                        shape.conv_k, shape.lin_key_dim, shape.lin_n_k_heads, shape.lin_n_v_heads,
+                        shape.lin_v_dim, shape.page_size, shape.max_context, shape.n_out,
+                        C.cast(lts, C.POINTER(C.c_int32)))
+        layers = (KevLayerWeights * shape.n_layers)()
+        for i in range(shape.n_layers):
+            for f, suffix in _LAYER_NAME.items():
+                t = staged.get(f"{PREFIX}layers.{i}.{suffix}")
+                if t is not None:
+                    setattr(layers[i], f, t.data_ptr())
+        head = staged.get("decision_head.weight")
+        h = C.c_void_p()
+        torch.cuda.synchronize(self.device)
+        ctx.check(abi.lib().hk_kev_model_create(
+            ctx.h, self.hk_dtype, C.byref(cfg), layers, staged[PREFIX + "embed_tokens.weight"].data_ptr(),
+            staged[PREFIX + "norm.weight"].data_ptr(), head.data_ptr() if head is not None else None, None,
+            C.byref(h)))
+        self.h = h
+        del staged  # the model holds its own fused copies
+        self._ws = None
+        self._ws_key = None
+
+    def close(self):
+        if getattr(self, "h", None):
+            abi.lib().hk_kev_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def workspace_bytes(self, n_tokens: int, n_seqs: int) -> int:
+        b = C.c_size_t()
+        self.ctx.check(abi.lib().hk_kev_workspace_size(self.h, n_tokens, n_seqs, C.byref(b)))
+        return b.value
+
+    def prepare(self, lengths, block_tables=None, seed: int = 0):
+        """Device-side batch metadata for row lengths: cu_seqlens (device + host) and block
+        tables (a seeded permutation of the pool pages when not given) and the workspace."""
+        P = self.shape.page_size
+        lengths = [int(x) for x in lengths]
+        if not 1 <= len(lengths) <= MAX_ROWS:
+            raise ValueError(f"batch of {len(lengths)} rows; 1..{MAX_ROWS} are accepted")
+        if min(lengths) <= 0:
+            raise ValueError("rows must be non-empty")
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        pages = [(L + P - 1) // P for L in lengths]
+        num_pages = int(sum(pages))
+        bt_stride = max(pages)
+        if block_tables is None:
+            perm = abi.synth_permutation(seed, 77, num_pages)
+            block_tables = np.full((len(lengths), bt_stride), -1, np.int32)
+            k = 0
+            for s, n in enumerate(pages):
+                block_tables[s, :n] = perm[k:k + n]
+                k += n
+        n = int(cu[-1])
+        need = self.workspace_bytes(n, len(lengths))
+        key = (n, len(lengths))
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+        batch = {
+            "cu_host": cu,
+            "cu": torch.from_numpy(cu).to(self.device),
+            "bt": torch.from_numpy(np.ascontiguousarray(block_tables, np.int32)).to(self.device),
+            "num_pages": int(max(num_pages, int(np.max(block_tables)) + 1)),
+            "n_tokens": n,
+            "logits": torch.empty((len(lengths), max(self.shape.n_out, 1)), dtype=torch.float32, device=self.device),
+            "hidden": torch.empty((len(lengths), self.shape.hidden), dtype=self.dtype, device=self.device),
+        }
+        return batch
+
+    def forward_ids(self, ids: torch.Tensor, batch: dict, want_hidden: bool = False):
+        """Runs the forward on device ids [n_tokens] (int32); returns device logits."""
+        cu_host = batch["cu_host"]
+        self.ctx.check(abi.lib().hk_kev_forward(
+            self.h, ids.data_ptr(), batch["cu"].data_ptr(), cu_host.ctypes.data_as(C.POINTER(C.c_int32)),
+            len(cu_host) - 1, batch["bt"].data_ptr(), batch["bt"].shape[1], batch["num_pages"],
+            self._ws.data_ptr(), self._ws.numel(), batch["logits"].data_ptr(),
+            batch["hidden"].data_ptr() if want_hidden else None))
+        return batch["logits"]
+
+    def forward_batch(self, rows, temperature: float = 1.0):
+        """Independent token rows -> (raw decision logits [rows, n_out], calibrated
+        probabilities). Rejects out-of-vocabulary ids before any work (qwen3_5.rs:2669-2678)."""
+        flat = np.concatenate([np.asarray(r, np.int64) for r in rows])
+        if flat.size and (flat.min() < 0 or flat.max() >= self.shape.vocab):
+            raise ValueError("token id outside the vocabulary")
+        batch = self.prepare([len(r) for r in rows])
+        ids = torch.from_numpy(flat.astype(np.int32)).to(self.device)
+        logits = self.forward_ids(ids, batch).cpu().numpy()
+        faults = self.ctx.take_faults()
+        if faults:
+            raise abi.HkError(abi.HK_ERR_INVALID, f"device fault flags {faults:#x}")
+        probs = np.stack([abi.calibrate(row, temperature) for row in logits])
+        return logits, probs

@@ -1,0 +1,150 @@
+"""torch-tensor entry points over the C ABI (device memory and streams come from torch;
+every computation runs in libhuncho_rocm).
+
+Each function validates tensor dtypes/devices/shapes, passes raw pointers and strides to
+the corresponding hk_* symbol on the context's stream, and raises HkError on failure.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import abi
+from .abi import HK_BF16, HK_F32, Context
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return HK_BF16
+    if t.dtype == torch.float32:
+        return HK_F32
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("tensors must live on the GPU")
+
+
+def context_for_torch(device: int = 0) -> Context:
+    """A context that runs on torch's current stream, so torch and library work stay ordered."""
+    ctx = Context(device)
+    ctx.set_stream(torch.cuda.current_stream(device).cuda_stream)
+    return ctx
+
+
+def paged_kv_write(ctx: Context, k, v, cu_seqlens, context_lens, block_tables, k_pool, v_pool):
+    """k, v [tokens, Hkv, d] -> pools [pages, Hkv, P, d] through block tables [n_seqs, bt_stride]."""
+    _dev(k, v, cu_seqlens, context_lens, block_tables, k_pool, v_pool)
+    assert k.is_contiguous() and v.is_contiguous() and k_pool.is_contiguous() and v_pool.is_contiguous()
+    n_seqs = cu_seqlens.numel() - 1
+    ctx.check(abi.lib().hk_paged_kv_write(ctx.h, _dt(k), _p(k), _p(v), _p(cu_seqlens), _p(context_lens), n_seqs,
+                                          k.shape[0], _p(block_tables), block_tables.shape[1], k_pool.shape[0],
+                                          k_pool.shape[2], k.shape[1], k.shape[2], _p(k_pool), _p(v_pool)))
+
+
+def qk_norm_rope_kv_write(ctx: Context, q_in, k_in, v_in, q_norm_eff, k_norm_eff, eps, rope_cos, rope_sin,
+                          rotary_dim, cu_seqlens, context_lens, block_tables, k_pool, v_pool, q_out):
+    """q_in/q_out [tokens, Hq, d] (any token/head strides, may alias); k_in, v_in [tokens, Hkv, d]
+    with unit head stride d. Norm weights (1 + w, fp32) and rope tables may be None."""
+    _dev(q_in, k_in, v_in, cu_seqlens, context_lens, block_tables, k_pool, v_pool, q_out)
+    assert k_in.stride(1) == k_in.shape[2] and v_in.stride(1) == v_in.shape[2] and k_in.stride(2) == 1
+    n_seqs = cu_seqlens.numel() - 1
+    max_pos = rope_cos.shape[0] if rope_cos is not None else 0
+    ctx.check(abi.lib().hk_qk_norm_rope_kv_write(
+        ctx.h, _dt(q_in), _p(q_in), q_in.stride(0), q_in.stride(1), _p(k_in), k_in.stride(0), _p(v_in),
+        v_in.stride(0), _p(q_norm_eff), _p(k_norm_eff), eps, _p(rope_cos), _p(rope_sin), rotary_dim, max_pos,
+        _p(cu_seqlens), _p(context_lens), n_seqs, q_in.shape[0], _p(block_tables), block_tables.shape[1],
+        k_pool.shape[0], k_pool.shape[2], q_in.shape[1], k_in.shape[1], q_in.shape[2], _p(q_out), q_out.stride(0),
+        q_out.stride(1), _p(k_pool), _p(v_pool)))
+
+
+def paged_prefill_attention(ctx: Context, q, k_pool, v_pool, block_tables, cu_seqlens_q, context_lens, max_q_len,
+                            scale=None, gate=None, out=None):
+    """q [tokens, Hq, d] (strided); pools [pages, Hkv, P, d]; returns o [tokens, Hq, d]."""
+    _dev(q, k_pool, v_pool, block_tables, cu_seqlens_q, context_lens, gate, out)
+    tokens, hq, d = q.shape
+    if out is None:
+        out = torch.empty((tokens, hq, d), dtype=q.dtype, device=q.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    assert q.stride(2) == 1 and out.stride(2) == 1 and (gate is None or gate.stride(2) == 1)
+    n_seqs = cu_seqlens_q.numel() - 1
+    ctx.check(abi.lib().hk_paged_prefill_attention(
+        ctx.h, _dt(q), _p(q), q.stride(0), q.stride(1), _p(k_pool), _p(v_pool), k_pool.shape[0], k_pool.shape[2],
+        _p(block_tables), block_tables.shape[1], _p(cu_seqlens_q), _p(context_lens), n_seqs, tokens, int(max_q_len),
+        hq, k_pool.shape[1], d, float(scale), _p(gate), gate.stride(0) if gate is not None else 0,
+        gate.stride(1) if gate is not None else 0, _p(out), out.stride(0), out.stride(1)))
+    return out
+
+
+def gated_delta_chunked(ctx: Context, q, k, v, g, beta, cu_seqlens, initial_state=None, final_state=None, out=None):
+    """q,k [tokens, Hk, 128]; v [tokens, H, 128]; g, beta fp32 [tokens, H]; states fp32
+    [n_seqs, H, 128, 128]. Returns o [tokens, H, 128]."""
+    _dev(q, k, v, g, beta, cu_seqlens, initial_state, final_state, out)
+    tokens, hk, dk = q.shape
+    h, dv = v.shape[1], v.shape[2]
+    assert g.dtype == torch.float32 and beta.dtype == torch.float32 and g.is_contiguous() and beta.is_contiguous()
+    if out is None:
+        out = torch.empty((tokens, h, dv), dtype=v.dtype, device=v.device)
+    n_seqs = cu_seqlens.numel() - 1
+    ctx.check(abi.lib().hk_gated_delta_chunked(
+        ctx.h, _dt(q), _p(q), q.stride(0), _p(k), k.stride(0), _p(v), v.stride(0), _p(g), _p(beta), _p(cu_seqlens),
+        n_seqs, tokens, h, hk, dk, dv, _p(initial_state), _p(final_state), _p(out), out.stride(0)))
+    return out
+
+
+def gdn_prep(ctx: Context, mixed, conv_w, ba, b_col, a_col, base_g, dt_bias, cu_seqlens, heads, k_heads,
+             conv_hist=None, want_tail=False):
+    """mixed [tokens, >= conv_dim] (q|k|v channels first); returns q, k, v, g, beta (, tail)."""
+    _dev(mixed, conv_w, ba, base_g, dt_bias, cu_seqlens, conv_hist)
+    tokens = mixed.shape[0]
+    dt = mixed.dtype
+    dev = mixed.device
+    n_seqs = cu_seqlens.numel() - 1
+    K = conv_w.shape[1]
+    conv_dim = (2 * k_heads + heads) * 128
+    q = torch.empty((tokens, k_heads, 128), dtype=dt, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty((tokens, heads, 128), dtype=dt, device=dev)
+    g = torch.empty((tokens, heads), dtype=torch.float32, device=dev)
+    beta = torch.empty_like(g)
+    tail = torch.empty((n_seqs, conv_dim, K - 1), dtype=dt, device=dev) if want_tail else None
+    ctx.check(abi.lib().hk_gdn_prep(
+        ctx.h, _dt(mixed), _p(mixed), mixed.stride(0), _p(conv_w), K, _p(conv_hist), _p(ba), ba.stride(0), b_col,
+        a_col, _p(base_g), _p(dt_bias), _p(cu_seqlens), n_seqs, tokens, heads, k_heads, _p(q), _p(k), _p(v), _p(g),
+        _p(beta), _p(tail)))
+    return (q, k, v, g, beta, tail) if want_tail else (q, k, v, g, beta)
+
+
+def rms_norm(ctx: Context, x, w_eff, eps, out=None):
+    _dev(x, w_eff, out)
+    rows, width = x.shape
+    out = torch.empty_like(x) if out is None else out
+    ctx.check(abi.lib().hk_rms_norm(ctx.h, _dt(x), _p(x), x.stride(0), _p(w_eff), eps, rows, width, _p(out),
+                                    out.stride(0)))
+    return out
+
+
+def gated_rms_norm(ctx: Context, x, z, w, eps, out=None):
+    """x [tokens, H, d] contiguous; z [tokens, >= H*d] (token-strided)."""
+    _dev(x, z, w, out)
+    tokens, heads, width = x.shape
+    out = torch.empty_like(x) if out is None else out
+    ctx.check(abi.lib().hk_gated_rms_norm(ctx.h, _dt(x), _p(x), _p(z), z.stride(0), heads, _p(w), eps,
+                                          tokens * heads, width, _p(out)))
+    return out
+
+
+def swiglu(ctx: Context, gu, width):
+    _dev(gu)
+    rows = gu.shape[0]
+    out = torch.empty((rows, width), dtype=gu.dtype, device=gu.device)
+    ctx.check(abi.lib().hk_swiglu(ctx.h, _dt(gu), _p(gu), gu.stride(0), width, rows, width, _p(out)))
+    return out

@@ -1,0 +1,227 @@
+/*
+ * huncho_rocm.h - C ABI of libhuncho_rocm, the MI355X (gfx950) implementation of Huncho's
+ * Kev/Qwen3.5 scoring-forward (prefill) path.
+ *
+ * The reference boundary is the Rust `huncho_core::backend::Backend` trait
+ * (crates/huncho-core/src/backend.rs:213-438) implemented for Kev by `Qwen3_5Backend`
+ * (crates/huncho-backend/src/qwen3_5.rs:2514-2935). A thin Rust FFI crate binds this header
+ * and keeps that trait's contract (see INTEGRATION.md in the repository). Each entry point
+ * below names the reference function whose numerics it replaces.
+ *
+ * Conventions
+ *   - Every pointer argument named *_dev is device memory owned by the caller; nothing is
+ *     retained after the call returns. Host pointers are named *_host.
+ *   - All work is stream-ordered on the context's stream (hk_ctx_set_stream), so calls
+ *     return before the GPU finishes; hk_ctx_synchronize waits.
+ *   - Returns HK_OK (0) or an error code; hk_ctx_last_error() gives the message. Shapes,
+ *     strides and dtypes are validated before any launch. Data-dependent faults found on
+ *     the device (block-table entry or token id out of range, malformed cu_seqlens) skip
+ *     the offending writes and set the context's fault flag, read and cleared by
+ *     hk_ctx_take_faults (no partial cache commit: the caller commits only after a clean
+ *     forward, as qwen3_5.rs:2747-2751 does).
+ *   - Activations are token-major: [tokens][heads][head_dim]; varlen batches are
+ *     delimited by cu_seqlens (int32, n_seqs + 1 entries, cu[0] = 0).
+ *   - Paged KV pools are [num_pages][kv_heads][page_size][head_dim]: one pool page holds
+ *     what one reference Page holds ([1, Hkv, rows, d], qwen3_5/kv_pages.rs:18-22). Token j
+ *     of sequence s lives in page block_tables[s * bt_stride + j / page_size], slot
+ *     j % page_size. page_size is a power of two in 16..256 (qwen3_5.rs parsers,
+ *     huncho-cli/src/load.rs:679-747).
+ *   - A context is used by one thread at a time (the engine serialises calls per model,
+ *     crates/huncho-core/src/engine.rs:175-178); distinct contexts are independent.
+ */
+#ifndef HUNCHO_ROCM_H
+#define HUNCHO_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HK_OK 0
+#define HK_ERR_INVALID 1     /* bad argument, shape or stride  -> Error::Backend / Request */
+#define HK_ERR_UNSUPPORTED 2 /* shape or dtype this build does not implement -> Error::Unsupported */
+#define HK_ERR_DEVICE 3      /* HIP runtime / launch failure -> Error::Backend */
+#define HK_ERR_NOMEM 4       /* allocation failed (context / model creation only) */
+
+#define HK_F32 0
+#define HK_BF16 1
+
+/* Device fault bits reported by hk_ctx_take_faults. */
+#define HK_FAULT_SEQLENS 1   /* cu_seqlens / context_lens inconsistent for a token */
+#define HK_FAULT_PAGE 2      /* block-table entry outside [0, num_pages) or past bt_stride */
+#define HK_FAULT_ROPE 4      /* position beyond the RoPE table */
+#define HK_FAULT_TOKEN 8     /* token id outside the vocabulary */
+
+typedef struct hk_ctx hk_ctx;
+
+typedef struct {
+    char name[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int compute_units;
+    int clock_khz;
+    int mem_clock_khz;
+    int mem_bus_width;
+    size_t total_mem;
+    size_t lds_per_block;
+    int l2_bytes;
+} hk_device_info_t;
+
+/* ---- context (replaces device selection, crates/huncho-backend/src/device.rs:12-72) ---- */
+/* Fails with HK_ERR_UNSUPPORTED when no GPU is visible (hipGetDeviceCount == 0). */
+int hk_ctx_create(int device_ordinal, hk_ctx** out);
+int hk_ctx_destroy(hk_ctx* ctx);
+/* Work is ordered on this hipStream_t from now on (NULL: HIP's null stream). A new
+ * context uses its own default-priority stream, returned by hk_ctx_own_stream. */
+int hk_ctx_set_stream(hk_ctx* ctx, void* hip_stream);
+void* hk_ctx_stream(hk_ctx* ctx);
+void* hk_ctx_own_stream(hk_ctx* ctx);
+int hk_ctx_synchronize(hk_ctx* ctx);
+const char* hk_ctx_last_error(hk_ctx* ctx);
+int hk_ctx_device_info(hk_ctx* ctx, hk_device_info_t* out);
+/* Synchronises, returns the OR of HK_FAULT_* bits raised since the last call, clears them. */
+int hk_ctx_take_faults(hk_ctx* ctx, int* faults_out);
+int hk_device_count(int* out);
+const char* hk_version(void);
+
+/* ---- RoPE tables (qwen3_5.rs:220-247: inv_freq = theta^(-2i/rd) in f32, cos/sin of
+ * pos * inv_freq in f32, cast to the model dtype when round_bf16) -------------------------
+ * Host-side helper: fills cos_host/sin_host [max_pos][rd/2] for upload. */
+int hk_rope_fill_table(int rotary_dim, double theta, int max_pos, int round_bf16, float* cos_host,
+                       float* sin_host);
+
+/* ---- fused q/k norm + partial RoPE + paged KV append -------------------------------------
+ * Replaces qwen3_5.rs:596-624 (q/gate split, q_norm/k_norm, apply_partial_rotary, page
+ * append) and kv_pages.rs:307-341. New token i of sequence s has absolute position
+ * context_lens[s] - q_len(s) + i. q_norm_eff/k_norm_eff are (1 + w) in fp32, or NULL to
+ * skip the norm; rope_cos/rope_sin NULL skips RoPE. head_dim must be 128. q_out may alias
+ * q_in (the q half of the fused projection is rotated in place). */
+int hk_qk_norm_rope_kv_write(hk_ctx* ctx, int dtype, const void* q_in_dev, long q_in_tok, long q_in_head,
+                             const void* k_in_dev, long k_in_tok, const void* v_in_dev, long v_in_tok,
+                             const float* q_norm_eff_dev, const float* k_norm_eff_dev, float eps,
+                             const float* rope_cos_dev, const float* rope_sin_dev, int rotary_dim,
+                             int rope_max_pos, const int32_t* cu_seqlens_q_dev, const int32_t* context_lens_dev,
+                             int n_seqs, int n_tokens, const int32_t* block_tables_dev, int bt_stride,
+                             int num_pages, int page_size, int q_heads, int kv_heads, int head_dim,
+                             void* q_out_dev, long q_out_tok, long q_out_head, void* k_pool_dev,
+                             void* v_pool_dev);
+
+/* ---- paged KV append only (kv_pages.rs:307-341): k/v [n_tokens][kv_heads][head_dim] ---- */
+int hk_paged_kv_write(hk_ctx* ctx, int dtype, const void* k_dev, const void* v_dev,
+                      const int32_t* cu_seqlens_q_dev, const int32_t* context_lens_dev, int n_seqs,
+                      int n_tokens, const int32_t* block_tables_dev, int bt_stride, int num_pages,
+                      int page_size, int kv_heads, int head_dim, void* k_pool_dev, void* v_pool_dev);
+
+/* ---- paged GQA causal prefill attention ----------------------------------------------------
+ * Replaces the attention core of Attention::forward (qwen3_5.rs:626-703), grouped GQA and
+ * query blocks (qwen3_5/attention.rs:6-111) and direct page attention
+ * (qwen3_5/kv_pages.rs:104-174): O = softmax(Q K^T * scale + causal) V with query head h
+ * reading KV head h / (q_heads / kv_heads). Sequence s has q_len(s) new queries at
+ * positions context_lens[s] - q_len(s) .. context_lens[s] - 1 and keys 0..pos through its
+ * block table. max_q_len bounds q_len over the batch. gate_dev (optional) applies
+ * o *= sigmoid(gate) (qwen3_5.rs:706-714). head_dim 128; q_heads / kv_heads in {1,2,4,8}.
+ * dtype HK_F32: fp32 everywhere; HK_BF16: bf16 in/out, fp32 accumulation and softmax. */
+int hk_paged_prefill_attention(hk_ctx* ctx, int dtype, const void* q_dev, long q_tok, long q_head,
+                               const void* k_pool_dev, const void* v_pool_dev, int num_pages, int page_size,
+                               const int32_t* block_tables_dev, int bt_stride, const int32_t* cu_seqlens_q_dev,
+                               const int32_t* context_lens_dev, int n_seqs, int n_tokens, int max_q_len,
+                               int q_heads, int kv_heads, int head_dim, float scale, const void* gate_dev,
+                               long gate_tok, long gate_head, void* o_dev, long o_tok, long o_head);
+
+/* ---- chunked gated delta rule ------------------------------------------------------------------
+ * Replaces recurrent_gated_delta (qwen3_5.rs:950-987) / delta_cpu::recurrent
+ * (delta_cpu.rs:29-138) with an equal chunked (C = 64) algorithm. q,k [tokens][k_heads][128]
+ * (token strides q_tok/k_tok), v [tokens][heads][128], g/beta fp32 [tokens][heads],
+ * value head h reads key head h / (heads / k_heads). initial_state (optional, fp32
+ * [n_seqs][heads][128][128], the carried cache state) and final_state (optional, same
+ * shape) may alias. o [tokens][heads][128] with token stride o_tok. */
+int hk_gated_delta_chunked(hk_ctx* ctx, int dtype, const void* q_dev, long q_tok, const void* k_dev, long k_tok,
+                           const void* v_dev, long v_tok, const float* g_dev, const float* beta_dev,
+                           const int32_t* cu_seqlens_dev, int n_seqs, int n_tokens, int heads, int k_heads,
+                           int dk, int dv, const float* initial_state_dev, float* final_state_dev, void* o_dev,
+                           long o_tok);
+
+/* ---- GDN input prep -----------------------------------------------------------------------------
+ * Replaces LinearAttn::forward up to the recurrence (qwen3_5.rs:846-925): causal depthwise
+ * conv (conv_w [conv_dim][K] fp32, ascending taps, conv_cpu.rs:34-48) + SiLU over the
+ * q|k|v channels of `mixed` (token stride mixed_tok), with the cached conv tail
+ * (conv_hist, [n_seqs][conv_dim][K-1], optional) prepended; l2norm of q and k per head,
+ * q * dk^-1/2; beta = sigmoid(b); g = base_g * softplus(a + dt_bias) with
+ * base_g = -exp(A_log). b and a are read at columns b_col/a_col of `ba` rows. Outputs
+ * q,k [tokens][k_heads][128], v [tokens][heads][128], g/beta fp32 [tokens][heads], and the
+ * new conv tail (optional). conv_dim = (2 * k_heads + heads) * 128. */
+int hk_gdn_prep(hk_ctx* ctx, int dtype, const void* mixed_dev, long mixed_tok, const float* conv_w_dev, int conv_k,
+                const void* conv_hist_dev, const void* ba_dev, long ba_tok, int b_col, int a_col,
+                const float* base_g_dev, const float* dt_bias_dev, const int32_t* cu_seqlens_dev, int n_seqs,
+                int n_tokens, int heads, int k_heads, void* q_out_dev, void* k_out_dev, void* v_out_dev,
+                float* g_out_dev, float* beta_out_dev, void* conv_tail_out_dev);
+
+/* ---- norms and gates (qwen3_5.rs:184-201, 1020-1031) -------------------------------------------- */
+int hk_rms_norm(hk_ctx* ctx, int dtype, const void* x_dev, long x_tok, const float* w_eff_dev, float eps, int rows,
+                int width, void* y_dev, long y_tok);
+int hk_gated_rms_norm(hk_ctx* ctx, int dtype, const void* x_dev, const void* z_dev, long z_tok, int heads,
+                      const float* w_dev, float eps, int rows, int width, void* y_dev);
+int hk_swiglu(hk_ctx* ctx, int dtype, const void* gu_dev, long gu_tok, long up_off, int rows, int width, void* y_dev);
+
+/* ---- Kev-shaped hybrid model (qwen3_5.rs:1283-1553 forward; Backend::forward_batch,
+ * qwen3_5.rs:3138-3194) -------------------------------------------------------------------------------*/
+typedef struct {
+    int hidden, n_layers, n_heads, n_kv_heads, head_dim, intermediate, vocab;
+    float eps;
+    double rope_theta;
+    int rotary_dim;
+    int conv_k, lin_key_dim, lin_n_k_heads, lin_n_v_heads, lin_v_dim;
+    int page_size;          /* KV pool page (power of two 16..256) */
+    int max_context;        /* longest sequence the model accepts (RoPE table size) */
+    int n_out;              /* decision-head outputs (0 = no head) */
+    const int32_t* layer_types_host; /* per layer: 0 = Gated DeltaNet, 1 = full attention */
+} hk_kev_config;
+
+/* Per-layer weights, device memory in the model dtype unless noted, PyTorch [out][in]
+ * layout. Norm weights are the raw checkpoint values (the model bakes 1 + w itself). */
+typedef struct {
+    const void *input_norm, *post_norm;                 /* [hidden] */
+    const void *gate_proj, *up_proj, *down_proj;
+    const void *in_qkv, *in_z, *in_b, *in_a, *out_proj; /* linear attention */
+    const void *conv_w;                                 /* [conv_dim][1][K] */
+    const void *norm_w, *a_log, *dt_bias;
+    const void *q_proj, *k_proj, *v_proj, *o_proj;      /* full attention */
+    const void *q_norm, *k_norm;
+} hk_kev_layer_weights;
+
+typedef struct hk_kev_model hk_kev_model;
+
+/* Loads (copies and fuses) the weights; the caller's buffers may be freed afterwards.
+ * head_w [n_out][hidden] (model dtype), head_b [n_out] fp32 or NULL. */
+int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* cfg, const hk_kev_layer_weights* layers_host,
+                        const void* embed_dev, const void* final_norm_dev, const void* head_w_dev,
+                        const float* head_b_dev, hk_kev_model** out);
+int hk_kev_model_destroy(hk_kev_model* m);
+/* Workspace bytes for a forward over n_tokens tokens in n_seqs sequences. */
+int hk_kev_workspace_size(hk_kev_model* m, int n_tokens, int n_seqs, size_t* bytes_out);
+/* Full scoring forward of a fresh (uncached) varlen batch: ids [n_tokens], cu_seqlens
+ * [n_seqs + 1] on device and on host (the host copy sizes the launch grids). Writes the
+ * decision logits [n_seqs][n_out] fp32 and, if hidden_last_dev != NULL, the final-normed
+ * last-token hidden rows [n_seqs][hidden]. Page assignment: sequence s uses pool pages
+ * block_tables_dev[s * bt_stride ...]; the pools live in the workspace. */
+int hk_kev_forward(hk_kev_model* m, const int32_t* ids_dev, const int32_t* cu_seqlens_dev,
+                   const int32_t* cu_seqlens_host, int n_seqs, const int32_t* block_tables_dev, int bt_stride,
+                   int num_pages, void* workspace_dev, size_t workspace_bytes, float* logits_dev,
+                   void* hidden_last_dev);
+
+/* ---- calibration (crates/huncho-core/src/calibration.rs:42-60, 170-173) --------------------------
+ * Host-side: fp32 exp((x - max) / T), fp64 ordered sum and divide, fp32 result. Returns
+ * HK_ERR_INVALID for a non-finite logit or a non-positive / non-finite temperature. */
+int hk_calibrate(const float* logits_host, int n, float temperature, float* probs_host);
+
+/* ---- synthetic inputs (seeded, host-side; identical streams to the test oracle) -------------
+ * splitmix64 -> two 24-bit uniforms per draw -> Box-Muller in double precision. */
+int hk_synth_normal(uint64_t seed, uint64_t stream, float* out_host, size_t n, float mean, float std);
+int hk_synth_normal_bf16(uint64_t seed, uint64_t stream, uint16_t* out_host, size_t n, float mean, float std);
+int hk_synth_uniform_int(uint64_t seed, uint64_t stream, int32_t* out_host, size_t n, int32_t lo, int32_t hi);
+int hk_synth_permutation(uint64_t seed, uint64_t stream, int32_t* out_host, int32_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -196,9 +196,10 @@ void ho_rope_cos_sin(int rd, double theta, const int32_t* positions, int n, int 
     }
 }
 
-/* qwen3_5.rs:249-283: x_rot*cos + rotate_half(x_rot)*sin on the first rd dims. */
+/* qwen3_5.rs:249-283: x_rot*cos + rotate_half(x_rot)*sin on the first rd dims; in bf16 mode
+ * the two products and the sum are each rounded (three bf16 tensor ops). */
 void ho_apply_rope(float* x, int n, int heads, int head_dim, int rd, const float* cos_t,
-                   const float* sin_t) {
+                   const float* sin_t, int bf16_mode) {
     int half = rd / 2;
     float tmp[1024];
     for (int t = 0; t < n; ++t)
@@ -210,7 +211,13 @@ void ho_apply_rope(float* x, int n, int heads, int head_dim, int rd, const float
                 float rot = i < half ? -xh[i + half] : xh[i - half];
                 float a = xh[i] * c[i];
                 float b = rot * s[i];
-                tmp[i] = a + b;
+                if (bf16_mode) { /* each bf16 tensor op rounds: mul, mul, add */
+                    a = rb(a);
+                    b = rb(b);
+                    tmp[i] = rb(a + b);
+                } else {
+                    tmp[i] = a + b;
+                }
             }
             for (int i = 0; i < rd; ++i) xh[i] = tmp[i];
         }
@@ -478,10 +485,8 @@ static void full_attention(const ho_qwen_cfg* c, const ho_qwen_layer* L, const f
     round_if(vv, (size_t)T * Hkv * d, bf);
     for (int t = 0; t < T; ++t) pos[t] = t;
     ho_rope_cos_sin(c->rotary_dim, c->rope_theta, pos, T, bf, cs, sn);
-    ho_apply_rope(q, T, Hq, d, c->rotary_dim, cs, sn);
-    round_if(q, (size_t)T * Hq * d, bf);
-    ho_apply_rope(kk, T, Hkv, d, c->rotary_dim, cs, sn);
-    round_if(kk, (size_t)T * Hkv * d, bf);
+    ho_apply_rope(q, T, Hq, d, c->rotary_dim, cs, sn, bf);
+    ho_apply_rope(kk, T, Hkv, d, c->rotary_dim, cs, sn, bf);
     /* Dense causal softmax attention: one page of T rows ([Hkv][T][d]) with table {0}
      * is exactly the materialized K/V of the reference's default path. */
     int32_t cu[2] = {0, T}, ctx[1] = {T}, table[1] = {0};

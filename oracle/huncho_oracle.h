@@ -54,9 +54,10 @@ int ho_rotary_dim(int head_dim, double partial_rotary_factor);
 /* cos/sin tables [n][rd] for absolute positions; bf16_mode rounds them (qwen3_5.rs:243-244) */
 void ho_rope_cos_sin(int rd, double theta, const int32_t* positions, int n, int bf16_mode,
                      float* cos_out, float* sin_out);
-/* x [n][heads][head_dim] in place; rotates the first rd dims of every head (NeoX halves). */
+/* x [n][heads][head_dim] in place; rotates the first rd dims of every head (NeoX halves);
+ * bf16_mode rounds each product and the sum. */
 void ho_apply_rope(float* x, int n, int heads, int head_dim, int rd, const float* cos_t,
-                   const float* sin_t);
+                   const float* sin_t, int bf16_mode);
 
 /* ---- paged KV, kv_pages.rs:63-98 and :307-341 ----------------------------
  * Pool layout [num_pages][kv_heads][page_size][head_dim] (one reference Page per

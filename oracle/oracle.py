@@ -49,7 +49,7 @@ def lib() -> C.CDLL:
         L.ho_rotary_dim.restype = C.c_int
         L.ho_rotary_dim.argtypes = [C.c_int, C.c_double]
         L.ho_rope_cos_sin.argtypes = [C.c_int, C.c_double, _i32p, C.c_int, C.c_int, _f32p, _f32p]
-        L.ho_apply_rope.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, _f32p]
+        L.ho_apply_rope.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
         L.ho_paged_kv_write.restype = C.c_int
         L.ho_paged_kv_write.argtypes = [C.c_void_p, C.c_void_p, C.c_int, _i32p, _i32p, C.c_int, C.c_int,
                                         C.c_int, C.c_int, _i32p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
@@ -175,11 +175,11 @@ def rope_cos_sin(rd, theta, positions, bf16_mode=False):
     return c, s
 
 
-def apply_rope(x, rd, cos_t, sin_t):
-    """x [n, heads, d] -> rotated copy."""
+def apply_rope(x, rd, cos_t, sin_t, bf16_mode=False):
+    """x [n, heads, d] -> rotated copy (bf16_mode: per-op bf16 rounding)."""
     y = f32(x).copy()
     n, heads, d = y.shape
-    lib().ho_apply_rope(y, n, heads, d, rd, f32(cos_t), f32(sin_t))
+    lib().ho_apply_rope(y, n, heads, d, rd, f32(cos_t), f32(sin_t), int(bf16_mode))
     return y
 
 

@@ -1,0 +1,448 @@
+"""GPU parity of the hot-path kernels against the CPU oracle on identical seeded inputs.
+
+Tolerances (stated per test): paged KV writes and RoPE'd K pages are bit-exact; fp32
+attention / delta-rule outputs within 1e-4 relative (max error over max magnitude);
+bf16 outputs within 2e-2 relative.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from huncho_amd import abi
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20261201
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from huncho_amd.ops import context_for_torch
+
+    c = context_for_torch(0)
+    yield c
+    c.close()
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def cuda(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def bf16_dev(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def bits_of(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def block_tables_for(lengths, page_size, pool_pages, seed):
+    """Seeded page assignment: a permutation of the pool, sequence s taking the next pages."""
+    perm = abi.synth_permutation(seed, 11, pool_pages)
+    need = [(L + page_size - 1) // page_size for L in lengths]
+    assert sum(need) <= pool_pages
+    bt = np.full((len(lengths), max(need)), -1, np.int32)
+    k = 0
+    for s, n in enumerate(need):
+        bt[s, :n] = perm[k:k + n]
+        k += n
+    return bt
+
+
+# ---------------------------------------------------------------------------
+# paged KV write + RoPE
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("page_size", [16, 64, 256])
+def test_paged_kv_write_bit_exact(ctx, page_size):
+    from huncho_amd.ops import paged_kv_write
+
+    lengths = [1, 15, 16, 17, 300, page_size * 3 + 1]
+    hkv, d = 8, 128
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n = int(cu[-1])
+    pool = sum((L + page_size - 1) // page_size for L in lengths) + 5
+    bt = block_tables_for(lengths, page_size, pool, SEED)
+    k = abi.synth_normal_bf16(SEED, 1, n * hkv * d).reshape(n, hkv, d)
+    v = abi.synth_normal_bf16(SEED, 2, n * hkv * d).reshape(n, hkv, d)
+    kp_ref = np.full((pool, hkv, page_size, d), 0x7FC1, np.uint16)
+    vp_ref = kp_ref.copy()
+    O.paged_kv_write(k, v, cu, np.concatenate([np.arange(L) for L in lengths]), bt, page_size, kp_ref, vp_ref)
+    kp = bf16_dev(np.full_like(kp_ref, 0x7FC1))
+    vp = bf16_dev(np.full_like(vp_ref, 0x7FC1))
+    paged_kv_write(ctx, bf16_dev(k), bf16_dev(v), cuda(cu), cuda(np.array(lengths, np.int32)), cuda(bt), kp, vp)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits_of(kp), kp_ref)
+    assert np.array_equal(bits_of(vp), vp_ref)
+    assert ctx.take_faults() == 0
+
+
+def test_paged_kv_write_rejects_bad_page_without_writing(ctx):
+    from huncho_amd.ops import paged_kv_write
+
+    hkv, d, P = 8, 128, 16
+    k = torch.ones((20, hkv, d), dtype=torch.bfloat16, device="cuda")
+    kp = torch.zeros((2, hkv, P, d), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    bt = cuda(np.array([[0, 7]], np.int32))  # page 7 is outside a 2-page pool
+    paged_kv_write(ctx, k, k, cuda(np.array([0, 20], np.int32)), cuda(np.array([20], np.int32)), bt, kp, vp)
+    assert ctx.take_faults() & abi.HK_FAULT_PAGE
+    assert kp[1].abs().sum().item() == 0 and kp[0].abs().sum().item() == P * hkv * d
+    assert ctx.take_faults() == 0
+
+
+def test_qk_norm_rope_bf16_bit_exact(ctx):
+    """q_norm/k_norm + partial RoPE (rd = 64 of 128) + page write against the oracle's bf16 op sequence."""
+    from huncho_amd.ops import qk_norm_rope_kv_write
+
+    lengths = [37, 100]
+    hq, hkv, d, P, rd, theta = 16, 8, 128, 16, 64, 1e7
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n = int(cu[-1])
+    qkv = abi.synth_normal_bf16(SEED, 3, n * (2 * hq * d + 2 * hkv * d)).reshape(n, -1)
+    wq = O.round_bf16(abi.synth_normal(SEED, 4, d, 0.0, 0.1)) + np.float32(1.0)
+    wk = O.round_bf16(abi.synth_normal(SEED, 5, d, 0.0, 0.1)) + np.float32(1.0)
+    bt = block_tables_for(lengths, P, 20, SEED)
+    # oracle
+    f = O.bf16_to_f32(qkv)
+    pos = np.concatenate([np.arange(L) for L in lengths])
+    cs, sn = O.rope_cos_sin(rd, theta, pos, True)
+    q = f[:, : 2 * hq * d].reshape(n, hq, 2 * d)[:, :, :d]
+    kk = f[:, 2 * hq * d: 2 * hq * d + hkv * d].reshape(n, hkv, d)
+    vv = qkv[:, 2 * hq * d + hkv * d:].reshape(n, hkv, d)
+    qn = O.round_bf16(O.rms_norm_effective(q, wq, 1e-6))
+    kn = O.round_bf16(O.rms_norm_effective(kk, wk, 1e-6))
+    q_ref = O.apply_rope(qn, rd, cs, sn, True)
+    k_ref = O.apply_rope(kn, rd, cs, sn, True)
+    kp_ref = np.zeros((20, hkv, P, d), np.uint16)
+    vp_ref = kp_ref.copy()
+    O.paged_kv_write(O.bf16_bits(k_ref), np.ascontiguousarray(vv), cu, pos, bt, P, kp_ref, vp_ref)
+    # GPU, rotating q in place inside the fused projection buffer
+    buf = bf16_dev(qkv)
+    tc, ts = abi.rope_table(rd, theta, 256, True)
+    qin = buf[:, : 2 * hq * d].view(n, hq, 2 * d)[:, :, :d]
+    kin = buf[:, 2 * hq * d: 2 * hq * d + hkv * d].view(n, hkv, d)
+    vin = buf[:, 2 * hq * d + hkv * d:].view(n, hkv, d)
+    kp = torch.zeros((20, hkv, P, d), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    qk_norm_rope_kv_write(ctx, qin, kin, vin, cuda(wq), cuda(wk), 1e-6, cuda(tc), cuda(ts), rd, cuda(cu),
+                          cuda(np.array(lengths, np.int32)), cuda(bt), kp, vp, qin)
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    assert np.array_equal(bits_of(vp), vp_ref)
+    kd = O.bf16_to_f32(bits_of(kp)).astype(np.float64) - O.bf16_to_f32(kp_ref)
+    qd = O.bf16_to_f32(bits_of(qin)) - q_ref
+    # identical op sequence; the only freedom is the rms reduction order (<= 1 bf16 ulp, rarely)
+    assert np.mean(kd != 0) < 0.01 and np.abs(kd).max() <= 2 ** -7 * 4
+    assert np.mean(qd != 0) < 0.01 and np.abs(qd).max() <= 2 ** -7 * 4
+    # the gate half of every head is untouched
+    assert np.array_equal(bits_of(buf[:, : 2 * hq * d].view(n, hq, 2 * d)[:, :, d:]),
+                          qkv[:, : 2 * hq * d].reshape(n, hq, 2 * d)[:, :, d:])
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+def test_attention_fp32_gqa_causal_config(ctx):
+    """B=1, T=256, 16 query / 8 KV heads, d=128, RoPE theta 1e7 on Q/K, pages of 16 with an
+    identity block table, scale 1/sqrt(128): fp32 output within 1e-4 relative."""
+    from huncho_amd.ops import paged_prefill_attention, qk_norm_rope_kv_write
+
+    T, hq, hkv, d, P = 256, 16, 8, 128, 16
+    q = abi.synth_normal(SEED, 10, T * hq * d).reshape(T, hq, d)
+    k = abi.synth_normal(SEED, 11, T * hkv * d).reshape(T, hkv, d)
+    v = abi.synth_normal(SEED, 12, T * hkv * d).reshape(T, hkv, d)
+    pos = np.arange(T, dtype=np.int32)
+    cs, sn = O.rope_cos_sin(d, 1e7, pos)
+    qr, kr = O.apply_rope(q, d, cs, sn), O.apply_rope(k, d, cs, sn)
+    bt = np.arange(T // P, dtype=np.int32)[None]
+    kp_ref = np.zeros((T // P, hkv, P, d), np.float32)
+    vp_ref = np.zeros_like(kp_ref)
+    O.paged_kv_write(kr, v, [0, T], pos, bt, P, kp_ref, vp_ref)
+    o_ref = O.paged_attention(qr, kp_ref, vp_ref, bt, [0, T], [T], P, 1 / math.sqrt(d))
+
+    tc, ts = abi.rope_table(d, 1e7, T, False)
+    qd, kd, vd = cuda(q), cuda(k), cuda(v)
+    kp = torch.zeros((T // P, hkv, P, d), device="cuda")
+    vp = torch.zeros_like(kp)
+    cu, cl, btd = cuda(np.array([0, T], np.int32)), cuda(np.array([T], np.int32)), cuda(bt)
+    qrot = torch.empty_like(qd)
+    qk_norm_rope_kv_write(ctx, qd, kd, vd, None, None, 0.0, cuda(tc), cuda(ts), d, cu, cl, btd, kp, vp, qrot)
+    o = paged_prefill_attention(ctx, qrot, kp, vp, btd, cu, cl, T)
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    assert rel_err(qrot.cpu().numpy(), qr) < 1e-6
+    assert rel_err(kp.cpu().numpy(), kp_ref) < 1e-6
+    e = rel_err(o.cpu().numpy(), o_ref)
+    assert e < 1e-4, e
+
+
+def _varlen_bf16_case(n_seqs, lo, hi, seed, page_size=16, pool_pages=4096):
+    lengths = abi.synth_uniform_int(seed, 20, n_seqs, lo, hi).tolist()
+    hq, hkv, d = 16, 8, 128
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n = int(cu[-1])
+    bt = block_tables_for(lengths, page_size, pool_pages, seed)
+    q = abi.synth_normal_bf16(seed, 21, n * hq * d).reshape(n, hq, d)
+    k = abi.synth_normal_bf16(seed, 22, n * hkv * d).reshape(n, hkv, d)
+    v = abi.synth_normal_bf16(seed, 23, n * hkv * d).reshape(n, hkv, d)
+    return lengths, cu, bt, q, k, v
+
+
+def _gpu_rope_and_pages(ctx, lengths, cu, bt, q, k, v, page_size, pool_pages, theta=1e7):
+    from huncho_amd.ops import qk_norm_rope_kv_write
+
+    hkv, d = k.shape[1], k.shape[2]
+    tc, ts = abi.rope_table(d, theta, max(lengths), True)
+    qd = bf16_dev(q)
+    kp = torch.zeros((pool_pages, hkv, page_size, d), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    cud, cl, btd = cuda(cu), cuda(np.array(lengths, np.int32)), cuda(bt)
+    qk_norm_rope_kv_write(ctx, qd, bf16_dev(k), bf16_dev(v), None, None, 0.0, cuda(tc), cuda(ts), d, cud, cl, btd,
+                          kp, vp, qd)
+    return qd, kp, vp, cud, cl, btd
+
+
+def test_attention_bf16_varlen_paged(ctx):
+    """32 sequences with seeded lengths in [64, 2048], pages of 16 from a seeded permutation of
+    a 4096-page pool, RoPE theta 1e7. Pages bit-exact; the shortest, the longest and two other
+    sequences against the oracle (2e-2 relative); every sequence against the fp32 kernel."""
+    from huncho_amd.ops import paged_prefill_attention
+
+    P, pool = 16, 4096
+    lengths, cu, bt, q, k, v = _varlen_bf16_case(32, 64, 2048, SEED)
+    qd, kp, vp, cud, cl, btd = _gpu_rope_and_pages(ctx, lengths, cu, bt, q, k, v, P, pool)
+    o = paged_prefill_attention(ctx, qd, kp, vp, btd, cud, cl, max(lengths))
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    # pages: oracle RoPE (bf16 op sequence) then oracle page write
+    pos = np.concatenate([np.arange(L) for L in lengths]).astype(np.int32)
+    cs, sn = O.rope_cos_sin(128, 1e7, pos, True)
+    k_ref = O.bf16_bits(O.apply_rope(O.bf16_to_f32(k), 128, cs, sn, True))
+    kp_ref = np.zeros((pool, 8, P, 128), np.uint16)
+    vp_ref = kp_ref.copy()
+    O.paged_kv_write(k_ref, v, cu, pos, bt, P, kp_ref, vp_ref)
+    assert np.array_equal(bits_of(kp), kp_ref) and np.array_equal(bits_of(vp), vp_ref)
+    q_ref = O.bf16_bits(O.apply_rope(O.bf16_to_f32(q), 128, cs, sn, True))
+    assert np.array_equal(bits_of(qd), q_ref)
+    # oracle on a subset of sequences
+    o_np = O.bf16_to_f32(bits_of(o))
+    pick = sorted({int(np.argmin(lengths)), int(np.argmax(lengths)), 3, 17})
+    for s in pick:
+        a, b = cu[s], cu[s + 1]
+        ref = O.paged_attention(q_ref[a:b], kp_ref, vp_ref, bt[s:s + 1], [0, b - a], [b - a], P, 1 / math.sqrt(128))
+        e = rel_err(o_np[a:b], ref)
+        assert e < 2e-2, (s, lengths[s], e)
+    # every sequence: bf16 kernel vs the fp32 kernel on the same (bf16-valued) inputs
+    o32 = paged_prefill_attention(ctx, qd.float(), kp.float(), vp.float(), btd, cud, cl, max(lengths))
+    e = rel_err(o_np, o32.cpu().numpy())
+    assert e < 2e-2, e
+
+
+@pytest.mark.parametrize("group,P", [(1, 32), (4, 64), (8, 256)])
+def test_attention_bf16_gqa_groups_and_pages(ctx, group, P):
+    """Other GQA ratios and page sizes, with a prefix already in the pages (context > q_len)."""
+    from huncho_amd.ops import paged_kv_write, paged_prefill_attention
+
+    hkv, d = 2, 128
+    hq = hkv * group
+    ctx_lens = [300, 77, 129]
+    q_lens = [100, 77, 1]
+    pool = sum((L + P - 1) // P for L in ctx_lens) + 3
+    bt = block_tables_for(ctx_lens, P, pool, SEED + group)
+    cu_k = np.concatenate([[0], np.cumsum(ctx_lens)]).astype(np.int32)
+    nk = int(cu_k[-1])
+    kk = abi.synth_normal_bf16(SEED, 30 + group, nk * hkv * d).reshape(nk, hkv, d)
+    vv = abi.synth_normal_bf16(SEED, 40 + group, nk * hkv * d).reshape(nk, hkv, d)
+    kp = torch.zeros((pool, hkv, P, d), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    paged_kv_write(ctx, bf16_dev(kk), bf16_dev(vv), cuda(cu_k), cuda(np.array(ctx_lens, np.int32)), cuda(bt), kp,
+                   vp)
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    nq = int(cu_q[-1])
+    q = abi.synth_normal_bf16(SEED, 50 + group, nq * hq * d).reshape(nq, hq, d)
+    gate = abi.synth_normal_bf16(SEED, 60 + group, nq * hq * d).reshape(nq, hq, d)
+    o = paged_prefill_attention(ctx, bf16_dev(q), kp, vp, cuda(bt), cuda(cu_q), cuda(np.array(ctx_lens, np.int32)),
+                                max(q_lens), gate=bf16_dev(gate))
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    ref = O.paged_attention(q, bits_of(kp), bits_of(vp), bt, cu_q, ctx_lens, P, 1 / math.sqrt(d))
+    sg = O.round_bf16(1 / (1 + np.exp(-O.bf16_to_f32(gate).astype(np.float64))))
+    ref = O.round_bf16(O.round_bf16(ref) * sg)
+    e = rel_err(O.bf16_to_f32(bits_of(o)), ref)
+    assert e < 2e-2, e
+
+
+# ---------------------------------------------------------------------------
+# gated delta rule
+# ---------------------------------------------------------------------------
+
+def _gdn_case(lengths, H, seed, hk=None):
+    hk = hk or H
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n = int(cu[-1])
+    q = O.l2norm(abi.synth_normal(seed, 70, n * hk * 128).reshape(n, hk, 128)) * np.float32(128 ** -0.5)
+    k = O.l2norm(abi.synth_normal(seed, 71, n * hk * 128).reshape(n, hk, 128))
+    v = abi.synth_normal(seed, 72, n * H * 128).reshape(n, H, 128)
+    beta = (1 / (1 + np.exp(-abi.synth_normal(seed, 73, n * H).astype(np.float64)))).astype(np.float32).reshape(n, H)
+    g = (-np.log1p(np.exp(abi.synth_normal(seed, 74, n * H).astype(np.float64))) * 0.5).astype(np.float32).reshape(n, H)
+    return cu, q, k, v, g, beta
+
+
+def _expand(x, H):
+    rep = H // x.shape[1]
+    return np.repeat(x, rep, axis=1) if rep > 1 else x
+
+
+def test_delta_rule_fp32_config(ctx):
+    """T=512, 16 heads, dk=dv=128, chunk 64, zero initial state: output and final state
+    within 1e-4 relative of the per-token recurrence."""
+    from huncho_amd.ops import gated_delta_chunked
+
+    cu, q, k, v, g, beta = _gdn_case([512], 16, SEED)
+    o_ref, s_ref = O.gated_delta_rule(q, k, v, g, beta, cu)
+    st = torch.zeros((1, 16, 128, 128), device="cuda")
+    o = gated_delta_chunked(ctx, cuda(q), cuda(k), cuda(v), cuda(g), cuda(beta), cuda(cu), final_state=st)
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    eo, es = rel_err(o.cpu().numpy(), o_ref), rel_err(st.cpu().numpy(), s_ref)
+    assert eo < 1e-4 and es < 1e-4, (eo, es)
+
+
+def test_delta_rule_fp32_varlen_ragged_initial_state_gqa(ctx):
+    """Ragged lengths (not multiples of 64, including 1), a nonzero carried state, and 2 value
+    heads per key head (repeat_interleave mapping)."""
+    from huncho_amd.ops import gated_delta_chunked
+
+    lengths = [1, 63, 64, 65, 200]
+    H, hk = 4, 2
+    cu, q, k, v, g, beta = _gdn_case(lengths, H, SEED + 1, hk)
+    s0 = abi.synth_normal(SEED, 75, len(lengths) * H * 128 * 128, 0.0, 0.05).reshape(len(lengths), H, 128, 128)
+    o_ref, s_ref = O.gated_delta_rule(_expand(q, H), _expand(k, H), v, g, beta, cu, s0)
+    st = cuda(s0.copy())
+    o = gated_delta_chunked(ctx, cuda(q), cuda(k), cuda(v), cuda(g), cuda(beta), cuda(cu), initial_state=st,
+                            final_state=st)
+    torch.cuda.synchronize()
+    eo, es = rel_err(o.cpu().numpy(), o_ref), rel_err(st.cpu().numpy(), s_ref)
+    assert eo < 1e-4 and es < 1e-4, (eo, es)
+
+
+def test_delta_rule_split_continuation(ctx):
+    """split(T) with the state handed over == whole (fp32, 1e-4)."""
+    from huncho_amd.ops import gated_delta_chunked
+
+    cu, q, k, v, g, beta = _gdn_case([300], 2, SEED + 2)
+    whole_s = torch.zeros((1, 2, 128, 128), device="cuda")
+    whole = gated_delta_chunked(ctx, cuda(q), cuda(k), cuda(v), cuda(g), cuda(beta), cuda(cu), final_state=whole_s)
+    s1 = torch.zeros_like(whole_s)
+    cut = 100
+    o1 = gated_delta_chunked(ctx, cuda(q[:cut]), cuda(k[:cut]), cuda(v[:cut]), cuda(g[:cut]), cuda(beta[:cut]),
+                             cuda(np.array([0, cut], np.int32)), final_state=s1)
+    o2 = gated_delta_chunked(ctx, cuda(q[cut:]), cuda(k[cut:]), cuda(v[cut:]), cuda(g[cut:]), cuda(beta[cut:]),
+                             cuda(np.array([0, 300 - cut], np.int32)), initial_state=s1, final_state=s1)
+    torch.cuda.synchronize()
+    assert rel_err(torch.cat([o1, o2]).cpu().numpy(), whole.cpu().numpy()) < 1e-4
+    assert rel_err(s1.cpu().numpy(), whole_s.cpu().numpy()) < 1e-4
+
+
+def test_delta_rule_bf16(ctx):
+    """bf16 q/k/v/o with fp32 state: 64 rows x 512 tokens x 16 heads (the Kev batch shape,
+    4 rows checked against the oracle), 2e-2 relative."""
+    from huncho_amd.ops import gated_delta_chunked
+
+    lengths = [512] * 64
+    cu, q, k, v, g, beta = _gdn_case(lengths, 16, SEED + 3)
+    qb, kb, vb = (O.bf16_bits(x) for x in (q, k, v))
+    beta = O.round_bf16(beta)
+    st = torch.zeros((64, 16, 128, 128), device="cuda")
+    o = gated_delta_chunked(ctx, bf16_dev(qb), bf16_dev(kb), bf16_dev(vb), cuda(g), cuda(beta), cuda(cu),
+                            final_state=st)
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    o_np = O.bf16_to_f32(bits_of(o))
+    st_np = st.cpu().numpy()
+    for s in (0, 21, 63):
+        a, b = cu[s], cu[s + 1]
+        o_ref, s_ref = O.gated_delta_rule(O.bf16_to_f32(qb[a:b]), O.bf16_to_f32(kb[a:b]), O.bf16_to_f32(vb[a:b]),
+                                          g[a:b], beta[a:b], [0, b - a])
+        eo, es = rel_err(o_np[a:b], o_ref), rel_err(st_np[s], s_ref[0])
+        assert eo < 2e-2 and es < 2e-2, (s, eo, es)
+
+
+# ---------------------------------------------------------------------------
+# GDN prep, norms, SwiGLU
+# ---------------------------------------------------------------------------
+
+def test_gdn_prep_bf16(ctx):
+    from huncho_amd.ops import gdn_prep
+
+    lengths = [3, 70, 130]
+    H = hk = 4
+    conv_dim = (2 * hk + H) * 128
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n = int(cu[-1])
+    width = conv_dim + 2 * H
+    mixed = abi.synth_normal_bf16(SEED, 80, n * width).reshape(n, width)
+    conv_w = O.round_bf16(abi.synth_normal(SEED, 81, conv_dim * 4, 0.0, 0.5)).reshape(conv_dim, 4)
+    a_log = O.round_bf16(abi.synth_normal(SEED, 82, H, 0.0, 0.3))
+    dt_bias = O.round_bf16(abi.synth_normal(SEED, 83, H, 0.0, 0.3))
+    base_g = (-np.exp(a_log)).astype(np.float32)
+    q, k, v, g, beta, tail = gdn_prep(ctx, bf16_dev(mixed), cuda(conv_w), bf16_dev(mixed), conv_dim, conv_dim + H,
+                                      cuda(base_g), cuda(dt_bias), cuda(cu), H, hk, want_tail=True)
+    torch.cuda.synchronize()
+    f = O.bf16_to_f32(mixed)
+    for s in range(len(lengths)):
+        a, b = cu[s], cu[s + 1]
+        conv, t_ref = O.causal_conv1d_silu(f[a:b, :conv_dim], conv_w, want_tail=True)
+        conv = O.round_bf16(conv)
+        qr = O.l2norm(conv[:, : hk * 128].reshape(-1, hk, 128)) * np.float32(128 ** -0.5)
+        kr = O.l2norm(conv[:, hk * 128: 2 * hk * 128].reshape(-1, hk, 128))
+        vr = conv[:, 2 * hk * 128:].reshape(-1, H, 128)
+        assert rel_err(O.bf16_to_f32(bits_of(q[a:b])), qr) < 1e-2
+        assert rel_err(O.bf16_to_f32(bits_of(k[a:b])), kr) < 1e-2
+        assert rel_err(O.bf16_to_f32(bits_of(v[a:b])), vr) < 1e-2
+        bb, aa = f[a:b, conv_dim:conv_dim + H], f[a:b, conv_dim + H:]
+        np.testing.assert_allclose(beta[a:b].cpu().numpy(), O.round_bf16(1 / (1 + np.exp(-bb))), rtol=1e-2, atol=1e-3)
+        np.testing.assert_allclose(g[a:b].cpu().numpy(), base_g * np.log(np.exp(aa + dt_bias) + 1), rtol=1e-4,
+                                   atol=1e-5)
+        got_tail = O.bf16_to_f32(bits_of(tail[s]))
+        if b - a >= 3:
+            assert np.array_equal(got_tail, t_ref)
+
+
+def test_norms_and_swiglu_bf16(ctx):
+    from huncho_amd.ops import gated_rms_norm, rms_norm, swiglu
+
+    n, H = 50, 1024
+    x = abi.synth_normal_bf16(SEED, 90, n * H).reshape(n, H)
+    w = O.round_bf16(abi.synth_normal(SEED, 91, H, 0.0, 0.02)) + np.float32(1)
+    y = rms_norm(ctx, bf16_dev(x), cuda(w), 1e-6)
+    ref = O.round_bf16(O.rms_norm_effective(O.bf16_to_f32(x), w, 1e-6))
+    assert rel_err(O.bf16_to_f32(bits_of(y)), ref) < 1e-2
+    heads = 8
+    o = abi.synth_normal_bf16(SEED, 92, n * heads * 128).reshape(n, heads, 128)
+    z = abi.synth_normal_bf16(SEED, 93, n * heads * 128 * 2).reshape(n, heads * 128 * 2)
+    nw = O.round_bf16(abi.synth_normal(SEED, 94, 128, 1.0, 0.1))
+    gn = gated_rms_norm(ctx, bf16_dev(o), bf16_dev(z)[:, heads * 128:], cuda(nw), 1e-6)
+    ref = O.round_bf16(O.rms_norm_gated(O.bf16_to_f32(o), O.bf16_to_f32(z)[:, heads * 128:].reshape(n, heads, 128),
+                                        nw, 1e-6))
+    assert rel_err(O.bf16_to_f32(bits_of(gn)), ref) < 1e-2
+    I = 3584
+    gu = abi.synth_normal_bf16(SEED, 95, n * 2 * I).reshape(n, 2 * I)
+    s = swiglu(ctx, bf16_dev(gu), I)
+    gf = O.bf16_to_f32(gu)
+    ref = O.round_bf16(O.round_bf16(gf[:, :I] / (1 + np.exp(-gf[:, :I]))) * gf[:, I:])
+    assert rel_err(O.bf16_to_f32(bits_of(s)), ref) < 1e-2
