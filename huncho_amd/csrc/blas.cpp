@@ -3,8 +3,9 @@
 // Row-major Y[n][out] = alpha * X[n][in] . W[out][in]^T + beta * C is the column-major
 // product Y^T = W . X^T: m = out, n = n, k = in, op(A) = T on the weight, op(B) = N on the
 // activations. bf16 operands with fp32 accumulation (HIPBLAS_COMPUTE_32F), or fp32.
-// Plans (descriptors + heuristic algorithm) are cached per shape; the workspace is owned
-// by the context and allocated on the first GEMM.
+// Plans (descriptors + the fastest of up to 16 heuristic algorithms, timed once on first
+// use of a shape) are cached per shape; the workspace is owned by the context and allocated
+// on the first GEMM.
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
@@ -68,6 +69,47 @@ static int blas_init(hk_ctx* ctx) {
     return HK_OK;
 }
 
+// Times every returned candidate (3 launches each, beta = 0 into a scratch output so the
+// caller's buffers are untouched) and returns the index of the fastest; 0 if timing fails.
+template <typename P, typename R>
+static int pick_fastest(hk_ctx* ctx, P& p, R* res, int returned, int dtype, int out, int n, const void* x,
+                        const void* w, void* y, long ldy) {
+    if (returned <= 1) return 0;
+    hk_blas* B = ctx->blas;
+    void* scratch = nullptr;
+    const size_t bytes = (size_t)ldy * n * (dtype == HK_BF16 ? 2 : 4);
+    if (hipMalloc(&scratch, bytes) != hipSuccess) return 0;
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0);
+    hipEventCreate(&e1);
+    const float one = 1.0f, zero = 0.0f;
+    int best = 0;
+    float best_ms = 1e30f;
+    for (int i = 0; i < returned; ++i) {
+        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > B->ws_bytes) continue;
+        bool ok = hipblasLtMatmul(B->handle, p.desc, &one, w, p.a, x, p.b, &zero, scratch, p.d, scratch, p.d,
+                                  &res[i].algo, B->workspace, res[i].workspaceSize, ctx->stream) == HIPBLAS_STATUS_SUCCESS;
+        hipEventRecord(e0, ctx->stream);
+        for (int r = 0; ok && r < 3; ++r)
+            ok = hipblasLtMatmul(B->handle, p.desc, &one, w, p.a, x, p.b, &zero, scratch, p.d, scratch, p.d,
+                                 &res[i].algo, B->workspace, res[i].workspaceSize, ctx->stream) == HIPBLAS_STATUS_SUCCESS;
+        hipEventRecord(e1, ctx->stream);
+        float ms = 0.0f;
+        if (ok && hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess &&
+            ms < best_ms) {
+            best_ms = ms;
+            best = i;
+        }
+    }
+    hipStreamSynchronize(ctx->stream);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipFree(scratch);
+    (void)out;
+    (void)y;
+    return best;
+}
+
 int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, long ldx, const void* w, long ldw,
                 void* y, long ldy, const void* c, long ldc, float alpha, float beta) {
     if (n == 0 || out == 0) return HK_OK;
@@ -98,9 +140,9 @@ int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, l
         uint64_t wsmax = B->ws_bytes;
         ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax,
                                                          sizeof(wsmax)) == HIPBLAS_STATUS_SUCCESS;
-        hipblasLtMatmulHeuristicResult_t res[4];
+        hipblasLtMatmulHeuristicResult_t res[16];
         int returned = 0;
-        ok = ok && hipblasLtMatmulAlgoGetHeuristic(B->handle, p.desc, p.a, p.b, p.c, p.d, pref, 4, res, &returned) ==
+        ok = ok && hipblasLtMatmulAlgoGetHeuristic(B->handle, p.desc, p.a, p.b, p.c, p.d, pref, 16, res, &returned) ==
                        HIPBLAS_STATUS_SUCCESS;
         if (pref) hipblasLtMatmulPreferenceDestroy(pref);
         if (!ok || returned == 0) {
@@ -111,8 +153,9 @@ int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, l
             if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
             return hk_fail(ctx, HK_ERR_UNSUPPORTED, "no hipBLASLt algorithm for %dx%dx%d", out, n, in);
         }
-        p.algo = res[0].algo;
-        p.ws = res[0].workspaceSize;
+        int best = pick_fastest(ctx, p, res, returned, dtype, out, n, x, w, y, ldy);
+        p.algo = res[best].algo;
+        p.ws = res[best].workspaceSize;
         it = B->plans.emplace(key, p).first;
     }
     Plan& p = it->second;

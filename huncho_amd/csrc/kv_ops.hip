@@ -127,10 +127,100 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_write(KvArgs a) {
     }
 }
 
+// 16-bit fast path: one 16-lane group per (token, head row), 8 consecutive elements per
+// lane (16-byte accesses). Rows are the Hq query heads then the Hkv key heads (with their
+// value rows). RoPE partners e +- rd/2 live in lane sub +- rd/16 of the same group, element i.
+// Requires rd % 16 == 0.
+template <typename T>
+__global__ __launch_bounds__(256) void qk_norm_rope_kv_write_vec(KvArgs a) {
+    typedef T v8 __attribute__((ext_vector_type(8)));
+    const int rows_per_tok = a.q_heads + a.kv_heads;
+    const long item = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int sub = threadIdx.x & 15, lane = threadIdx.x & 63, gbase = lane & ~15;
+    const bool live = item < (long)a.n_tokens * rows_per_tok;
+    const int t = live ? (int)(item / rows_per_tok) : 0, r = live ? (int)(item % rows_per_tok) : 0;
+    const int s = find_seq(a.cu_seqlens_q, a.n_seqs, t);
+    const int q0 = a.cu_seqlens_q[s], q_len = a.cu_seqlens_q[s + 1] - q0;
+    const int pos = a.context_lens[s] - q_len + (t - q0);
+    bool ok = live && pos >= 0 && t - q0 < q_len;
+    if (live && !ok && sub == 0) atomicOr(a.fault, 1);
+    if (ok && a.rope_cos && pos >= a.rope_max_pos) {
+        if (sub == 0) atomicOr(a.fault, 4);
+        ok = false;
+    }
+    const bool is_q = r < a.q_heads;
+    const int h = is_q ? r : r - a.q_heads;
+    const T* src = is_q ? (const T*)a.q_in + (long)t * a.q_in_tok + (long)h * a.q_in_head
+                        : (const T*)a.k_in + (long)t * a.k_in_tok + (long)h * HD;
+    float x[8];
+    {
+        v8 raw = ok ? *(const v8*)(src + sub * 8) : v8{};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = to_f(raw[e]);
+    }
+    const float* w = is_q ? a.q_norm : a.k_norm;
+    if (w) {  // uniform across the workgroup's groups only per row type; shuffles stay in-group
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        const float denom = sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = rnd<T>((x[e] / denom) * w[sub * 8 + e]);
+    }
+    if (a.rope_cos) {
+        const int half = a.rd >> 1, hl = half >> 3;  // partner lane offset
+        const bool rot = sub * 8 < a.rd;
+        const bool first = sub * 8 < half;
+        const int psub = rot ? (first ? sub + hl : sub - hl) : sub;
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = __shfl(x[e], gbase + psub);
+        if (rot && ok) {
+            const float* cs = a.rope_cos + (long)pos * half;
+            const float* sn = a.rope_sin + (long)pos * half;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int fi = (first ? sub * 8 : sub * 8 - half) + e;
+                const float rv = first ? -pv[e] : pv[e];
+                x[e] = rnd<T>(rnd<T>(x[e] * cs[fi]) + rnd<T>(rv * sn[fi]));
+            }
+        }
+    }
+    if (!ok) return;
+    v8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = from_f<T>(x[e]);
+    if (is_q) {
+        *(v8*)((T*)a.q_out + (long)t * a.q_out_tok + (long)h * a.q_out_head + sub * 8) = out;
+        return;
+    }
+    const int pidx = pos >> a.page_shift;
+    const int page = pidx < a.bt_stride ? a.block_tables[(long)s * a.bt_stride + pidx] : -1;
+    if (page < 0 || page >= a.num_pages) {
+        if (sub == 0) atomicOr(a.fault, 2);
+        return;
+    }
+    const long row = (((long)page * a.kv_heads + h) << a.page_shift) + (pos & ((1 << a.page_shift) - 1));
+    *(v8*)((T*)a.k_pool + row * HD + sub * 8) = out;
+    *(v8*)((T*)a.v_pool + row * HD + sub * 8) = *(const v8*)((const T*)a.v_in + (long)t * a.v_in_tok + (long)h * HD + sub * 8);
+}
+
 }  // namespace hk
 
 extern "C" int hk_launch_qk_norm_rope_kv_write(int is_bf16, const hk::KvArgs* args, hipStream_t stream) {
     if (args->n_tokens == 0) return HK_OK;
+    const bool aligned = ((args->q_in_tok | args->q_in_head | args->k_in_tok | args->v_in_tok | args->q_out_tok |
+                           args->q_out_head) % 8) == 0 &&
+                         (((uintptr_t)args->q_in | (uintptr_t)args->k_in | (uintptr_t)args->v_in |
+                           (uintptr_t)args->q_out | (uintptr_t)args->k_pool | (uintptr_t)args->v_pool) & 15) == 0;
+    if (is_bf16 && aligned && (!args->rope_cos || args->rd % 16 == 0)) {
+        const long items = (long)args->n_tokens * (args->q_heads + args->kv_heads);
+        hipLaunchKernelGGL(hk::qk_norm_rope_kv_write_vec<hk::bf16>, dim3((unsigned)((items + 15) / 16)), dim3(256), 0,
+                           stream, *args);
+        return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+    }
     if (is_bf16)
         hipLaunchKernelGGL(hk::qk_norm_rope_kv_write<hk::bf16>, dim3(args->n_tokens), dim3(256), 0, stream, *args);
     else

@@ -104,6 +104,112 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
     }
 }
 
+// Vectorised GDN prep for 16-bit activations and K = 4 taps. Workgroup = PREP_TB consecutive
+// tokens x 2048 channels; thread = 8 consecutive channels (one 16-byte load per row). The
+// thread walks its tokens in order keeping the previous 3 input rows in registers, so each
+// input row is read once; the per-head l2norm (128 channels = 16 lanes) reduces across the
+// 16-lane group. A token block may cross a sequence boundary: the window restarts there.
+constexpr int PREP_TB = 32;
+
+template <typename T>
+__global__ __launch_bounds__(256) void gdn_prep_vec4(PrepArgs a) {
+    typedef T v8 __attribute__((ext_vector_type(8)));
+    const int tid = threadIdx.x;
+    const int key_dim = a.Hk * HW, conv_dim = 2 * key_dim + a.Hv * HW;
+    const int c0 = blockIdx.y * 2048 + tid * 8;
+    const bool active = c0 < conv_dim;
+    const int region = c0 < key_dim ? 0 : (c0 < 2 * key_dim ? 1 : 2);
+    const int head = (c0 - region * key_dim) / HW, ch = c0 % HW;
+    const int tb0 = blockIdx.x * PREP_TB;
+    if (tb0 >= a.n_tokens) return;
+    const int tend = min(tb0 + PREP_TB, a.n_tokens);
+    float w[8][4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int tap = 0; tap < 4; ++tap) w[e][tap] = active ? a.conv_w[(long)(c0 + e) * 4 + tap] : 0.0f;
+    int s = seq_of(a.cu_seqlens, a.n_seqs, tb0);
+    int start = a.cu_seqlens[s], next = a.cu_seqlens[s + 1];
+    if (start < 0 || start > tb0 || next > a.n_tokens || next <= tb0) {
+        if (tid == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    // raw input (or cached tail / zero) at position tt of sequence s
+    auto load_row = [&](int tt, int sq, int st, float* dst) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[e] = 0.0f;
+        if (!active) return;
+        if (tt >= st) {
+            v8 x = *(const v8*)((const T*)a.mixed + (long)tt * a.mixed_tok + c0);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dst[e] = to_f(x[e]);
+        } else if (a.hist && tt >= st - 3) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                dst[e] = to_f(((const T*)a.hist)[((long)sq * conv_dim + c0 + e) * 3 + (tt - st + 3)]);
+        }
+    };
+    float win[3][8];
+    load_row(tb0 - 3, s, start, win[0]);
+    load_row(tb0 - 2, s, start, win[1]);
+    load_row(tb0 - 1, s, start, win[2]);
+    for (int t = tb0; t < tend; ++t) {
+        while (t == next && s + 1 < a.n_seqs) {  // a new sequence starts in this block (skip empty ones)
+            ++s;
+            start = next;
+            next = a.cu_seqlens[s + 1];
+            load_row(t - 3, s, start, win[0]);
+            load_row(t - 2, s, start, win[1]);
+            load_row(t - 1, s, start, win[2]);
+        }
+        float cur[8], y[8];
+        load_row(t, s, start, cur);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float acc = 0.0f;
+            acc += w[e][0] * win[0][e];
+            acc += w[e][1] * win[1][e];
+            acc += w[e][2] * win[2][e];
+            acc += w[e][3] * cur[e];
+            y[e] = rndt<T>(silu(acc));
+        }
+        if (region < 2) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+#pragma unroll
+            for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+            float inv = 1.0f / sqrtf(ss + 1e-6f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = region == 0 ? (y[e] * inv) * a.scale : y[e] * inv;
+        }
+        if (active) {
+            v8 out;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) out[e] = from_f<T>(y[e]);
+            const int nh = region == 2 ? a.Hv : a.Hk;
+            T* dst = (T*)(region == 0 ? a.q_out : region == 1 ? a.k_out : a.v_out);
+            *(v8*)(dst + ((long)t * nh + head) * HW + ch) = out;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            win[0][e] = win[1][e];
+            win[1][e] = win[2][e];
+            win[2][e] = cur[e];
+        }
+    }
+    if (blockIdx.y == 0) {
+        for (int idx = tid; idx < (tend - tb0) * a.Hv; idx += 256) {
+            const int t = tb0 + idx / a.Hv, h = idx % a.Hv;
+            const T* row = (const T*)a.ba + (long)t * a.ba_tok;
+            const float b = to_f(row[a.b_col + h]);
+            const float av = to_f(row[a.a_col + h]);
+            a.beta_out[(long)t * a.Hv + h] = rndt<T>(1.0f / (1.0f + __expf(-b)));
+            a.g_out[(long)t * a.Hv + h] = a.base_g[h] * __logf(__expf(av + a.dt_bias[h]) + 1.0f);
+        }
+    }
+}
+
 // Tail of the concatenated [history, x] sequence: its last K-1 raw inputs per channel.
 template <typename T>
 __global__ void conv_tail(PrepArgs a, void* tail_out, int conv_dim) {
@@ -141,6 +247,66 @@ __global__ __launch_bounds__(256) void rms_norm(NormArgs a) {
     ss = wsum(ss);
     const float denom = sqrtf(ss / (float)a.width + a.eps);
     for (int i = lane; i < a.width; i += 64) y[i] = from_f<T>((to_f(x[i]) / denom) * a.w[i]);
+}
+
+// 16-bit rows of width 512 * N8: one wave per row, 8 consecutive elements per lane per step.
+template <typename T, int N8>
+__global__ __launch_bounds__(256) void rms_norm_vec(NormArgs a) {
+    typedef T v8 __attribute__((ext_vector_type(8)));
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= a.rows) return;
+    const T* x = (const T*)a.x + (long)row * a.x_tok;
+    T* y = (T*)a.y + (long)row * a.y_tok;
+    float v[N8][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N8; ++i) {
+        v8 t = *(const v8*)(x + (i * 64 + lane) * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[i][e] = to_f(t[e]);
+            ss += v[i][e] * v[i][e];
+        }
+    }
+    ss = wsum(ss);
+    const float denom = sqrtf(ss / (float)a.width + a.eps);
+#pragma unroll
+    for (int i = 0; i < N8; ++i) {
+        const int c = (i * 64 + lane) * 8;
+        v8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = from_f<T>((v[i][e] / denom) * a.w[c + e]);
+        *(v8*)(y + c) = o;
+    }
+}
+
+// 16-bit rows of width 128: 16 lanes per row (8 elements each), 16 rows per workgroup.
+template <typename T>
+__global__ __launch_bounds__(256) void gated_rms_norm_vec128(GatedNormArgs a) {
+    typedef T v8 __attribute__((ext_vector_type(8)));
+    const int row = blockIdx.x * 16 + (threadIdx.x >> 4), sub = threadIdx.x & 15;
+    const bool ok = row < a.rows;
+    const int t = row / a.heads, h = row % a.heads;
+    float xv[8], zv[8];
+    float ss = 0.0f;
+    if (ok) {
+        v8 xr = *(const v8*)((const T*)a.x + (long)row * 128 + sub * 8);
+        v8 zr = *(const v8*)((const T*)a.z + (long)t * a.z_tok + (long)h * 128 + sub * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            xv[e] = to_f(xr[e]);
+            zv[e] = to_f(zr[e]);
+            ss += xv[e] * xv[e];
+        }
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if (!ok) return;
+    const float denom = sqrtf(ss / 128.0f + a.eps);
+    v8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = from_f<T>(((xv[e] / denom) * a.w[sub * 8 + e]) * silu(zv[e]));
+    *(v8*)((T*)a.y + (long)row * 128 + sub * 8) = out;
 }
 
 template <typename T>
@@ -237,7 +403,11 @@ __global__ void final_norm_head(const void* x, long x_tok, const int* cu, const 
 using namespace hk;
 
 extern "C" int hk_launch_gdn_prep(int is_bf16, const PrepArgs* a, void* tail_out, hipStream_t st) {
-    if (a->n_tokens > 0) {
+    const int conv_dim_v = (2 * a->Hk + a->Hv) * HW;
+    if (a->n_tokens > 0 && is_bf16 && a->K == 4 && a->mixed_tok % 8 == 0 && ((uintptr_t)a->mixed & 15) == 0) {
+        dim3 grid((a->n_tokens + PREP_TB - 1) / PREP_TB, (conv_dim_v + 2047) / 2048);
+        hipLaunchKernelGGL(gdn_prep_vec4<bf16>, grid, dim3(256), 0, st, *a);
+    } else if (a->n_tokens > 0) {
         if (is_bf16)
             hipLaunchKernelGGL(gdn_prep<bf16>, dim3(a->n_tokens), dim3(256), 0, st, *a);
         else
@@ -257,7 +427,15 @@ extern "C" int hk_launch_gdn_prep(int is_bf16, const PrepArgs* a, void* tail_out
 extern "C" int hk_launch_rms_norm(int is_bf16, const NormArgs* a, hipStream_t st) {
     if (a->rows == 0) return HK_OK;
     dim3 grid((a->rows + 3) / 4);
-    if (is_bf16)
+    const bool aligned = ((uintptr_t)a->x & 15) == 0 && ((uintptr_t)a->y & 15) == 0 && a->x_tok % 8 == 0 &&
+                         a->y_tok % 8 == 0;
+    if (is_bf16 && aligned && a->width == 1024)
+        hipLaunchKernelGGL((rms_norm_vec<bf16, 2>), grid, dim3(256), 0, st, *a);
+    else if (is_bf16 && aligned && a->width == 2048)
+        hipLaunchKernelGGL((rms_norm_vec<bf16, 4>), grid, dim3(256), 0, st, *a);
+    else if (is_bf16 && aligned && a->width == 512)
+        hipLaunchKernelGGL((rms_norm_vec<bf16, 1>), grid, dim3(256), 0, st, *a);
+    else if (is_bf16)
         hipLaunchKernelGGL(rms_norm<bf16>, grid, dim3(256), 0, st, *a);
     else
         hipLaunchKernelGGL(rms_norm<float>, grid, dim3(256), 0, st, *a);
@@ -267,7 +445,10 @@ extern "C" int hk_launch_rms_norm(int is_bf16, const NormArgs* a, hipStream_t st
 extern "C" int hk_launch_gated_rms_norm(int is_bf16, const GatedNormArgs* a, hipStream_t st) {
     if (a->rows == 0) return HK_OK;
     dim3 grid((a->rows + 3) / 4);
-    if (is_bf16)
+    if (is_bf16 && a->width == 128 && ((uintptr_t)a->x & 15) == 0 && ((uintptr_t)a->z & 15) == 0 &&
+        ((uintptr_t)a->y & 15) == 0 && a->z_tok % 8 == 0)
+        hipLaunchKernelGGL(gated_rms_norm_vec128<bf16>, dim3((a->rows + 15) / 16), dim3(256), 0, st, *a);
+    else if (is_bf16)
         hipLaunchKernelGGL(gated_rms_norm<bf16>, grid, dim3(256), 0, st, *a);
     else
         hipLaunchKernelGGL(gated_rms_norm<float>, grid, dim3(256), 0, st, *a);
