@@ -18,7 +18,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "_build" / "libhuncho_rocm.so"
 
 HK_OK, HK_ERR_INVALID, HK_ERR_UNSUPPORTED, HK_ERR_DEVICE, HK_ERR_NOMEM = 0, 1, 2, 3, 4
-HK_F32, HK_BF16 = 0, 1
+HK_F32, HK_BF16, HK_F16 = 0, 1, 2
 HK_FAULT_SEQLENS, HK_FAULT_PAGE, HK_FAULT_ROPE, HK_FAULT_TOKEN = 1, 2, 4, 8
 
 vp = C.c_void_p
@@ -75,6 +75,8 @@ SIGNATURES = {
                                        L, vp, L, L]),
     "hk_gated_delta_chunked": (I, [vp, I, vp, L, vp, L, vp, L, vp, vp, vp, I, I, I, I, I, I, vp, vp, vp, L]),
     "hk_gdn_prep": (I, [vp, I, vp, L, vp, I, vp, vp, L, I, I, vp, vp, vp, I, I, I, I, vp, vp, vp, vp, vp, vp]),
+    "hk_gdn_fused": (I, [vp, I, vp, L, vp, I, vp, vp, vp, L, I, I, vp, vp, vp, L, vp, F, vp, I, I, I, I, vp, vp,
+                         vp, L]),
     "hk_rms_norm": (I, [vp, I, vp, L, vp, F, I, I, vp, L]),
     "hk_gated_rms_norm": (I, [vp, I, vp, vp, L, I, vp, F, I, I, vp]),
     "hk_swiglu": (I, [vp, I, vp, L, L, I, I, vp]),
@@ -159,13 +161,15 @@ class Context:
             pass
 
 
-def rope_table(rotary_dim: int, theta: float, max_pos: int, round_bf16: bool):
-    """Host cos/sin tables [max_pos][rd/2] (float32 numpy arrays)."""
+def rope_table(rotary_dim: int, theta: float, max_pos: int, round_bf16=False):
+    """Host cos/sin tables [max_pos][rd/2] (float32 numpy arrays). round_bf16: True/HK_BF16
+    rounds to bf16, HK_F16 to fp16, False/HK_F32 keeps fp32."""
     import numpy as np
 
     cs = np.empty((max_pos, rotary_dim // 2), np.float32)
     sn = np.empty_like(cs)
-    rc = lib().hk_rope_fill_table(rotary_dim, theta, max_pos, int(round_bf16), cs.ctypes.data, sn.ctypes.data)
+    mode = HK_BF16 if round_bf16 is True else int(round_bf16)
+    rc = lib().hk_rope_fill_table(rotary_dim, theta, max_pos, mode, cs.ctypes.data, sn.ctypes.data)
     if rc != HK_OK:
         raise HkError(rc, "bad rope table arguments")
     return cs, sn

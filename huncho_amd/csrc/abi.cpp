@@ -146,6 +146,43 @@ static inline uint16_t f32_to_bf16_bits(float x) {
     if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
+static inline uint16_t f32_to_f16_bits(float x) {
+    // round-to-nearest-even IEEE binary16 (finite inputs; overflow saturates to inf)
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const uint32_t au = u & 0x7fffffffu;
+    if (au >= 0x47800000u) return (uint16_t)(sign | (au > 0x7f800000u ? 0x7e00u : 0x7c00u));
+    if (au < 0x38800000u) {  // subnormal half: quantum 2^-24
+        float ax;
+        memcpy(&ax, &au, 4);
+        const uint32_t m = (uint32_t)nearbyintf(ax * 16777216.0f);
+        return (uint16_t)(sign | m);
+    }
+    const uint32_t r = au + 0x0fffu + ((au >> 13) & 1u) - 0x38000000u;
+    return (uint16_t)(sign | (r >> 13));
+}
+static inline float f16_bits_to_f32(uint16_t hbits) {
+    const uint32_t sign = (uint32_t)(hbits & 0x8000u) << 16;
+    const uint32_t e = (hbits >> 10) & 0x1fu, m = hbits & 0x3ffu;
+    float v;
+    if (e == 0) {
+        v = (float)m * (1.0f / 16777216.0f);
+    } else if (e == 31) {
+        v = m ? NAN : INFINITY;
+    } else {
+        uint32_t u = ((e + 112u) << 23) | (m << 13);
+        memcpy(&v, &u, 4);
+    }
+    uint32_t bits;
+    memcpy(&bits, &v, 4);
+    bits |= sign;
+    memcpy(&v, &bits, 4);
+    return v;
+}
+float hk_host_f16_to_f32(uint16_t b) { return f16_bits_to_f32(b); }
+uint16_t hk_host_f32_to_f16(float x) { return f32_to_f16_bits(x); }
+
 static inline float bf16_bits_to_f32(uint16_t b) {
     uint32_t u = (uint32_t)b << 16;
     float f;
@@ -153,7 +190,7 @@ static inline float bf16_bits_to_f32(uint16_t b) {
     return f;
 }
 
-extern "C" int hk_rope_fill_table(int rd, double theta, int max_pos, int round_bf16, float* cos_host, float* sin_host) {
+extern "C" int hk_rope_fill_table(int rd, double theta, int max_pos, int round_dtype, float* cos_host, float* sin_host) {
     if (rd < 2 || (rd & 1) || max_pos < 0 || !cos_host || !sin_host || !(theta > 0)) return HK_ERR_INVALID;
     const int half = rd / 2;
     for (int p = 0; p < max_pos; ++p)
@@ -162,9 +199,12 @@ extern "C" int hk_rope_fill_table(int rd, double theta, int max_pos, int round_b
             float inv = powf((float)theta, -(2.0f * (float)i) / (float)rd);
             float f = (float)p * inv;
             float c = cosf(f), s = sinf(f);
-            if (round_bf16) {
+            if (round_dtype == HK_BF16) {
                 c = bf16_bits_to_f32(f32_to_bf16_bits(c));
                 s = bf16_bits_to_f32(f32_to_bf16_bits(s));
+            } else if (round_dtype == HK_F16) {
+                c = f16_bits_to_f32(f32_to_f16_bits(c));
+                s = f16_bits_to_f32(f32_to_f16_bits(s));
             }
             cos_host[(size_t)p * half + i] = c;
             sin_host[(size_t)p * half + i] = s;
@@ -275,7 +315,8 @@ static int log2_exact(int v) {
     } while (0)
 
 static int check_dtype(hk_ctx* ctx, int dtype) {
-    if (dtype != HK_F32 && dtype != HK_BF16) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d is not supported", dtype);
+    if (dtype != HK_F32 && dtype != HK_BF16 && dtype != HK_F16)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d is not supported", dtype);
     return HK_OK;
 }
 
@@ -302,7 +343,7 @@ int hk_qk_norm_rope_kv_write_impl(hk_ctx* ctx, int dtype, const void* q_in, long
     hk::KvArgs a{q_in, q_in_tok, q_in_head, k_in, k_in_tok, v_in, v_in_tok, q_norm, k_norm, eps, rope_cos, rope_sin,
                  rd, rope_max_pos, cu, ctxl, n_seqs, n_tokens, bt, bt_stride, num_pages, shift, q_heads, kv_heads,
                  q_out, q_out_tok, q_out_head, k_pool, v_pool, ctx->fault_dev};
-    int rc = hk_launch_qk_norm_rope_kv_write(dtype == HK_BF16, &a, ctx->stream);
+    int rc = hk_launch_qk_norm_rope_kv_write(dtype, &a, ctx->stream);
     return rc ? hk_fail(ctx, rc, "qk_norm_rope_kv_write launch failed") : HK_OK;
 }
 
@@ -359,7 +400,7 @@ extern "C" int hk_paged_prefill_attention(hk_ctx* ctx, int dtype, const void* q,
     hk::AttnArgs a{q, q_tok, q_head, k_pool, v_pool, shift, bt, bt_stride, cu, ctxl, q_heads, kv_heads, group,
                    pos_per_block, scale * 1.4426950408889634f, gate, gate_tok, gate_head, o, o_tok, o_head,
                    num_pages, n_tokens, ctx->fault_dev};
-    int rc = hk_launch_paged_prefill_attention(dtype == HK_BF16, &a, n_seqs, n_qblocks, ctx->stream);
+    int rc = hk_launch_paged_prefill_attention(dtype, &a, n_seqs, n_qblocks, ctx->stream);
     return rc ? hk_fail(ctx, rc, "attention launch failed") : HK_OK;
 }
 
@@ -376,10 +417,15 @@ extern "C" int hk_gated_delta_chunked(hk_ctx* ctx, int dtype, const void* q, lon
     REQUIRE(q_tok >= (long)k_heads * dk && k_tok >= (long)k_heads * dk && v_tok >= (long)heads * dv &&
                 o_tok >= (long)heads * dv,
             "token strides too small");
+    if (dtype != HK_F32) {  // the 16-bit kernel moves rows in 16-byte vectors
+        REQUIRE(q_tok % 8 == 0 && k_tok % 8 == 0 && v_tok % 8 == 0 && o_tok % 8 == 0 &&
+                    (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15) == 0,
+                "16-bit q/k/v/o rows must be 16-byte aligned (token strides a multiple of 8)");
+    }
     hipSetDevice(ctx->device);
     hk::GdnArgs a{q, k, v, q_tok, k_tok, v_tok, heads / k_heads, g, beta, (long)heads, cu, initial_state,
                   final_state, o, o_tok, heads, n_tokens, ctx->fault_dev};
-    int rc = hk_launch_gated_delta_chunked(dtype == HK_BF16, &a, n_seqs, ctx->stream);
+    int rc = hk_launch_gated_delta_chunked(dtype, &a, n_seqs, ctx->stream);
     return rc ? hk_fail(ctx, rc, "gated delta launch failed") : HK_OK;
 }
 
@@ -401,7 +447,7 @@ extern "C" int hk_gdn_prep(hk_ctx* ctx, int dtype, const void* mixed, long mixed
     hk::PrepArgs a{mixed, mixed_tok, conv_w, conv_k, conv_hist, ba, ba_tok, b_col, a_col, base_g, dt_bias, cu, n_seqs,
                    n_tokens, k_heads, heads, 1.0f / sqrtf(128.0f), q_out, k_out, v_out, g_out, beta_out,
                    ctx->fault_dev};
-    int rc = hk_launch_gdn_prep(dtype == HK_BF16, &a, conv_tail_out, ctx->stream);
+    int rc = hk_launch_gdn_prep(dtype, &a, conv_tail_out, ctx->stream);
     return rc ? hk_fail(ctx, rc, "gdn_prep launch failed") : HK_OK;
 }
 
@@ -412,7 +458,7 @@ extern "C" int hk_rms_norm(hk_ctx* ctx, int dtype, const void* x, long x_tok, co
     REQUIRE(x && w && y && rows >= 0 && width > 0 && x_tok >= width && y_tok >= width, "bad rms_norm arguments");
     hipSetDevice(ctx->device);
     hk::NormArgs a{x, x_tok, w, eps, rows, width, y, y_tok};
-    int rc = hk_launch_rms_norm(dtype == HK_BF16, &a, ctx->stream);
+    int rc = hk_launch_rms_norm(dtype, &a, ctx->stream);
     return rc ? hk_fail(ctx, rc, "rms_norm launch failed") : HK_OK;
 }
 
@@ -424,7 +470,7 @@ extern "C" int hk_gated_rms_norm(hk_ctx* ctx, int dtype, const void* x, const vo
             "bad gated_rms_norm arguments");
     hipSetDevice(ctx->device);
     hk::GatedNormArgs a{x, z, z_tok, heads, w, eps, rows, width, y};
-    int rc = hk_launch_gated_rms_norm(dtype == HK_BF16, &a, ctx->stream);
+    int rc = hk_launch_gated_rms_norm(dtype, &a, ctx->stream);
     return rc ? hk_fail(ctx, rc, "gated_rms_norm launch failed") : HK_OK;
 }
 
@@ -434,6 +480,33 @@ extern "C" int hk_swiglu(hk_ctx* ctx, int dtype, const void* gu, long gu_tok, lo
     REQUIRE(gu && y && rows >= 0 && width > 0 && up_off >= width && gu_tok >= up_off + width, "bad swiglu arguments");
     hipSetDevice(ctx->device);
     hk::SwigluArgs a{gu, gu_tok, up_off, rows, width, y};
-    int rc = hk_launch_swiglu(dtype == HK_BF16, &a, ctx->stream);
+    int rc = hk_launch_swiglu(dtype, &a, ctx->stream);
     return rc ? hk_fail(ctx, rc, "swiglu launch failed") : HK_OK;
+}
+
+extern "C" int hk_gdn_fused(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
+                            const void* conv_hist, void* conv_tail_out, const void* ba, long ba_tok, int b_col,
+                            int a_col, const float* base_g, const float* dt_bias, const void* z, long z_tok,
+                            const float* norm_w, float eps, const int32_t* cu, int n_seqs, int n_tokens, int heads,
+                            int k_heads, const float* initial_state, float* final_state, void* out, long out_tok) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (dtype != HK_BF16 && dtype != HK_F16)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "fused Gated DeltaNet layer: 16-bit dtypes only (got %d)", dtype);
+    if (conv_k != 4) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "fused Gated DeltaNet layer: conv kernel 4 only");
+    REQUIRE(heads > 0 && k_heads > 0 && heads % k_heads == 0, "heads %d not a multiple of k_heads %d", heads, k_heads);
+    REQUIRE(n_seqs > 0 && n_seqs <= 65535 && n_tokens >= 0, "bad batch geometry");
+    REQUIRE(mixed && conv_w && ba && base_g && dt_bias && z && norm_w && cu && out, "null pointer argument");
+    const long conv_dim = (2L * k_heads + heads) * 128;
+    REQUIRE(mixed_tok >= conv_dim && mixed_tok % 8 == 0 && ((uintptr_t)mixed & 15) == 0,
+            "mixed rows must hold conv_dim channels with 16-byte aligned rows");
+    REQUIRE(z_tok >= (long)heads * 128 && z_tok % 8 == 0 && ((uintptr_t)z & 15) == 0, "bad z rows");
+    REQUIRE(out_tok >= (long)heads * 128 && out_tok % 8 == 0 && ((uintptr_t)out & 15) == 0, "bad output rows");
+    REQUIRE(b_col >= 0 && a_col >= 0 && b_col + heads <= ba_tok && a_col + heads <= ba_tok, "b/a columns outside a row");
+    hipSetDevice(ctx->device);
+    hk::GdnArgs a{nullptr, nullptr, nullptr, 0, 0, 0, heads / k_heads, nullptr, nullptr, 0, cu, initial_state,
+                  final_state, out, out_tok, heads, n_tokens, ctx->fault_dev};
+    hk::GdnFusedArgs fa{mixed, mixed_tok, conv_w, (int)conv_dim, conv_hist, conv_tail_out, ba, ba_tok, b_col, a_col,
+                        base_g, dt_bias, 1.0f / sqrtf(128.0f), k_heads, z, z_tok, norm_w, eps};
+    int rc = hk_launch_gdn_v2(dtype, 1, &a, &fa, n_seqs, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "fused Gated DeltaNet launch failed") : HK_OK;
 }

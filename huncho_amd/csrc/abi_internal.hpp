@@ -23,6 +23,8 @@ struct hk_ctx {
 int hk_fail(hk_ctx* ctx, int code, const char* fmt, ...);
 int hk_check_hip(hk_ctx* ctx, hipError_t e, const char* what);
 void hk_blas_release(hk_ctx* ctx);
+float hk_host_f16_to_f32(uint16_t b);
+uint16_t hk_host_f32_to_f16(float x);
 
 // Row-major Y[n][out] = alpha * X[n][in] . W[out][in]^T + beta * C (C may alias Y or be null).
 // dtype HK_BF16: bf16 in/out, fp32 accumulation; HK_F32: fp32.

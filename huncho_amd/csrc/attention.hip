@@ -53,11 +53,14 @@ __device__ __forceinline__ int page_of(const AttnArgs& a, const int* table, int 
 }
 
 // ---------------------------------------------------------------------------
-// bf16 inputs, fp32 accumulation
+// 16-bit inputs (bf16 or fp16), fp32 accumulation
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) bf16 Ks[BN * KS_STRIDE_BF16];
-    __shared__ __attribute__((aligned(16))) bf16 Vt[D * VT_STRIDE_BF16];
+template <typename T>
+__global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
+    typedef typename Mma16<T>::v8 v8;
+    typedef typename Mma16<T>::v4 v4;
+    __shared__ __attribute__((aligned(16))) T Ks[BN * KS_STRIDE_BF16];
+    __shared__ __attribute__((aligned(16))) T Vt[D * VT_STRIDE_BF16];
 
     const int kvh = blockIdx.x;
     const int seq = blockIdx.y;
@@ -85,15 +88,15 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
     int qpos = off + (q_valid ? qi : q_len - 1);
 
     // Q fragment: Q[q][ks*16 + g*8 .. +8] for ks = 0..7
-    bf16x8 qf[8];
+    v8 qf[8];
     {
-        const bf16* qp = (const bf16*)a.q + (long)(q0 + (q_valid ? qi : 0)) * a.q_tok + (long)head * a.q_head;
+        const T* qp = (const T*)a.q + (long)(q0 + (q_valid ? qi : 0)) * a.q_tok + (long)head * a.q_head;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             if (q_valid)
-                qf[ks] = *(const bf16x8*)(qp + ks * 16 + g * 8);
+                qf[ks] = *(const v8*)(qp + ks * 16 + g * 8);
             else
-                qf[ks] = bf16x8{};
+                qf[ks] = v8{};
         }
     }
 
@@ -115,7 +118,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
             int page = key < ctx ? page_of(a, table, key) : -1;
             if (page >= 0) {
                 long base = (((long)page * a.kv_heads + kvh) << a.page_shift) + (key & pmask);
-                kr[i] = *(const uint4*)((const bf16*)a.k_pool + base * D + (tid & 15) * 8);
+                kr[i] = *(const uint4*)((const T*)a.k_pool + base * D + (tid & 15) * 8);
             } else {
                 kr[i] = uint4{0, 0, 0, 0};
             }
@@ -123,7 +126,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
             int vpage = vkey < ctx ? page_of(a, table, vkey) : -1;
             if (vpage >= 0) {
                 long base = (((long)vpage * a.kv_heads + kvh) << a.page_shift) + (vkey & pmask);
-                vr[i] = *(const uint4*)((const bf16*)a.v_pool + base * D + (tid & 15) * 8);
+                vr[i] = *(const uint4*)((const T*)a.v_pool + base * D + (tid & 15) * 8);
             } else {
                 vr[i] = uint4{0, 0, 0, 0};
             }
@@ -134,15 +137,15 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
         for (int i = 0; i < 4; ++i)
             *(uint4*)(Ks + ((tid >> 4) + 16 * i) * KS_STRIDE_BF16 + (tid & 15) * 8) = kr[i];
         // transpose V: Vt[d][key]; each thread writes 4 consecutive keys for each of its 8 dims
-        const bf16* v0 = (const bf16*)&vr[0];
-        const bf16* v1 = (const bf16*)&vr[1];
-        const bf16* v2 = (const bf16*)&vr[2];
-        const bf16* v3 = (const bf16*)&vr[3];
+        const T* v0 = (const T*)&vr[0];
+        const T* v1 = (const T*)&vr[1];
+        const T* v2 = (const T*)&vr[2];
+        const T* v3 = (const T*)&vr[3];
         const int kbase = 4 * (tid >> 4), d0 = (tid & 15) * 8;
 #pragma unroll
         for (int dd = 0; dd < 8; ++dd) {
-            bf16x4 w = {v0[dd], v1[dd], v2[dd], v3[dd]};
-            *(bf16x4*)(Vt + (d0 + dd) * VT_STRIDE_BF16 + kbase) = w;
+            v4 w = {v0[dd], v1[dd], v2[dd], v3[dd]};
+            *(v4*)(Vt + (d0 + dd) * VT_STRIDE_BF16 + kbase) = w;
         }
     };
 
@@ -163,11 +166,11 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             s[kb] = f32x16{};
-            const bf16* krow = Ks + (kb * 32 + perm_key(col)) * KS_STRIDE_BF16 + g * 8;
+            const T* krow = Ks + (kb * 32 + perm_key(col)) * KS_STRIDE_BF16 + g * 8;
 #pragma unroll
             for (int ks = 0; ks < 8; ++ks) {
-                bf16x8 af = *(const bf16x8*)(krow + ks * 16);
-                s[kb] = mfma_bf16(af, qf[ks], s[kb]);
+                v8 af = *(const v8*)(krow + ks * 16);
+                s[kb] = Mma16<T>::mma(af, qf[ks], s[kb]);
             }
         }
         // scale to base 2, causal mask (only tiles that reach past the block's first query)
@@ -187,17 +190,17 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
         const float alpha = fast_exp2(m_run - m_new);
         m_run = m_new;
         float lsum = 0.0f;
-        bf16x8 pf[4];
+        v8 pf[4];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                bf16x8 t;
+                v8 t;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     float e = fast_exp2(s[kb][h * 8 + i] - m_new);
                     lsum += e;
-                    t[i] = (bf16)e;
+                    t[i] = (T)e;
                 }
                 pf[kb * 2 + h] = t;
             }
@@ -209,12 +212,12 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
         // O^T += V^T P^T
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-            const bf16* vrow = Vt + (db * 32 + col) * VT_STRIDE_BF16 + g * 16;
+            const T* vrow = Vt + (db * 32 + col) * VT_STRIDE_BF16 + g * 16;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const int kb = c >> 1, h = c & 1;
-                bf16x8 af = *(const bf16x8*)(vrow + kb * 32 + h * 8);
-                acc_o[db] = mfma_bf16(af, pf[c], acc_o[db]);
+                v8 af = *(const v8*)(vrow + kb * 32 + h * 8);
+                acc_o[db] = Mma16<T>::mma(af, pf[c], acc_o[db]);
             }
         }
     }
@@ -223,8 +226,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
     const float l_tot = l_run + __shfl_xor(l_run, 32);
     const float inv_l = 1.0f / l_tot;
     if (!q_valid) return;
-    bf16* op = (bf16*)a.o + (long)(q0 + qi) * a.o_tok + (long)head * a.o_head;
-    const bf16* gp = a.gate ? (const bf16*)a.gate + (long)(q0 + qi) * a.g_tok + (long)head * a.g_head : nullptr;
+    T* op = (T*)a.o + (long)(q0 + qi) * a.o_tok + (long)head * a.o_head;
+    const T* gp = a.gate ? (const T*)a.gate + (long)(q0 + qi) * a.g_tok + (long)head * a.g_head : nullptr;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -233,15 +236,15 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_bf16(AttnArgs a) {
             float r0 = acc_o[db][jj * 4 + 0] * inv_l, r1 = acc_o[db][jj * 4 + 1] * inv_l;
             float r2 = acc_o[db][jj * 4 + 2] * inv_l, r3 = acc_o[db][jj * 4 + 3] * inv_l;
             if (gp) {
-                bf16x4 gv = *(const bf16x4*)(gp + d);
+                v4 gv = *(const v4*)(gp + d);
                 // the reference rounds attn and sigmoid(gate) to the activation dtype, then multiplies
-                r0 = (float)(bf16)r0 * (float)(bf16)sigmoidf_((float)gv[0]);
-                r1 = (float)(bf16)r1 * (float)(bf16)sigmoidf_((float)gv[1]);
-                r2 = (float)(bf16)r2 * (float)(bf16)sigmoidf_((float)gv[2]);
-                r3 = (float)(bf16)r3 * (float)(bf16)sigmoidf_((float)gv[3]);
+                r0 = (float)(T)r0 * (float)(T)sigmoidf_((float)gv[0]);
+                r1 = (float)(T)r1 * (float)(T)sigmoidf_((float)gv[1]);
+                r2 = (float)(T)r2 * (float)(T)sigmoidf_((float)gv[2]);
+                r3 = (float)(T)r3 * (float)(T)sigmoidf_((float)gv[3]);
             }
-            bf16x4 w = {(bf16)r0, (bf16)r1, (bf16)r2, (bf16)r3};
-            *(bf16x4*)(op + d) = w;
+            v4 w = {(T)r0, (T)r1, (T)r2, (T)r3};
+            *(v4*)(op + d) = w;
         }
 }
 
@@ -408,11 +411,13 @@ __global__ __launch_bounds__(256, 1) void paged_prefill_attn_f32(AttnArgs a) {
 // ---------------------------------------------------------------------------
 // launcher (called by the C ABI after validation)
 // ---------------------------------------------------------------------------
-extern "C" int hk_launch_paged_prefill_attention(int is_bf16, const hk::AttnArgs* args, int n_seqs,
+extern "C" int hk_launch_paged_prefill_attention(int dtype, const hk::AttnArgs* args, int n_seqs,
                                                  int n_qblocks, hipStream_t stream) {
     dim3 grid(args->kv_heads, n_seqs, n_qblocks);
-    if (is_bf16)
-        hipLaunchKernelGGL(hk::paged_prefill_attn_bf16, grid, dim3(256), 0, stream, *args);
+    if (dtype == hk::DT_BF16)
+        hipLaunchKernelGGL(hk::paged_prefill_attn_16<hk::bf16>, grid, dim3(256), 0, stream, *args);
+    else if (dtype == hk::DT_F16)
+        hipLaunchKernelGGL(hk::paged_prefill_attn_16<hk::f16>, grid, dim3(256), 0, stream, *args);
     else
         hipLaunchKernelGGL(hk::paged_prefill_attn_f32, grid, dim3(256), 0, stream, *args);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;

@@ -2,7 +2,7 @@
 //
 // Row-major Y[n][out] = alpha * X[n][in] . W[out][in]^T + beta * C is the column-major
 // product Y^T = W . X^T: m = out, n = n, k = in, op(A) = T on the weight, op(B) = N on the
-// activations. bf16 operands with fp32 accumulation (HIPBLAS_COMPUTE_32F), or fp32.
+// activations. bf16 or fp16 operands with fp32 accumulation (HIPBLAS_COMPUTE_32F), or fp32.
 // Plans (descriptors + the fastest of up to 16 heuristic algorithms, timed once on first
 // use of a shape) are cached per shape; the workspace is owned by the context and allocated
 // on the first GEMM.
@@ -77,7 +77,7 @@ static int pick_fastest(hk_ctx* ctx, P& p, R* res, int returned, int dtype, int 
     if (returned <= 1) return 0;
     hk_blas* B = ctx->blas;
     void* scratch = nullptr;
-    const size_t bytes = (size_t)ldy * n * (dtype == HK_BF16 ? 2 : 4);
+    const size_t bytes = (size_t)ldy * n * (dtype == HK_F32 ? 4 : 2);
     if (hipMalloc(&scratch, bytes) != hipSuccess) return 0;
     hipEvent_t e0, e1;
     hipEventCreate(&e0);
@@ -124,7 +124,7 @@ int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, l
     auto it = B->plans.find(key);
     if (it == B->plans.end()) {
         Plan p;
-        const hipDataType t = dtype == HK_BF16 ? HIP_R_16BF : HIP_R_32F;
+        const hipDataType t = dtype == HK_BF16 ? HIP_R_16BF : dtype == HK_F16 ? HIP_R_16F : HIP_R_32F;
         bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
         hipblasOperation_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
         ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)) ==

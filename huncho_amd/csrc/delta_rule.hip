@@ -21,9 +21,8 @@
 // the reduction index of each product is permuted to match the accumulator's row order
 // instead of transposing the data. Inputs stream from HBM once: q, k, v, g, beta in, o out.
 //
-// Two variants: fp32 inputs on v_mfma_f32_32x32x2_f32 (fp32 model path), and bf16 q/k/v/o
-// on v_mfma_f32_32x32x16_bf16 with fp32 accumulation, fp32 state and an fp32 solve (bf16
-// model path).
+// This file holds the fp32 variant (v_mfma_f32_32x32x2_f32, the fp32 model path); the 16-bit
+// variants and the fused Gated DeltaNet layer kernel live in gdn_v2.hip.
 #include "common.hpp"
 #include "kernel_args.hpp"
 
@@ -317,261 +316,18 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_f32(GdnArgs a) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// bf16 variant
-// ---------------------------------------------------------------------------
-constexpr int B_KSTR = DK + 8;  // bf16 row stride of Kc/Qc
-constexpr int B_TSTR = CH + 8;  // bf16 row stride of Kt (transposed k), T and Aqk
-constexpr int B_ASTR = CH + 4;  // fp32 row stride of A (aliased by T afterwards)
-constexpr size_t GDN_BF16_LDS =
-    2 * CH * B_KSTR * 2 + DK * B_TSTR * 2 + 2 * CH * B_ASTR * 4 + CH * B_TSTR * 2 + 32 * XSTR * 4 + 2 * CH * 4;
-
-// 8 bf16 operands whose reduction index g*8+i maps to accumulator rows acc_row(hh*8+i, g)
-// of a 32-block starting at column `base`: two runs of 4 (base+16hh+4g, base+16hh+8+4g).
-__device__ __forceinline__ bf16x8 ld_perm8(const bf16* row, int base, int hh, int g) {
-    bf16x4 lo = *(const bf16x4*)(row + base + 16 * hh + 4 * g);
-    bf16x4 hi = *(const bf16x4*)(row + base + 16 * hh + 8 + 4 * g);
-    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-__device__ __forceinline__ bf16x8 pack8(const f32x16& v, int hh) {
-    bf16x8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (bf16)v[hh * 8 + i];
-    return r;
-}
-
-__global__ __launch_bounds__(256, 1) void gdn_chunk_bf16(GdnArgs a) {
-    extern __shared__ __attribute__((aligned(16))) char smem_b[];
-    bf16* Kc = (bf16*)smem_b;                   // [64][136]
-    bf16* Qc = Kc + CH * B_KSTR;                // [64][136]
-    bf16* Kt = Qc + CH * B_KSTR;                // [128][72]
-    float* Am = (float*)(Kt + DK * B_TSTR);     // [64][68] fp32; bf16 T [64][72] reuses it
-    bf16* Tm = (bf16*)Am;
-    float* Tf = Am + CH * B_ASTR;               // [64][68] fp32 inverse
-    bf16* Aq = (bf16*)(Tf + CH * B_ASTR);       // [64][72]
-    float* Xs = (float*)(Aq + CH * B_TSTR);     // [32][36]
-    float* Gs = Xs + 32 * XSTR;
-    float* Bs = Gs + CH;
-
-    const int h = blockIdx.x, seq = blockIdx.y, H = a.H;
-    const int t0 = a.cu_seqlens[seq];
-    const int T = a.cu_seqlens[seq + 1] - t0;
-    if (t0 < 0 || T < 0 || t0 + T > a.n_tokens) {
-        if (threadIdx.x == 0) atomicOr(a.fault, 1);
-        return;
-    }
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, col = lane & 31;
-    const int dvc = wave * 32 + col;
-    const int kh = h / a.qk_rep;
-    const bf16* qg = (const bf16*)a.q + (long)kh * DK;
-    const bf16* kg = (const bf16*)a.k + (long)kh * DK;
-    const bf16* vg = (const bf16*)a.v + (long)h * DV;
-    bf16* og = (bf16*)a.o + (long)h * DV;
-    const long sbase = ((long)seq * H + h) * DK * DV;
-
-    f32x16 S[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-            S[rb][j] = a.initial_state ? a.initial_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] : 0.0f;
-
-    for (int c0 = 0; c0 < T; c0 += CH) {
-        const int Lc = min(CH, T - c0);
-        __syncthreads();
-        // q rows -> Qc; k rows -> Kc and transposed into Kt. Thread t handles rows
-        // 4*(t/16)+i (i = 0..3) and the 8 dims (t%16)*8.
-        {
-            const int rbase = 4 * (tid >> 4), d0 = (tid & 15) * 8;
-            uint4 kr[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = rbase + i;
-                uint4 qv = {0, 0, 0, 0}, kv = {0, 0, 0, 0};
-                if (r < Lc) {
-                    qv = *(const uint4*)(qg + (long)(t0 + c0 + r) * a.q_tok + d0);
-                    kv = *(const uint4*)(kg + (long)(t0 + c0 + r) * a.k_tok + d0);
-                }
-                *(uint4*)(Qc + r * B_KSTR + d0) = qv;
-                *(uint4*)(Kc + r * B_KSTR + d0) = kv;
-                kr[i] = kv;
-            }
-            const bf16* k0 = (const bf16*)&kr[0];
-            const bf16* k1 = (const bf16*)&kr[1];
-            const bf16* k2 = (const bf16*)&kr[2];
-            const bf16* k3 = (const bf16*)&kr[3];
-#pragma unroll
-            for (int dd = 0; dd < 8; ++dd) {
-                bf16x4 w = {k0[dd], k1[dd], k2[dd], k3[dd]};
-                *(bf16x4*)(Kt + (d0 + dd) * B_TSTR + rbase) = w;
-            }
-        }
-        if (wave == 0) {
-            float gv = 0.f, bv = 0.f;
-            if (lane < Lc) {
-                gv = a.g[(long)(t0 + c0 + lane) * a.gb_tok + h];
-                bv = a.beta[(long)(t0 + c0 + lane) * a.gb_tok + h];
-            }
-            Gs[lane] = wave_incl_scan(gv, lane);
-            Bs[lane] = bv;
-        }
-        __syncthreads();
-        if (wave < 3) {
-            const int tb = wave == 0 ? 0 : 1, sb = wave == 2 ? 1 : 0;
-            f32x16 kk = f32x16{}, qk = f32x16{};
-            const bf16* ka = Kc + (tb * 32 + col) * B_KSTR + g * 8;
-            const bf16* qa = Qc + (tb * 32 + col) * B_KSTR + g * 8;
-            const bf16* kbp = Kc + (sb * 32 + col) * B_KSTR + g * 8;
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                bf16x8 bv = *(const bf16x8*)(kbp + ks * 16);
-                kk = mfma_bf16(*(const bf16x8*)(ka + ks * 16), bv, kk);
-                qk = mfma_bf16(*(const bf16x8*)(qa + ks * 16), bv, qk);
-            }
-            const int s = sb * 32 + col;
-            const float Gs_s = Gs[s];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int t = tb * 32 + acc_row(j, g);
-                const float dec = s <= t ? __expf(Gs[t] - Gs_s) : 0.0f;
-                Am[t * B_ASTR + s] = s < t ? Bs[t] * dec * kk[j] : 0.0f;
-                Aq[t * B_TSTR + s] = (bf16)(s <= t ? dec * qk[j] : 0.0f);
-            }
-        } else {
-            for (int idx = lane; idx < 32 * 32; idx += 64) {
-                const int t = idx >> 5, s = 32 + (idx & 31);
-                Am[t * B_ASTR + s] = 0.0f;
-                Aq[t * B_TSTR + s] = (bf16)0.0f;
-            }
-        }
-        __syncthreads();
-        invert_unit_lower(Am, Tf, B_ASTR, Xs, XSTR, wave, lane);
-        // A is dead: round T to bf16 into its space
-        for (int idx = tid; idx < CH * CH; idx += 256) {
-            const int i = idx >> 6, j = idx & 63;
-            Tm[i * B_TSTR + j] = (bf16)Tf[i * B_ASTR + j];
-        }
-        // K S0 and Q S0 (S0 rounded to bf16 as the B operand)
-        bf16x8 Sb[4][2];
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            Sb[rb][0] = pack8(S[rb], 0);
-            Sb[rb][1] = pack8(S[rb], 1);
-        }
-        f32x16 ks[2], qs[2];
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            ks[tb] = f32x16{};
-            qs[tb] = f32x16{};
-            const bf16* kr = Kc + (tb * 32 + col) * B_KSTR;
-            const bf16* qr = Qc + (tb * 32 + col) * B_KSTR;
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    ks[tb] = mfma_bf16(ld_perm8(kr, rb * 32, hh, g), Sb[rb][hh], ks[tb]);
-                    qs[tb] = mfma_bf16(ld_perm8(qr, rb * 32, hh, g), Sb[rb][hh], qs[tb]);
-                }
-        }
-        f32x16 R[2];
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int t = tb * 32 + acc_row(j, g);
-                const float eg = __expf(Gs[t]);
-                const float vv = t < Lc ? (float)vg[(long)(t0 + c0 + t) * a.v_tok + dvc] : 0.0f;
-                R[tb][j] = Bs[t] * (vv - eg * ks[tb][j]);
-                qs[tb][j] *= eg;
-            }
-        __syncthreads();  // bf16 T ready
-        bf16x8 Rb[2][2];
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-            Rb[sb][0] = pack8(R[sb], 0);
-            Rb[sb][1] = pack8(R[sb], 1);
-        }
-        f32x16 dl[2];
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            dl[tb] = f32x16{};
-            const bf16* tr = Tm + (tb * 32 + col) * B_TSTR;
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) dl[tb] = mfma_bf16(ld_perm8(tr, sb * 32, hh, g), Rb[sb][hh], dl[tb]);
-        }
-        bf16x8 Db[2][2];
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-            Db[sb][0] = pack8(dl[sb], 0);
-            Db[sb][1] = pack8(dl[sb], 1);
-        }
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            const bf16* ar = Aq + (tb * 32 + col) * B_TSTR;
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) qs[tb] = mfma_bf16(ld_perm8(ar, sb * 32, hh, g), Db[sb][hh], qs[tb]);
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int t = tb * 32 + acc_row(j, g);
-                if (t < Lc) og[(long)(t0 + c0 + t) * a.o_tok + dvc] = (bf16)qs[tb][j];
-            }
-        }
-        const float glast = Gs[CH - 1];
-        const float eglast = __expf(glast);
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) dl[tb][j] *= __expf(glast - Gs[tb * 32 + acc_row(j, g)]);
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            Db[tb][0] = pack8(dl[tb], 0);
-            Db[tb][1] = pack8(dl[tb], 1);
-        }
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) S[rb][j] *= eglast;
-            const bf16* ktr = Kt + (rb * 32 + col) * B_TSTR;
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) S[rb] = mfma_bf16(ld_perm8(ktr, tb * 32, hh, g), Db[tb][hh], S[rb]);
-        }
-    }
-    if (a.final_state) {
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) a.final_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] = S[rb][j];
-    }
-}
-
 }  // namespace hk
 
-extern "C" int hk_launch_gated_delta_chunked(int is_bf16, const hk::GdnArgs* args, int n_seqs, hipStream_t stream) {
+extern "C" int hk_launch_gated_delta_chunked(int dtype, const hk::GdnArgs* args, int n_seqs, hipStream_t stream) {
+    if (dtype != hk::DT_F32) return hk_launch_gdn_v2(dtype, 0, args, nullptr, n_seqs, stream);
     dim3 grid(args->H, n_seqs);
-    if (is_bf16) {
-        static bool configured = false;
-        if (!configured) {
-            if (hipFuncSetAttribute((const void*)hk::gdn_chunk_bf16, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)hk::GDN_BF16_LDS) != hipSuccess)
-                return HK_ERR_DEVICE;
-            configured = true;
-        }
-        hipLaunchKernelGGL(hk::gdn_chunk_bf16, grid, dim3(256), hk::GDN_BF16_LDS, stream, *args);
-    } else {
-        static bool configured = false;
-        if (!configured) {
-            if (hipFuncSetAttribute((const void*)hk::gdn_chunk_f32, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)hk::GDN_F32_LDS) != hipSuccess)
-                return HK_ERR_DEVICE;
-            configured = true;
-        }
-        hipLaunchKernelGGL(hk::gdn_chunk_f32, grid, dim3(256), hk::GDN_F32_LDS, stream, *args);
+    static bool configured = false;
+    if (!configured) {
+        if (hipFuncSetAttribute((const void*)hk::gdn_chunk_f32, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)hk::GDN_F32_LDS) != hipSuccess)
+            return HK_ERR_DEVICE;
+        configured = true;
     }
+    hipLaunchKernelGGL(hk::gdn_chunk_f32, grid, dim3(256), hk::GDN_F32_LDS, stream, *args);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }

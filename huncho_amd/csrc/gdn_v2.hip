@@ -1,0 +1,508 @@
+// gdn_v2.hip - chunked gated delta rule for 16-bit activations (bf16 / fp16) on gfx950, with
+// an optional fused Gated DeltaNet prologue and epilogue.
+//
+// Recurrence (crates/huncho-backend/src/delta_cpu.rs:95-131, qwen3_5.rs:950-987), per token t:
+//   S <- S exp(g_t); delta_t = beta_t (v_t - S^T k_t); S <- S + k_t delta_t^T; o_t = S^T q_t
+// evaluated in the equal chunked form (chunk 64, G = inclusive cumsum of g in the chunk):
+//   A = strict_lower(beta_t exp(G_t - G_s) k_t.k_s),  T = (I + A)^-1
+//   delta = T [beta (V - exp(G) K S0)],  O = exp(G) Q S0 + lower(exp(G_t - G_s) q_t.k_s) delta
+//   S1 = exp(G_last) S0 + K^T [exp(G_last - G) delta]
+// State S stays in fp32 MFMA accumulators for the whole sequence (wave w owns value columns
+// 32w..32w+31); products use 16-bit operands with fp32 accumulation; T is formed in fp32.
+//
+// Two modes (template FUSED):
+//   standalone  q, k [tokens][k_heads][128], v [tokens][heads][128], g, beta fp32 -> o
+//   fused       the Gated DeltaNet layer body of LinearAttn::forward (qwen3_5.rs:846-940)
+//               straight from the fused in_proj output rows [q | k | v | z | b | a]:
+//               causal depthwise conv (K = 4, ascending taps, conv_cpu.rs:34-48) + SiLU,
+//               l2norm of q and k, q * 128^-1/2, beta = sigmoid(b),
+//               g = -exp(A_log) softplus(a + dt_bias), the recurrence, then the gated
+//               RMSNorm rms(o) * w * silu(z) (193-201) -> out_proj input
+// so one kernel streams each layer's q|k|v|z|b|a once and writes one output row per token.
+//
+// Chunk pipeline, one workgroup (4 waves) per (sequence, value head):
+//   P0  global -> LDS: q, k, v rows (row-major) and k transposed; g scan and beta
+//   P1  waves 0-2: K K^T and Q K^T blocks -> A (fp32) and Aqk; wave 3 zeroes the upper
+//       blocks; every wave: K S0, Q S0 for its columns -> R and exp(G) Q S0 in registers
+//   P2  in-place blocked inverse of I + A (four 16x16 diagonal solves, two merges)
+//   P3  delta = T R, O = exp(G) Q S0 + Aqk delta (staged in LDS), S update
+//   P4  O (or the gated-normed O) -> HBM with 16-byte stores
+#include "common.hpp"
+#include "kernel_args.hpp"
+
+namespace hk {
+namespace gdn2 {
+
+template <typename T> using Ops = Mma16<T>;
+
+template <typename T> __device__ __forceinline__ float f(T x) { return (float)x; }
+template <typename T> __device__ __forceinline__ float rnd(float x) { return (float)(T)x; }
+
+constexpr int CH = 64, DK = 128, DV = 128;
+constexpr int RS = DK + 8;  // row stride (elements) of Qc / Kc / Vc / O staging
+constexpr int TS = CH + 8;  // row stride of Kt [128][72] and Aq [64][72]
+constexpr int AS = CH + 4;  // fp32 row stride of A / T [64][68]
+constexpr int XS = 32 + 4;  // fp32 row stride of the merge scratch [32][36]
+constexpr size_t LDS_BYTES = 3 * CH * RS * 2 + DK * TS * 2 + CH * AS * 4 + CH * TS * 2 + 32 * XS * 4 + 2 * CH * 4;
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ float wave_incl_scan(float x, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        float y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
+// ---- 16x16 fp32 tiles on v_mfma_f32_16x16x4_f32 (operand lane l: row/col l % 16, reduction
+// index l / 16; accumulator lane l: column l % 16, rows 4 (l / 16) + j) ----
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+template <int K>
+__device__ __forceinline__ f32x4 tile_mm(const float* X, int ldx, const float* Y, int ldy, int lane) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const int r = lane & 15, kq = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < K; k += 4) acc = mfma16(X[r * ldx + k + kq], Y[(k + kq) * ldy + r], acc);
+    return acc;
+}
+// -W[16][16] . Xacc, pairing reduction step j with the accumulator row 4 (l / 16) + j
+__device__ __forceinline__ f32x4 tile_neg_mm_acc(const float* W, int ldw, f32x4 xacc, int lane) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const int r = lane & 15, kq = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = mfma16(-W[r * ldw + 4 * kq + j], xacc[j], acc);
+    return acc;
+}
+__device__ __forceinline__ void tile_store(float* D, int ldd, f32x4 acc, int lane) {
+    const int c = lane & 15, r0 = (lane >> 4) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) D[(r0 + j) * ldd + c] = acc[j];
+}
+
+// In-place T = (I + A)^-1 for strictly lower A [64][AS] whose upper triangle is zero.
+// Diagonal 16x16 blocks by forward substitution (wave w: block w, lane j: column j), then T10 = -T11 A10 T00 and T32 = -T33 A32 T22, then
+// T[2:4][0:2] = -T[2:4][2:4] (A[2:4][0:2] T[0:2][0:2]). Every thread must call it.
+__device__ void invert_in_place(float* Am, float* Xs, int wave, int lane) {
+    {
+        const int b = wave * 16, j = lane & 15;
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float* row = Am + (b + i) * AS + b;
+            float a0 = (i == j) ? 1.0f : 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+            for (int k = 0; k + 3 < i; k += 4) {
+                f32x4 rv = *(const f32x4*)(row + k);
+                a0 -= rv[0] * x[k];
+                a1 -= rv[1] * x[k + 1];
+                a2 -= rv[2] * x[k + 2];
+                a3 -= rv[3] * x[k + 3];
+            }
+#pragma unroll
+            for (int k = i & ~3; k < i; ++k) a0 -= row[k] * x[k];
+            x[i] = (a0 + a1) + (a2 + a3);
+        }
+        if (lane < 16) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) Am[(b + i) * AS + b + j] = x[i];
+        }
+    }
+    __syncthreads();
+    if (wave < 2) {
+        const int b = wave * 32;
+        f32x4 xa = tile_mm<16>(Am + (b + 16) * AS + b, AS, Am + b * AS + b, AS, lane);
+        f32x4 t = tile_neg_mm_acc(Am + (b + 16) * AS + b + 16, AS, xa, lane);
+        tile_store(Am + (b + 16) * AS + b, AS, t, lane);
+    }
+    __syncthreads();
+    const int rt = wave >> 1, ct = wave & 1;
+    {
+        f32x4 xa = tile_mm<32>(Am + (32 + 16 * rt) * AS, AS, Am + 16 * ct, AS, lane);
+        tile_store(Xs + 16 * rt * XS + 16 * ct, XS, xa, lane);
+    }
+    __syncthreads();
+    {
+        f32x4 t = tile_mm<32>(Am + (32 + 16 * rt) * AS + 32, AS, Xs + 16 * ct, XS, lane);
+        t = -t;
+        tile_store(Am + (32 + 16 * rt) * AS + 16 * ct, AS, t, lane);
+    }
+    __syncthreads();
+}
+
+// 8 operands whose reduction index g*8+i pairs with accumulator rows acc_row(hh*8+i, g) of the
+// 32-block at `base`: two runs of four, base+16hh+4g and base+16hh+8+4g.
+template <typename T>
+__device__ __forceinline__ typename Ops<T>::v8 ld_perm(const T* row, int base, int hh, int g) {
+    typedef typename Ops<T>::v4 v4;
+    v4 lo = *(const v4*)(row + base + 16 * hh + 4 * g);
+    v4 hi = *(const v4*)(row + base + 16 * hh + 8 + 4 * g);
+    return typename Ops<T>::v8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+template <typename T>
+__device__ __forceinline__ typename Ops<T>::v8 ld_perm_f32(const float* row, int base, int hh, int g) {
+    f32x4 lo = *(const f32x4*)(row + base + 16 * hh + 4 * g);
+    f32x4 hi = *(const f32x4*)(row + base + 16 * hh + 8 + 4 * g);
+    return typename Ops<T>::v8{(T)lo[0], (T)lo[1], (T)lo[2], (T)lo[3], (T)hi[0], (T)hi[1], (T)hi[2], (T)hi[3]};
+}
+template <typename T>
+__device__ __forceinline__ typename Ops<T>::v8 pack(const f32x16& v, int hh) {
+    typename Ops<T>::v8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (T)v[hh * 8 + i];
+    return r;
+}
+
+template <typename T, bool FUSED>
+__global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) {
+    typedef typename Ops<T>::v8 v8;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    T* Qc = (T*)smem;                       // [64][RS]; later O staging
+    T* Kc = Qc + CH * RS;                   // [64][RS]
+    T* Vc = Kc + CH * RS;                   // [64][RS]
+    T* Kt = Vc + CH * RS;                   // [128][TS]
+    float* Am = (float*)(Kt + DK * TS);     // [64][AS]: A, then T
+    T* Aq = (T*)(Am + CH * AS);             // [64][TS]
+    float* Xs = (float*)(Aq + CH * TS);     // [32][XS]
+    float* Gs = Xs + 32 * XS;
+    float* Bs = Gs + CH;
+
+    const int h = blockIdx.x, seq = blockIdx.y, H = a.H;
+    const int t0 = a.cu_seqlens[seq];
+    const int Tn = a.cu_seqlens[seq + 1] - t0;
+    if (t0 < 0 || Tn < 0 || t0 + Tn > a.n_tokens) {
+        if (threadIdx.x == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, col = lane & 31;
+    const int dvc = wave * 32 + col;
+    const int kh = h / a.qk_rep;
+    const long sbase = ((long)seq * H + h) * DK * DV;
+    // loader mapping (waves 0..2): slice = wave (q, k, v); 8 channels 8*sub..; rows 16*rg..
+    const int sub = lane & 15, rg = lane >> 4;
+
+    f32x16 S[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            S[rb][j] = a.initial_state ? a.initial_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] : 0.0f;
+
+    float convw[8][4];
+    long mcol = 0;
+    if (FUSED && wave < 3) {
+        const int key_dim = fa.Hk * 128;
+        mcol = wave == 0 ? kh * 128 : wave == 1 ? key_dim + kh * 128 : 2 * key_dim + h * 128;
+        mcol += 8 * sub;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int tap = 0; tap < 4; ++tap) convw[e][tap] = fa.conv_w[(mcol + e) * 4 + tap];
+    }
+
+    for (int c0 = 0; c0 < Tn; c0 += CH) {
+        const int Lc = min(CH, Tn - c0);
+        __syncthreads();
+        // ---------------- P0: inputs -> LDS ----------------
+        if (wave < 3) {
+            T* dst = wave == 0 ? Qc : wave == 1 ? Kc : Vc;
+            if (FUSED) {
+                // raw conv inputs for chunk rows 16rg-3 .. 16rg+15 (sequence position c0 + row);
+                // loads use a clamped position and are zeroed outside [0, Tn) afterwards
+                v8 raw[19];
+#pragma unroll
+                for (int i = 0; i < 19; ++i) {
+                    const int p = c0 + 16 * rg - 3 + i;
+                    const int pc = p < 0 ? 0 : (p >= Tn ? Tn - 1 : p);
+                    raw[i] = *(const v8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + mcol);
+                    if (p < 0 || p >= Tn) raw[i] = v8{};
+                }
+                if (fa.hist && c0 == 0 && rg == 0) {
+#pragma unroll
+                    for (int i = 0; i < 3; ++i)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            raw[i][e] = ((const T*)fa.hist)[((long)seq * fa.conv_dim + mcol + e) * 3 + i];
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    float y[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        float acc = 0.0f;
+                        acc += convw[e][0] * f(raw[i][e]);
+                        acc += convw[e][1] * f(raw[i + 1][e]);
+                        acc += convw[e][2] * f(raw[i + 2][e]);
+                        acc += convw[e][3] * f(raw[i + 3][e]);
+                        y[e] = rnd<T>(silu(acc));
+                    }
+                    if (wave < 2) {  // l2norm over the head's 128 channels (16 lanes)
+                        float ss = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+#pragma unroll
+                        for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+                        const float inv = 1.0f / sqrtf(ss + 1e-6f);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) y[e] = wave == 0 ? (y[e] * inv) * fa.scale : y[e] * inv;
+                    }
+                    const bool live = 16 * rg + i < Lc;
+                    v8 o;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[e] = live ? (T)y[e] : (T)0.0f;
+                    *(v8*)(dst + (16 * rg + i) * RS + 8 * sub) = o;
+                }
+            } else {
+                const T* src = wave == 0 ? (const T*)a.q + (long)kh * DK
+                             : wave == 1 ? (const T*)a.k + (long)kh * DK : (const T*)a.v + (long)h * DV;
+                const long tok = wave == 0 ? a.q_tok : wave == 1 ? a.k_tok : a.v_tok;
+                v8 x[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int r = 16 * rg + i;
+                    x[i] = *(const v8*)(src + (long)(t0 + c0 + (r < Lc ? r : Lc - 1)) * tok + 8 * sub);
+                    if (r >= Lc) x[i] = v8{};
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) *(v8*)(dst + (16 * rg + i) * RS + 8 * sub) = x[i];
+            }
+        } else {
+            float gv = 0.0f, bv = 0.0f;
+            if (lane < Lc) {
+                const long tt = t0 + c0 + lane;
+                if (FUSED) {
+                    const T* row = (const T*)fa.ba + tt * fa.ba_tok;
+                    const float b = f(row[fa.b_col + h]);
+                    const float av = f(row[fa.a_col + h]);
+                    bv = rnd<T>(1.0f / (1.0f + __expf(-b)));
+                    gv = fa.base_g[h] * __logf(__expf(av + fa.dt_bias[h]) + 1.0f);
+                } else {
+                    gv = a.g[tt * a.gb_tok + h];
+                    bv = a.beta[tt * a.gb_tok + h];
+                }
+            }
+            Gs[lane] = wave_incl_scan(gv, lane);
+            Bs[lane] = bv;
+        }
+        __syncthreads();
+        // ---------------- P1: A, Aqk; K S0, Q S0 ----------------
+        {  // k transposed for the state update (read in P3, after the inversion's barriers):
+            // thread t moves rows 4*(t/16)..+3, channels 8*(t%16)..+7
+            typedef typename Ops<T>::v4 v4;
+            const int r0 = 4 * (tid >> 4), d0 = 8 * (tid & 15);
+            v8 k0 = *(const v8*)(Kc + (r0 + 0) * RS + d0);
+            v8 k1 = *(const v8*)(Kc + (r0 + 1) * RS + d0);
+            v8 k2 = *(const v8*)(Kc + (r0 + 2) * RS + d0);
+            v8 k3 = *(const v8*)(Kc + (r0 + 3) * RS + d0);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) *(v4*)(Kt + (d0 + e) * TS + r0) = v4{k0[e], k1[e], k2[e], k3[e]};
+        }
+        if (wave < 3) {
+            const int tb = wave == 0 ? 0 : 1, sb = wave == 2 ? 1 : 0;
+            f32x16 kk = f32x16{}, qk = f32x16{};
+            const T* ka = Kc + (tb * 32 + col) * RS + g * 8;
+            const T* qa = Qc + (tb * 32 + col) * RS + g * 8;
+            const T* kbp = Kc + (sb * 32 + col) * RS + g * 8;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                v8 bv = *(const v8*)(kbp + ks * 16);
+                kk = Ops<T>::mma(*(const v8*)(ka + ks * 16), bv, kk);
+                qk = Ops<T>::mma(*(const v8*)(qa + ks * 16), bv, qk);
+            }
+            const int s = sb * 32 + col;
+            const float gs = Gs[s];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = tb * 32 + acc_row(j, g);
+                const float dec = s <= t ? __expf(Gs[t] - gs) : 0.0f;
+                Am[t * AS + s] = s < t ? Bs[t] * dec * kk[j] : 0.0f;
+                Aq[t * TS + s] = (T)(dec * qk[j]);
+            }
+        } else {
+            for (int idx = lane; idx < 32 * 32; idx += 64) {
+                const int t = idx >> 5, s = 32 + (idx & 31);
+                Am[t * AS + s] = 0.0f;
+                Aq[t * TS + s] = (T)0.0f;
+            }
+        }
+        v8 Sb[4][2];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            Sb[rb][0] = pack<T>(S[rb], 0);
+            Sb[rb][1] = pack<T>(S[rb], 1);
+        }
+        f32x16 R[2], Og[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            f32x16 ks = f32x16{}, qs = f32x16{};
+            const T* kr = Kc + (tb * 32 + col) * RS;
+            const T* qr = Qc + (tb * 32 + col) * RS;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    ks = Ops<T>::mma(ld_perm<T>(kr, rb * 32, hh, g), Sb[rb][hh], ks);
+                    qs = Ops<T>::mma(ld_perm<T>(qr, rb * 32, hh, g), Sb[rb][hh], qs);
+                }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = tb * 32 + acc_row(j, g);
+                const float eg = __expf(Gs[t]);
+                R[tb][j] = Bs[t] * (f(Vc[t * RS + dvc]) - eg * ks[j]);
+                Og[tb][j] = eg * qs[j];
+            }
+        }
+        __syncthreads();
+        // ---------------- P2: T = (I + A)^-1 in place ----------------
+        invert_in_place(Am, Xs, wave, lane);
+        // ---------------- P3: delta, O, state ----------------
+        v8 Rb[2][2];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            Rb[sb][0] = pack<T>(R[sb], 0);
+            Rb[sb][1] = pack<T>(R[sb], 1);
+        }
+        f32x16 dl[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            dl[tb] = f32x16{};
+            const float* tr = Am + (tb * 32 + col) * AS;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) dl[tb] = Ops<T>::mma(ld_perm_f32<T>(tr, sb * 32, hh, g), Rb[sb][hh], dl[tb]);
+        }
+        v8 Db[2][2];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            Db[sb][0] = pack<T>(dl[sb], 0);
+            Db[sb][1] = pack<T>(dl[sb], 1);
+        }
+        T* Os = Qc;  // Q is no longer read in this chunk
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            const T* ar = Aq + (tb * 32 + col) * TS;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) Og[tb] = Ops<T>::mma(ld_perm<T>(ar, sb * 32, hh, g), Db[sb][hh], Og[tb]);
+        }
+        // every wave finished reading Qc (K S0 / Q S0) before the inversion's barriers
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) Os[(tb * 32 + acc_row(j, g)) * RS + dvc] = (T)Og[tb][j];
+        const float glast = Gs[CH - 1];
+        const float eglast = __expf(glast);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) dl[tb][j] *= __expf(glast - Gs[tb * 32 + acc_row(j, g)]);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            Db[tb][0] = pack<T>(dl[tb], 0);
+            Db[tb][1] = pack<T>(dl[tb], 1);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) S[rb][j] *= eglast;
+            const T* ktr = Kt + (rb * 32 + col) * TS;
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) S[rb] = Ops<T>::mma(ld_perm<T>(ktr, tb * 32, hh, g), Db[tb][hh], S[rb]);
+        }
+        __syncthreads();
+        // ---------------- P4: O -> HBM (gated RMSNorm when fused) ----------------
+        {
+            const int rsub = tid & 15, rrow = tid >> 4;  // 16 lanes per row, 16 rows per pass
+#pragma unroll
+            for (int pass = 0; pass < 4; ++pass) {
+                const int r = pass * 16 + rrow;
+                v8 ov = *(const v8*)(Os + r * RS + 8 * rsub);
+                const long tt = t0 + c0 + r;
+                if (FUSED) {
+                    float x[8], ss = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        x[e] = f(ov[e]);
+                        ss += x[e] * x[e];
+                    }
+#pragma unroll
+                    for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+                    if (r < Lc) {
+                        const float denom = sqrtf(ss / 128.0f + fa.eps);
+                        v8 zv = *(const v8*)((const T*)fa.z + tt * fa.z_tok + (long)h * DV + 8 * rsub);
+                        v8 y;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            y[e] = (T)(((x[e] / denom) * fa.norm_w[8 * rsub + e]) * silu(f(zv[e])));
+                        *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
+                    }
+                } else if (r < Lc) {
+                    *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = ov;
+                }
+            }
+        }
+    }
+    if (a.final_state) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a.final_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] = S[rb][j];
+    }
+    if (FUSED && fa.tail_out && wave < 3) {
+        // cache tail: the last 3 raw conv inputs of [history, sequence] for this lane's channels
+        if (rg == 0) {
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const int p = Tn - 3 + i;
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+                if (p >= 0) {
+                    v8 x = *(const v8*)((const T*)fa.mixed + (long)(t0 + p) * fa.mixed_tok + mcol);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = f(x[e]);
+                } else if (fa.hist) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        v[e] = f(((const T*)fa.hist)[((long)seq * fa.conv_dim + mcol + e) * 3 + (p + 3)]);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ((T*)fa.tail_out)[((long)seq * fa.conv_dim + mcol + e) * 3 + i] = (T)v[e];
+            }
+        }
+    }
+}
+
+}  // namespace gdn2
+}  // namespace hk
+
+template <typename T, bool FUSED>
+static int launch_v2(const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs, hipStream_t stream) {
+    static bool configured = false;
+    auto kern = hk::gdn2::gdn_chunk<T, FUSED>;
+    if (!configured) {
+        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)hk::gdn2::LDS_BYTES) != hipSuccess)
+            return HK_ERR_DEVICE;
+        configured = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(a->H, n_seqs), dim3(256), hk::gdn2::LDS_BYTES, stream, *a, *fa);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+// dtype16: 1 = bf16, 2 = fp16
+extern "C" int hk_launch_gdn_v2(int dtype16, int fused, const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs,
+                                hipStream_t stream) {
+    hk::GdnFusedArgs none{};
+    if (!fa) fa = &none;
+    if (dtype16 == 1)
+        return fused ? launch_v2<hk::bf16, true>(a, fa, n_seqs, stream) : launch_v2<hk::bf16, false>(a, fa, n_seqs, stream);
+    return fused ? launch_v2<hk::f16, true>(a, fa, n_seqs, stream) : launch_v2<hk::f16, false>(a, fa, n_seqs, stream);
+}

@@ -46,6 +46,27 @@ struct GdnArgs {
     int* fault;
 };
 
+// Gated DeltaNet layer body read straight from the fused in_proj output (gdn_v2 FUSED mode).
+struct GdnFusedArgs {
+    const void* mixed;     // token rows [q(Hk*128) | k(Hk*128) | v(H*128) | ...]
+    long mixed_tok;
+    const float* conv_w;   // [conv_dim][4]
+    int conv_dim;
+    const void* hist;      // [n_seqs][conv_dim][3] cached conv tail or null
+    void* tail_out;        // [n_seqs][conv_dim][3] new tail or null
+    const void* ba;        // b at column b_col, a at column a_col of each token row
+    long ba_tok;
+    int b_col, a_col;
+    const float* base_g;   // -exp(A_log) [H]
+    const float* dt_bias;  // [H]
+    float scale;           // q scale (128^-1/2)
+    int Hk;
+    const void* z;         // gate z at [t * z_tok + h * 128 + i]
+    long z_tok;
+    const float* norm_w;   // [128] gated-norm weight
+    float eps;
+};
+
 struct KvArgs {
     const void* q_in;
     long q_in_tok, q_in_head;
@@ -126,17 +147,19 @@ struct SwigluArgs {
 }  // namespace hk
 
 extern "C" {
-int hk_launch_paged_prefill_attention(int is_bf16, const hk::AttnArgs* args, int n_seqs, int n_qblocks,
+int hk_launch_paged_prefill_attention(int dtype, const hk::AttnArgs* args, int n_seqs, int n_qblocks,
                                       hipStream_t stream);
-int hk_launch_gated_delta_chunked(int is_bf16, const hk::GdnArgs* args, int n_seqs, hipStream_t stream);
-int hk_launch_qk_norm_rope_kv_write(int is_bf16, const hk::KvArgs* args, hipStream_t stream);
-int hk_launch_gdn_prep(int is_bf16, const hk::PrepArgs* a, void* tail_out, hipStream_t st);
-int hk_launch_rms_norm(int is_bf16, const hk::NormArgs* a, hipStream_t st);
-int hk_launch_gated_rms_norm(int is_bf16, const hk::GatedNormArgs* a, hipStream_t st);
-int hk_launch_swiglu(int is_bf16, const hk::SwigluArgs* a, hipStream_t st);
-int hk_launch_embed(int is_bf16, const int* ids, int n, const void* table, int vocab, int width, void* out, int* fault,
+int hk_launch_gated_delta_chunked(int dtype, const hk::GdnArgs* args, int n_seqs, hipStream_t stream);
+int hk_launch_gdn_v2(int dtype16, int fused, const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs,
+                     hipStream_t stream);
+int hk_launch_qk_norm_rope_kv_write(int dtype, const hk::KvArgs* args, hipStream_t stream);
+int hk_launch_gdn_prep(int dtype, const hk::PrepArgs* a, void* tail_out, hipStream_t st);
+int hk_launch_rms_norm(int dtype, const hk::NormArgs* a, hipStream_t st);
+int hk_launch_gated_rms_norm(int dtype, const hk::GatedNormArgs* a, hipStream_t st);
+int hk_launch_swiglu(int dtype, const hk::SwigluArgs* a, hipStream_t st);
+int hk_launch_embed(int dtype, const int* ids, int n, const void* table, int vocab, int width, void* out, int* fault,
                     hipStream_t st);
-int hk_launch_final_norm_head(int is_bf16, const void* x, long x_tok, const int* cu, int n_seqs, const float* w_eff,
+int hk_launch_final_norm_head(int dtype, const void* x, long x_tok, const int* cu, int n_seqs, const float* w_eff,
                               float eps, int width, const void* head_w, const float* head_b, int n_out, float* logits,
                               void* h_out, hipStream_t st);
 int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st);

@@ -76,7 +76,7 @@ static int read_as_f32(hk_kev_model* m, const void* src, size_t count, std::vect
     std::vector<uint16_t> tmp(count);
     if (int rc = hk_check_hip(m->ctx, hipMemcpy(tmp.data(), src, count * 2, hipMemcpyDeviceToHost), "weight read"))
         return rc;
-    for (size_t i = 0; i < count; ++i) out[i] = bf16_to_f32(tmp[i]);
+    for (size_t i = 0; i < count; ++i) out[i] = m->dtype == HK_F16 ? hk_host_f16_to_f32(tmp[i]) : bf16_to_f32(tmp[i]);
     return HK_OK;
 }
 
@@ -128,7 +128,7 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
                                    hk_kev_model** out) {
     if (!ctx || !cfg || !lw || !embed || !final_norm || !out) return HK_ERR_INVALID;
     *out = nullptr;
-    if (dtype != HK_BF16 && dtype != HK_F32) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d", dtype);
+    if (dtype != HK_BF16 && dtype != HK_F16 && dtype != HK_F32) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d", dtype);
     const hk_kev_config& c = *cfg;
     if (c.head_dim != 128 || c.lin_key_dim != 128 || c.lin_v_dim != 128)
         return hk_fail(ctx, HK_ERR_UNSUPPORTED, "head dims must be 128 (got %d/%d/%d)", c.head_dim, c.lin_key_dim,
@@ -143,7 +143,7 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
     hk_kev_model* m = new hk_kev_model();
     m->ctx = ctx;
     m->dtype = dtype;
-    m->esz = dtype == HK_BF16 ? 2 : 4;
+    m->esz = dtype == HK_F32 ? 4 : 2;
     m->cfg = c;
     m->layer_types.assign(c.layer_types_host, c.layer_types_host + c.n_layers);
     m->cfg.layer_types_host = m->layer_types.data();
@@ -204,7 +204,7 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
     {
         const int half = c.rotary_dim / 2;
         std::vector<float> cs((size_t)c.max_context * half), sn((size_t)c.max_context * half);
-        hk_rope_fill_table(c.rotary_dim, c.rope_theta, c.max_context, dtype == HK_BF16, cs.data(), sn.data());
+        hk_rope_fill_table(c.rotary_dim, c.rope_theta, c.max_context, dtype, cs.data(), sn.data());
         if ((rc = upload_f32(m, cs, &m->rope_cos)) || (rc = upload_f32(m, sn, &m->rope_sin))) return fail(rc);
     }
     *out = m;
@@ -307,13 +307,13 @@ extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t
     Buffers b = carve(m, ws, n, n_seqs, num_pages);
     if (ws.off > workspace_bytes) return hk_fail(ctx, HK_ERR_INVALID, "workspace too small: %zu < %zu", workspace_bytes, ws.off);
     hipSetDevice(ctx->device);
-    const int dt = m->dtype, isb = dt == HK_BF16;
+    const int dt = m->dtype;
     const size_t e = m->esz;
     const int H = c.hidden, I = c.intermediate, hd = c.head_dim;
     const int Hq = c.n_heads, Hkv = c.n_kv_heads, Hv = c.lin_n_v_heads, Hk = c.lin_n_k_heads;
 
     RUN(hk_launch_seq_lens(cu_dev, n_seqs, b.ctx_lens, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "seq_lens") : 0);
-    RUN(hk_launch_embed(isb, ids, n, m->embed, c.vocab, H, b.x, ctx->fault_dev, ctx->stream)
+    RUN(hk_launch_embed(dt, ids, n, m->embed, c.vocab, H, b.x, ctx->fault_dev, ctx->stream)
             ? hk_fail(ctx, HK_ERR_DEVICE, "embed launch")
             : 0);
     for (int l = 0; l < c.n_layers; ++l) {
@@ -322,14 +322,21 @@ extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t
         if (L.type == 0) {
             const int rows = m->gdn_rows;
             RUN(hk_gemm_xwt(ctx, dt, n, rows, H, b.h, H, L.w_in, H, b.big, rows, nullptr, 0, 1.0f, 0.0f));
-            RUN(hk_gdn_prep(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, b.big, rows,
-                            m->conv_dim + m->value_dim, m->conv_dim + m->value_dim + Hv, L.base_g, L.dt_bias, cu_dev,
-                            n_seqs, n, Hv, Hk, b.q, b.k, b.v, b.g, b.beta, nullptr));
-            RUN(hk_gated_delta_chunked(ctx, dt, b.q, (long)Hk * 128, b.k, (long)Hk * 128, b.v, (long)Hv * 128, b.g,
-                                       b.beta, cu_dev, n_seqs, n, Hv, Hk, 128, 128, nullptr, nullptr, b.o,
-                                       (long)Hv * 128));
-            RUN(hk_gated_rms_norm(ctx, dt, b.o, (char*)b.big + (size_t)m->conv_dim * e, rows, Hv, L.norm_w, c.eps,
-                                  n * Hv, 128, b.o));
+            const int b_col = m->conv_dim + m->value_dim, a_col = b_col + Hv;
+            if (dt != HK_F32 && c.conv_k == 4 && rows % 8 == 0) {
+                // one kernel: conv + SiLU + l2norm + beta/g + chunked delta rule + gated RMSNorm
+                RUN(hk_gdn_fused(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, nullptr, b.big, rows, b_col, a_col,
+                                 L.base_g, L.dt_bias, (char*)b.big + (size_t)m->conv_dim * e, rows, L.norm_w, c.eps,
+                                 cu_dev, n_seqs, n, Hv, Hk, nullptr, nullptr, b.o, (long)Hv * 128));
+            } else {
+                RUN(hk_gdn_prep(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, b.big, rows, b_col, a_col, L.base_g,
+                                L.dt_bias, cu_dev, n_seqs, n, Hv, Hk, b.q, b.k, b.v, b.g, b.beta, nullptr));
+                RUN(hk_gated_delta_chunked(ctx, dt, b.q, (long)Hk * 128, b.k, (long)Hk * 128, b.v, (long)Hv * 128,
+                                           b.g, b.beta, cu_dev, n_seqs, n, Hv, Hk, 128, 128, nullptr, nullptr, b.o,
+                                           (long)Hv * 128));
+                RUN(hk_gated_rms_norm(ctx, dt, b.o, (char*)b.big + (size_t)m->conv_dim * e, rows, Hv, L.norm_w, c.eps,
+                                      n * Hv, 128, b.o));
+            }
             RUN(hk_gemm_xwt(ctx, dt, n, H, m->value_dim, b.o, m->value_dim, L.w_out, m->value_dim, b.x, H, b.x, H, 1.0f,
                             1.0f));
         } else {
@@ -354,7 +361,7 @@ extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t
         RUN(hk_gemm_xwt(ctx, dt, n, H, I, b.act, I, L.w_down, I, b.x, H, b.x, H, 1.0f, 1.0f));
     }
     if (c.n_out > 0 || hidden_last) {
-        RUN(hk_launch_final_norm_head(isb, b.x, H, cu_dev, n_seqs, m->final_norm, c.eps, H, m->head_w, m->head_b,
+        RUN(hk_launch_final_norm_head(dt, b.x, H, cu_dev, n_seqs, m->final_norm, c.eps, H, m->head_w, m->head_b,
                                       c.n_out, logits, hidden_last, ctx->stream)
                 ? hk_fail(ctx, HK_ERR_DEVICE, "final head launch")
                 : 0);

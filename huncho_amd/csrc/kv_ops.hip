@@ -209,19 +209,25 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_write_vec(KvArgs a) {
 
 }  // namespace hk
 
-extern "C" int hk_launch_qk_norm_rope_kv_write(int is_bf16, const hk::KvArgs* args, hipStream_t stream) {
+extern "C" int hk_launch_qk_norm_rope_kv_write(int dtype, const hk::KvArgs* args, hipStream_t stream) {
     if (args->n_tokens == 0) return HK_OK;
     const bool aligned = ((args->q_in_tok | args->q_in_head | args->k_in_tok | args->v_in_tok | args->q_out_tok |
                            args->q_out_head) % 8) == 0 &&
                          (((uintptr_t)args->q_in | (uintptr_t)args->k_in | (uintptr_t)args->v_in |
                            (uintptr_t)args->q_out | (uintptr_t)args->k_pool | (uintptr_t)args->v_pool) & 15) == 0;
-    if (is_bf16 && aligned && (!args->rope_cos || args->rd % 16 == 0)) {
+    if (dtype != hk::DT_F32 && aligned && (!args->rope_cos || args->rd % 16 == 0)) {
         const long items = (long)args->n_tokens * (args->q_heads + args->kv_heads);
-        hipLaunchKernelGGL(hk::qk_norm_rope_kv_write_vec<hk::bf16>, dim3((unsigned)((items + 15) / 16)), dim3(256), 0,
-                           stream, *args);
+        if (dtype == hk::DT_BF16)
+            hipLaunchKernelGGL(hk::qk_norm_rope_kv_write_vec<hk::bf16>, dim3((unsigned)((items + 15) / 16)), dim3(256),
+                               0, stream, *args);
+        else
+            hipLaunchKernelGGL(hk::qk_norm_rope_kv_write_vec<hk::f16>, dim3((unsigned)((items + 15) / 16)), dim3(256),
+                               0, stream, *args);
         return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
     }
-    if (is_bf16)
+    if (dtype == hk::DT_F16)
+        hipLaunchKernelGGL(hk::qk_norm_rope_kv_write<hk::f16>, dim3(args->n_tokens), dim3(256), 0, stream, *args);
+    else if (dtype == hk::DT_BF16)
         hipLaunchKernelGGL(hk::qk_norm_rope_kv_write<hk::bf16>, dim3(args->n_tokens), dim3(256), 0, stream, *args);
     else
         hipLaunchKernelGGL(hk::qk_norm_rope_kv_write<float>, dim3(args->n_tokens), dim3(256), 0, stream, *args);

@@ -339,19 +339,21 @@ __global__ __launch_bounds__(256) void swiglu(SwigluArgs a) {
     }
 }
 
-// bf16 fast path: 8 elements per thread with 16-byte accesses (width % 8 == 0).
-__global__ __launch_bounds__(256) void swiglu_bf16x8(SwigluArgs a) {
+// 16-bit fast path: 8 elements per thread with 16-byte accesses (width % 8 == 0).
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_x8(SwigluArgs a) {
+    typedef typename Mma16<T>::v8 v8;
     const int w8 = a.width >> 3;
     const long n = (long)a.rows * w8;
     for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
         const long r = idx / w8, i = (idx % w8) * 8;
-        const bf16* row = (const bf16*)a.gu + r * a.gu_tok;
-        bf16x8 gv = *(const bf16x8*)(row + i);
-        bf16x8 uv = *(const bf16x8*)(row + a.up_off + i);
-        bf16x8 out;
+        const T* row = (const T*)a.gu + r * a.gu_tok;
+        v8 gv = *(const v8*)(row + i);
+        v8 uv = *(const v8*)(row + a.up_off + i);
+        v8 out;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] = (bf16)((float)(bf16)silu((float)gv[e]) * (float)uv[e]);
-        *(bf16x8*)((bf16*)a.y + r * a.width + i) = out;
+        for (int e = 0; e < 8; ++e) out[e] = (T)((float)(T)silu((float)gv[e]) * (float)uv[e]);
+        *(v8*)((T*)a.y + r * a.width + i) = out;
     }
 }
 
@@ -402,93 +404,100 @@ __global__ void final_norm_head(const void* x, long x_tok, const int* cu, const 
 
 using namespace hk;
 
-extern "C" int hk_launch_gdn_prep(int is_bf16, const PrepArgs* a, void* tail_out, hipStream_t st) {
+#define HK_DISPATCH3(KERNEL, GRID, BLOCK, ...)                                 \
+    do {                                                                        \
+        if (dtype == DT_BF16)                                                   \
+            hipLaunchKernelGGL(KERNEL<bf16>, GRID, BLOCK, 0, st, __VA_ARGS__);  \
+        else if (dtype == DT_F16)                                               \
+            hipLaunchKernelGGL(KERNEL<f16>, GRID, BLOCK, 0, st, __VA_ARGS__);   \
+        else                                                                    \
+            hipLaunchKernelGGL(KERNEL<float>, GRID, BLOCK, 0, st, __VA_ARGS__); \
+    } while (0)
+
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int hk_launch_gdn_prep(int dtype, const PrepArgs* a, void* tail_out, hipStream_t st) {
     const int conv_dim_v = (2 * a->Hk + a->Hv) * HW;
-    if (a->n_tokens > 0 && is_bf16 && a->K == 4 && a->mixed_tok % 8 == 0 && ((uintptr_t)a->mixed & 15) == 0) {
+    if (a->n_tokens > 0 && dtype != DT_F32 && a->K == 4 && a->mixed_tok % 8 == 0 && al16(a->mixed)) {
         dim3 grid((a->n_tokens + PREP_TB - 1) / PREP_TB, (conv_dim_v + 2047) / 2048);
-        hipLaunchKernelGGL(gdn_prep_vec4<bf16>, grid, dim3(256), 0, st, *a);
-    } else if (a->n_tokens > 0) {
-        if (is_bf16)
-            hipLaunchKernelGGL(gdn_prep<bf16>, dim3(a->n_tokens), dim3(256), 0, st, *a);
+        if (dtype == DT_BF16)
+            hipLaunchKernelGGL(gdn_prep_vec4<bf16>, grid, dim3(256), 0, st, *a);
         else
-            hipLaunchKernelGGL(gdn_prep<float>, dim3(a->n_tokens), dim3(256), 0, st, *a);
+            hipLaunchKernelGGL(gdn_prep_vec4<f16>, grid, dim3(256), 0, st, *a);
+    } else if (a->n_tokens > 0) {
+        HK_DISPATCH3(gdn_prep, dim3(a->n_tokens), dim3(256), *a);
     }
     if (tail_out) {
-        const int conv_dim = (2 * a->Hk + a->Hv) * HW;
-        dim3 grid((conv_dim + 255) / 256, a->n_seqs);
-        if (is_bf16)
-            hipLaunchKernelGGL(conv_tail<bf16>, grid, dim3(256), 0, st, *a, tail_out, conv_dim);
-        else
-            hipLaunchKernelGGL(conv_tail<float>, grid, dim3(256), 0, st, *a, tail_out, conv_dim);
+        dim3 grid((conv_dim_v + 255) / 256, a->n_seqs);
+        HK_DISPATCH3(conv_tail, grid, dim3(256), *a, tail_out, conv_dim_v);
     }
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
-extern "C" int hk_launch_rms_norm(int is_bf16, const NormArgs* a, hipStream_t st) {
+extern "C" int hk_launch_rms_norm(int dtype, const NormArgs* a, hipStream_t st) {
     if (a->rows == 0) return HK_OK;
     dim3 grid((a->rows + 3) / 4);
-    const bool aligned = ((uintptr_t)a->x & 15) == 0 && ((uintptr_t)a->y & 15) == 0 && a->x_tok % 8 == 0 &&
-                         a->y_tok % 8 == 0;
-    if (is_bf16 && aligned && a->width == 1024)
-        hipLaunchKernelGGL((rms_norm_vec<bf16, 2>), grid, dim3(256), 0, st, *a);
-    else if (is_bf16 && aligned && a->width == 2048)
-        hipLaunchKernelGGL((rms_norm_vec<bf16, 4>), grid, dim3(256), 0, st, *a);
-    else if (is_bf16 && aligned && a->width == 512)
-        hipLaunchKernelGGL((rms_norm_vec<bf16, 1>), grid, dim3(256), 0, st, *a);
-    else if (is_bf16)
-        hipLaunchKernelGGL(rms_norm<bf16>, grid, dim3(256), 0, st, *a);
-    else
-        hipLaunchKernelGGL(rms_norm<float>, grid, dim3(256), 0, st, *a);
+    const bool vec = dtype != DT_F32 && al16(a->x) && al16(a->y) && a->x_tok % 8 == 0 && a->y_tok % 8 == 0 &&
+                     (a->width == 512 || a->width == 1024 || a->width == 2048);
+    if (vec) {
+        const int n8 = a->width / 512;
+        if (dtype == DT_BF16) {
+            if (n8 == 1) hipLaunchKernelGGL((rms_norm_vec<bf16, 1>), grid, dim3(256), 0, st, *a);
+            if (n8 == 2) hipLaunchKernelGGL((rms_norm_vec<bf16, 2>), grid, dim3(256), 0, st, *a);
+            if (n8 == 4) hipLaunchKernelGGL((rms_norm_vec<bf16, 4>), grid, dim3(256), 0, st, *a);
+        } else {
+            if (n8 == 1) hipLaunchKernelGGL((rms_norm_vec<f16, 1>), grid, dim3(256), 0, st, *a);
+            if (n8 == 2) hipLaunchKernelGGL((rms_norm_vec<f16, 2>), grid, dim3(256), 0, st, *a);
+            if (n8 == 4) hipLaunchKernelGGL((rms_norm_vec<f16, 4>), grid, dim3(256), 0, st, *a);
+        }
+    } else {
+        HK_DISPATCH3(rms_norm, grid, dim3(256), *a);
+    }
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
-extern "C" int hk_launch_gated_rms_norm(int is_bf16, const GatedNormArgs* a, hipStream_t st) {
+extern "C" int hk_launch_gated_rms_norm(int dtype, const GatedNormArgs* a, hipStream_t st) {
     if (a->rows == 0) return HK_OK;
-    dim3 grid((a->rows + 3) / 4);
-    if (is_bf16 && a->width == 128 && ((uintptr_t)a->x & 15) == 0 && ((uintptr_t)a->z & 15) == 0 &&
-        ((uintptr_t)a->y & 15) == 0 && a->z_tok % 8 == 0)
-        hipLaunchKernelGGL(gated_rms_norm_vec128<bf16>, dim3((a->rows + 15) / 16), dim3(256), 0, st, *a);
-    else if (is_bf16)
-        hipLaunchKernelGGL(gated_rms_norm<bf16>, grid, dim3(256), 0, st, *a);
-    else
-        hipLaunchKernelGGL(gated_rms_norm<float>, grid, dim3(256), 0, st, *a);
+    if (dtype != DT_F32 && a->width == 128 && al16(a->x) && al16(a->z) && al16(a->y) && a->z_tok % 8 == 0) {
+        dim3 grid((a->rows + 15) / 16);
+        if (dtype == DT_BF16)
+            hipLaunchKernelGGL(gated_rms_norm_vec128<bf16>, grid, dim3(256), 0, st, *a);
+        else
+            hipLaunchKernelGGL(gated_rms_norm_vec128<f16>, grid, dim3(256), 0, st, *a);
+    } else {
+        HK_DISPATCH3(gated_rms_norm, dim3((a->rows + 3) / 4), dim3(256), *a);
+    }
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
-extern "C" int hk_launch_swiglu(int is_bf16, const SwigluArgs* a, hipStream_t st) {
+extern "C" int hk_launch_swiglu(int dtype, const SwigluArgs* a, hipStream_t st) {
     if (a->rows == 0) return HK_OK;
-    const bool vec = is_bf16 && a->width % 8 == 0 && a->gu_tok % 8 == 0 && a->up_off % 8 == 0;
+    const bool vec = dtype != DT_F32 && a->width % 8 == 0 && a->gu_tok % 8 == 0 && a->up_off % 8 == 0 && al16(a->gu) &&
+                     al16(a->y);
     const long work = vec ? (long)a->rows * a->width / 8 : (long)a->rows * a->width;
     const int blocks = (int)((work + 255) / 256 < 65536 ? (work + 255) / 256 : 65536);
-    if (vec)
-        hipLaunchKernelGGL(swiglu_bf16x8, dim3(blocks), dim3(256), 0, st, *a);
-    else if (is_bf16)
-        hipLaunchKernelGGL(swiglu<bf16>, dim3(blocks), dim3(256), 0, st, *a);
+    if (vec && dtype == DT_BF16)
+        hipLaunchKernelGGL(swiglu_x8<bf16>, dim3(blocks), dim3(256), 0, st, *a);
+    else if (vec)
+        hipLaunchKernelGGL(swiglu_x8<f16>, dim3(blocks), dim3(256), 0, st, *a);
     else
-        hipLaunchKernelGGL(swiglu<float>, dim3(blocks), dim3(256), 0, st, *a);
+        HK_DISPATCH3(swiglu, dim3(blocks), dim3(256), *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
-extern "C" int hk_launch_embed(int is_bf16, const int* ids, int n, const void* table, int vocab, int width, void* out,
+extern "C" int hk_launch_embed(int dtype, const int* ids, int n, const void* table, int vocab, int width, void* out,
                                int* fault, hipStream_t st) {
     if (n == 0) return HK_OK;
-    if (is_bf16)
-        hipLaunchKernelGGL(embed_gather<bf16>, dim3(n), dim3(128), 0, st, ids, n, table, vocab, width, out, fault);
-    else
-        hipLaunchKernelGGL(embed_gather<float>, dim3(n), dim3(128), 0, st, ids, n, table, vocab, width, out, fault);
+    HK_DISPATCH3(embed_gather, dim3(n), dim3(128), ids, n, table, vocab, width, out, fault);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
-extern "C" int hk_launch_final_norm_head(int is_bf16, const void* x, long x_tok, const int* cu, int n_seqs,
+extern "C" int hk_launch_final_norm_head(int dtype, const void* x, long x_tok, const int* cu, int n_seqs,
                                          const float* w_eff, float eps, int width, const void* head_w,
                                          const float* head_b, int n_out, float* logits, void* h_out, hipStream_t st) {
     if (n_seqs == 0) return HK_OK;
-    if (is_bf16)
-        hipLaunchKernelGGL(final_norm_head<bf16>, dim3(n_seqs), dim3(64), 0, st, x, x_tok, cu, w_eff, eps, width,
-                           head_w, head_b, n_out, logits, h_out);
-    else
-        hipLaunchKernelGGL(final_norm_head<float>, dim3(n_seqs), dim3(64), 0, st, x, x_tok, cu, w_eff, eps, width,
-                           head_w, head_b, n_out, logits, h_out);
+    HK_DISPATCH3(final_norm_head, dim3(n_seqs), dim3(64), x, x_tok, cu, w_eff, eps, width, head_w, head_b, n_out,
+                 logits, h_out);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 

@@ -18,7 +18,7 @@ import numpy as np
 import torch
 
 from . import abi
-from .abi import HK_BF16, HK_F32, KevConfig, KevLayerWeights
+from .abi import HK_BF16, HK_F16, HK_F32, KevConfig, KevLayerWeights
 
 PREFIX = "model.language_model."
 MAX_ROWS = 64  # BatchLimits { max_rows: 64 } (crates/huncho-core/src/backend.rs:107-119)
@@ -115,14 +115,14 @@ _LAYER_NAME = {
 
 
 def _to_device(a: np.ndarray, dtype: torch.dtype, device) -> torch.Tensor:
-    if a.dtype == np.uint16:
+    if a.dtype == np.uint16:  # bf16 checkpoint bits; loaded into the model dtype
         t = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
-        if dtype == torch.float32:
-            t = t.float()
+        if dtype != torch.bfloat16:
+            t = t.to(dtype)
     else:
         t = torch.from_numpy(np.ascontiguousarray(a, np.float32))
-        if dtype == torch.bfloat16:
-            t = t.to(torch.bfloat16)
+        if dtype != torch.float32:
+            t = t.to(dtype)
     return t.to(device).contiguous()
 
 
@@ -133,7 +133,7 @@ class KevModel:
                  device=0):
         self.ctx, self.shape, self.dtype = ctx, shape, dtype
         self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
-        self.hk_dtype = HK_BF16 if dtype == torch.bfloat16 else HK_F32
+        self.hk_dtype = {torch.bfloat16: HK_BF16, torch.float16: HK_F16, torch.float32: HK_F32}[dtype]
         staged = {k: _to_device(v, dtype, self.device) for k, v in weights.items()}
         lts = (C.c_int32 * shape.n_layers)(*shape.layer_types)
         cfg = KevConfig(shape.hidden, shape.n_layers, shape.n_heads, shape.n_kv_heads, shape.head_dim,

@@ -11,12 +11,14 @@ import math
 import torch
 
 from . import abi
-from .abi import HK_BF16, HK_F32, Context
+from .abi import HK_BF16, HK_F16, HK_F32, Context
 
 
 def _dt(t: torch.Tensor) -> int:
     if t.dtype == torch.bfloat16:
         return HK_BF16
+    if t.dtype == torch.float16:
+        return HK_F16
     if t.dtype == torch.float32:
         return HK_F32
     raise TypeError(f"unsupported dtype {t.dtype}")
@@ -121,6 +123,24 @@ def gdn_prep(ctx: Context, mixed, conv_w, ba, b_col, a_col, base_g, dt_bias, cu_
         a_col, _p(base_g), _p(dt_bias), _p(cu_seqlens), n_seqs, tokens, heads, k_heads, _p(q), _p(k), _p(v), _p(g),
         _p(beta), _p(tail)))
     return (q, k, v, g, beta, tail) if want_tail else (q, k, v, g, beta)
+
+
+def gdn_fused(ctx: Context, mixed, conv_w, ba, b_col, a_col, base_g, dt_bias, z, norm_w, eps, cu_seqlens, heads,
+              k_heads, conv_hist=None, want_tail=False, initial_state=None, final_state=None, out=None):
+    """The fused Gated DeltaNet layer body (16-bit): mixed rows [q | k | v ...] -> gated-normed
+    recurrence output [tokens, heads, 128]. z is token-strided [tokens, >= heads * 128]."""
+    _dev(mixed, conv_w, ba, base_g, dt_bias, z, norm_w, cu_seqlens, conv_hist, initial_state, final_state, out)
+    tokens = mixed.shape[0]
+    n_seqs = cu_seqlens.numel() - 1
+    conv_dim = (2 * k_heads + heads) * 128
+    if out is None:
+        out = torch.empty((tokens, heads, 128), dtype=mixed.dtype, device=mixed.device)
+    tail = torch.empty((n_seqs, conv_dim, 3), dtype=mixed.dtype, device=mixed.device) if want_tail else None
+    ctx.check(abi.lib().hk_gdn_fused(
+        ctx.h, _dt(mixed), _p(mixed), mixed.stride(0), _p(conv_w), conv_w.shape[1], _p(conv_hist), _p(tail), _p(ba),
+        ba.stride(0), b_col, a_col, _p(base_g), _p(dt_bias), _p(z), z.stride(0), _p(norm_w), eps, _p(cu_seqlens),
+        n_seqs, tokens, heads, k_heads, _p(initial_state), _p(final_state), _p(out), out.stride(0)))
+    return (out, tail) if want_tail else out
 
 
 def rms_norm(ctx: Context, x, w_eff, eps, out=None):

@@ -47,6 +47,7 @@ extern "C" {
 
 #define HK_F32 0
 #define HK_BF16 1
+#define HK_F16 2
 
 /* Device fault bits reported by hk_ctx_take_faults. */
 #define HK_FAULT_SEQLENS 1   /* cu_seqlens / context_lens inconsistent for a token */
@@ -85,9 +86,10 @@ int hk_device_count(int* out);
 const char* hk_version(void);
 
 /* ---- RoPE tables (qwen3_5.rs:220-247: inv_freq = theta^(-2i/rd) in f32, cos/sin of
- * pos * inv_freq in f32, cast to the model dtype when round_bf16) -------------------------
- * Host-side helper: fills cos_host/sin_host [max_pos][rd/2] for upload. */
-int hk_rope_fill_table(int rotary_dim, double theta, int max_pos, int round_bf16, float* cos_host,
+ * pos * inv_freq in f32, cast to the model dtype) -----------------------------------------------
+ * Host-side helper: fills cos_host/sin_host [max_pos][rd/2] for upload; round_dtype HK_BF16 /
+ * HK_F16 rounds the values to that type (HK_F32: no rounding). */
+int hk_rope_fill_table(int rotary_dim, double theta, int max_pos, int round_dtype, float* cos_host,
                        float* sin_host);
 
 /* ---- fused q/k norm + partial RoPE + paged KV append -------------------------------------
@@ -120,7 +122,7 @@ int hk_paged_kv_write(hk_ctx* ctx, int dtype, const void* k_dev, const void* v_d
  * positions context_lens[s] - q_len(s) .. context_lens[s] - 1 and keys 0..pos through its
  * block table. max_q_len bounds q_len over the batch. gate_dev (optional) applies
  * o *= sigmoid(gate) (qwen3_5.rs:706-714). head_dim 128; q_heads / kv_heads in {1,2,4,8}.
- * dtype HK_F32: fp32 everywhere; HK_BF16: bf16 in/out, fp32 accumulation and softmax. */
+ * dtype HK_F32: fp32 everywhere; HK_BF16 / HK_F16: 16-bit in/out, fp32 accumulation and softmax. */
 int hk_paged_prefill_attention(hk_ctx* ctx, int dtype, const void* q_dev, long q_tok, long q_head,
                                const void* k_pool_dev, const void* v_pool_dev, int num_pages, int page_size,
                                const int32_t* block_tables_dev, int bt_stride, const int32_t* cu_seqlens_q_dev,
@@ -155,6 +157,22 @@ int hk_gdn_prep(hk_ctx* ctx, int dtype, const void* mixed_dev, long mixed_tok, c
                 const float* base_g_dev, const float* dt_bias_dev, const int32_t* cu_seqlens_dev, int n_seqs,
                 int n_tokens, int heads, int k_heads, void* q_out_dev, void* k_out_dev, void* v_out_dev,
                 float* g_out_dev, float* beta_out_dev, void* conv_tail_out_dev);
+
+/* ---- fused Gated DeltaNet layer body (16-bit dtypes) ------------------------------------------
+ * Replaces LinearAttn::forward between in_proj and out_proj (qwen3_5.rs:846-940) in one
+ * kernel: causal depthwise conv (conv_w [conv_dim][4] fp32, cached tail conv_hist
+ * [n_seqs][conv_dim][3] optional) + SiLU over the q|k|v channels at the start of each
+ * `mixed` row, l2norm of q and k, q * 128^-1/2, beta = sigmoid(b), g = base_g *
+ * softplus(a + dt_bias), the chunked gated delta rule (states as in
+ * hk_gated_delta_chunked), and the gated RMSNorm rms(o) * norm_w * silu(z) (193-201).
+ * out [tokens][heads][128] (token stride out_tok) is the out_proj input. Rows of mixed / z /
+ * out must be 16-byte aligned with strides that are multiples of 8 elements. */
+int hk_gdn_fused(hk_ctx* ctx, int dtype, const void* mixed_dev, long mixed_tok, const float* conv_w_dev, int conv_k,
+                 const void* conv_hist_dev, void* conv_tail_out_dev, const void* ba_dev, long ba_tok, int b_col,
+                 int a_col, const float* base_g_dev, const float* dt_bias_dev, const void* z_dev, long z_tok,
+                 const float* norm_w_dev, float eps, const int32_t* cu_seqlens_dev, int n_seqs, int n_tokens,
+                 int heads, int k_heads, const float* initial_state_dev, float* final_state_dev, void* out_dev,
+                 long out_tok);
 
 /* ---- norms and gates (qwen3_5.rs:184-201, 1020-1031) -------------------------------------------- */
 int hk_rms_norm(hk_ctx* ctx, int dtype, const void* x_dev, long x_tok, const float* w_eff_dev, float eps, int rows,

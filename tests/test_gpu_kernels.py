@@ -382,6 +382,125 @@ def test_delta_rule_bf16(ctx):
         assert eo < 2e-2 and es < 2e-2, (s, eo, es)
 
 
+def _round16(x, dtype):
+    """Round fp32 values to the 16-bit activation dtype (returned as fp32)."""
+    x = np.asarray(x, np.float32)
+    return O.round_bf16(x) if dtype == torch.bfloat16 else x.astype(np.float16).astype(np.float32)
+
+
+def _dev16(x, dtype):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dtype).cuda()
+
+
+TOL16 = {torch.bfloat16: 2e-2, torch.float16: 4e-3}
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_delta_rule_16bit_ragged_initial_state_gqa(ctx, dtype):
+    """16-bit q/k/v/o, fp32 state: ragged lengths (1, 63, 64, 65, 200), a carried state and
+    2 value heads per key head; 2e-2 relative (bf16) / 4e-3 (fp16)."""
+    from huncho_amd.ops import gated_delta_chunked
+
+    lengths = [1, 63, 64, 65, 200]
+    H, hk = 4, 2
+    cu, q, k, v, g, beta = _gdn_case(lengths, H, SEED + 4, hk)
+    q, k, v, beta = (_round16(x, dtype) for x in (q, k, v, beta))
+    s0 = abi.synth_normal(SEED, 76, len(lengths) * H * 128 * 128, 0.0, 0.05).reshape(len(lengths), H, 128, 128)
+    o_ref, s_ref = O.gated_delta_rule(_expand(q, H), _expand(k, H), v, g, beta, cu, s0)
+    st = cuda(s0.copy())
+    o = gated_delta_chunked(ctx, _dev16(q, dtype), _dev16(k, dtype), _dev16(v, dtype), cuda(g), cuda(beta), cuda(cu),
+                            initial_state=st, final_state=st)
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    eo, es = rel_err(o.float().cpu().numpy(), o_ref), rel_err(st.cpu().numpy(), s_ref)
+    print(f"16-bit delta rule {dtype}: out {eo:.2e} state {es:.2e}")
+    assert eo < TOL16[dtype] and es < TOL16[dtype], (eo, es)
+
+
+def _gdn_layer_ref(mixed, conv_w, hist, base_g, dt_bias, norm_w, s0, cu, H, hk, eps, dtype):
+    """Oracle composition of the Gated DeltaNet layer body (qwen3_5.rs:846-940): causal conv +
+    SiLU, l2norm, beta/g, the per-token recurrence and the gated RMSNorm, rounding to the
+    activation dtype where the fused kernel stores."""
+    conv_dim = (2 * hk + H) * 128
+    zc, bc = conv_dim, conv_dim + H * 128
+    outs, states, tails = [], [], []
+    for s in range(len(cu) - 1):
+        a, b = cu[s], cu[s + 1]
+        x = mixed[a:b]
+        conv, tail = O.causal_conv1d_silu(x[:, :conv_dim], conv_w, history=None if hist is None else hist[s],
+                                          want_tail=True)
+        conv = _round16(conv, dtype)
+        qr = _round16(O.l2norm(conv[:, :hk * 128].reshape(-1, hk, 128)) * np.float32(128 ** -0.5), dtype)
+        kr = _round16(O.l2norm(conv[:, hk * 128:2 * hk * 128].reshape(-1, hk, 128)), dtype)
+        vr = conv[:, 2 * hk * 128:].reshape(-1, H, 128)
+        beta = _round16(1 / (1 + np.exp(-x[:, bc:bc + H].astype(np.float64))), dtype).astype(np.float32)
+        g = (base_g * np.log(np.exp(x[:, bc + H:bc + 2 * H].astype(np.float64) + dt_bias) + 1)).astype(np.float32)
+        o, st = O.gated_delta_rule(_expand(qr, H), _expand(kr, H), vr, g, beta, [0, b - a],
+                                   None if s0 is None else s0[s:s + 1])
+        o = _round16(o, dtype)
+        z = x[:, zc:zc + H * 128].reshape(-1, H, 128)
+        outs.append(O.rms_norm_gated(o, z, norm_w, eps))
+        states.append(st[0])
+        tails.append(tail)
+    return np.concatenate(outs), np.stack(states), tails
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("with_history", [False, True])
+def test_gdn_fused_layer(ctx, dtype, with_history):
+    """The fused Gated DeltaNet layer body (one kernel: conv K=4 + SiLU + l2norm + beta/g +
+    chunked recurrence + gated RMSNorm, reading the fused projection rows q|k|v|z|b|a) against
+    the oracle composition; ragged lengths, GQA 2:1, optional conv history and carried state.
+    Output and state within 2e-2 relative (bf16) / 4e-3 (fp16); conv tails bit-exact."""
+    from huncho_amd.ops import gdn_fused
+
+    lengths = [1, 3, 64, 70, 130]
+    H, hk, eps = 4, 2, 1e-6
+    conv_dim = (2 * hk + H) * 128
+    width = conv_dim + H * 128 + 2 * H
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n, ns = int(cu[-1]), len(lengths)
+    seed = SEED + (7 if with_history else 8)
+    mixed = _round16(abi.synth_normal(seed, 100, n * width), dtype).reshape(n, width)
+    conv_w = O.round_bf16(abi.synth_normal(seed, 101, conv_dim * 4, 0.0, 0.5)).reshape(conv_dim, 4)
+    base_g = (-np.exp(O.round_bf16(abi.synth_normal(seed, 102, H, 0.0, 0.3)))).astype(np.float32)
+    dt_bias = O.round_bf16(abi.synth_normal(seed, 103, H, 0.0, 0.3))
+    norm_w = O.round_bf16(abi.synth_normal(seed, 104, 128, 1.0, 0.1))
+    hist = s0 = None
+    if with_history:
+        hist = _round16(abi.synth_normal(seed, 105, ns * conv_dim * 3), dtype).reshape(ns, conv_dim, 3)
+        s0 = abi.synth_normal(seed, 106, ns * H * 128 * 128, 0.0, 0.05).reshape(ns, H, 128, 128)
+    o_ref, s_ref, t_ref = _gdn_layer_ref(mixed, conv_w, hist, base_g, dt_bias, norm_w, s0, cu, H, hk, eps, dtype)
+
+    md = _dev16(mixed, dtype)
+    st = torch.zeros((ns, H, 128, 128), device="cuda") if s0 is None else cuda(s0.copy())
+    out, tail = gdn_fused(ctx, md, cuda(conv_w), md, conv_dim + H * 128, conv_dim + H * 128 + H, cuda(base_g),
+                          cuda(dt_bias), md[:, conv_dim:], cuda(norm_w), eps, cuda(cu), H, hk,
+                          conv_hist=None if hist is None else _dev16(hist, dtype), want_tail=True,
+                          initial_state=None if s0 is None else st, final_state=st)
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    eo, es = rel_err(out.float().cpu().numpy(), o_ref), rel_err(st.cpu().numpy(), s_ref)
+    print(f"fused GDN {dtype} history={with_history}: out {eo:.2e} state {es:.2e}")
+    assert eo < TOL16[dtype] and es < TOL16[dtype], (eo, es)
+    got_tail = tail.float().cpu().numpy()
+    for s in range(ns):
+        assert np.array_equal(got_tail[s], t_ref[s]), s
+
+
+def test_gdn_fused_rejects_misaligned_rows(ctx):
+    from huncho_amd.ops import gdn_fused
+
+    H = hk = 1
+    conv_dim = 3 * 128
+    md = torch.zeros((4, conv_dim + 128 + 2 * H + 3), dtype=torch.bfloat16, device="cuda")  # odd token stride
+    z = torch.zeros((4, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(abi.HkError):
+        gdn_fused(ctx, md, torch.zeros((conv_dim, 4), device="cuda"), md, conv_dim + 128, conv_dim + 129,
+                  torch.zeros(1, device="cuda"), torch.zeros(1, device="cuda"), z, torch.ones(128, device="cuda"),
+                  1e-6, cuda(np.array([0, 4], np.int32)), H, hk)
+
+
 # ---------------------------------------------------------------------------
 # GDN prep, norms, SwiGLU
 # ---------------------------------------------------------------------------
