@@ -67,6 +67,10 @@ SIGNATURES = {
     "hk_ctx_last_error": (C.c_char_p, [vp]),
     "hk_ctx_device_info": (I, [vp, C.POINTER(DeviceInfo)]),
     "hk_ctx_take_faults": (I, [vp, C.POINTER(I)]),
+    "hk_buffer_alloc": (I, [vp, C.c_size_t, C.POINTER(vp)]),
+    "hk_buffer_free": (I, [vp, vp]),
+    "hk_memcpy_h2d": (I, [vp, vp, vp, C.c_size_t]),
+    "hk_memcpy_d2h": (I, [vp, vp, vp, C.c_size_t]),
     "hk_rope_fill_table": (I, [I, D, I, I, vp, vp]),
     "hk_qk_norm_rope_kv_write": (I, [vp, I, vp, L, L, vp, L, vp, L, vp, vp, F, vp, vp, I, I, vp, vp, I, I, vp, I,
                                      I, I, I, I, I, vp, L, L, vp, vp]),

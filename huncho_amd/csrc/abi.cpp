@@ -136,6 +136,41 @@ extern "C" int hk_ctx_take_faults(hk_ctx* ctx, int* faults_out) {
     return rc;
 }
 
+extern "C" int hk_buffer_alloc(hk_ctx* ctx, size_t bytes, void** dev_out) {
+    if (!ctx || !dev_out) return HK_ERR_INVALID;
+    *dev_out = nullptr;
+    if (bytes == 0) return HK_OK;
+    hipSetDevice(ctx->device);
+    if (hipMalloc(dev_out, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        *dev_out = nullptr;
+        return hk_fail(ctx, HK_ERR_NOMEM, "hipMalloc of %zu bytes failed", bytes);
+    }
+    return HK_OK;
+}
+
+extern "C" int hk_buffer_free(hk_ctx* ctx, void* dev) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (!dev) return HK_OK;
+    hipSetDevice(ctx->device);
+    return hk_check_hip(ctx, hipFree(dev), "hipFree");
+}
+
+extern "C" int hk_memcpy_h2d(hk_ctx* ctx, void* dev_dst, const void* host_src, size_t bytes) {
+    if (!ctx || ((!dev_dst || !host_src) && bytes)) return HK_ERR_INVALID;
+    if (!bytes) return HK_OK;
+    hipSetDevice(ctx->device);
+    return hk_check_hip(ctx, hipMemcpyAsync(dev_dst, host_src, bytes, hipMemcpyHostToDevice, ctx->stream), "h2d copy");
+}
+
+extern "C" int hk_memcpy_d2h(hk_ctx* ctx, void* host_dst, const void* dev_src, size_t bytes) {
+    if (!ctx || ((!host_dst || !dev_src) && bytes)) return HK_ERR_INVALID;
+    if (!bytes) return HK_OK;
+    hipSetDevice(ctx->device);
+    int rc = hk_check_hip(ctx, hipMemcpyAsync(host_dst, dev_src, bytes, hipMemcpyDeviceToHost, ctx->stream), "d2h copy");
+    return rc ? rc : hk_check_hip(ctx, hipStreamSynchronize(ctx->stream), "d2h sync");
+}
+
 // ---------------------------------------------------------------------------
 // host helpers: rope table, calibration, synthetic inputs
 // ---------------------------------------------------------------------------

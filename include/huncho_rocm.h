@@ -43,7 +43,7 @@ extern "C" {
 #define HK_ERR_INVALID 1     /* bad argument, shape or stride  -> Error::Backend / Request */
 #define HK_ERR_UNSUPPORTED 2 /* shape or dtype this build does not implement -> Error::Unsupported */
 #define HK_ERR_DEVICE 3      /* HIP runtime / launch failure -> Error::Backend */
-#define HK_ERR_NOMEM 4       /* allocation failed (context / model creation only) */
+#define HK_ERR_NOMEM 4       /* allocation failed (context, model creation, hk_buffer_alloc) */
 
 #define HK_F32 0
 #define HK_BF16 1
@@ -84,6 +84,14 @@ int hk_ctx_device_info(hk_ctx* ctx, hk_device_info_t* out);
 int hk_ctx_take_faults(hk_ctx* ctx, int* faults_out);
 int hk_device_count(int* out);
 const char* hk_version(void);
+
+/* ---- device memory for callers without a HIP binding (the Rust FFI crate): plain
+ * hipMalloc / hipFree on the context's device, stream-ordered copies on the context's
+ * stream. hk_memcpy_d2h returns after the copy has completed. -------------------------- */
+int hk_buffer_alloc(hk_ctx* ctx, size_t bytes, void** dev_out);
+int hk_buffer_free(hk_ctx* ctx, void* dev);
+int hk_memcpy_h2d(hk_ctx* ctx, void* dev_dst, const void* host_src, size_t bytes);
+int hk_memcpy_d2h(hk_ctx* ctx, void* host_dst, const void* dev_src, size_t bytes);
 
 /* ---- RoPE tables (qwen3_5.rs:220-247: inv_freq = theta^(-2i/rd) in f32, cos/sin of
  * pos * inv_freq in f32, cast to the model dtype) -----------------------------------------------

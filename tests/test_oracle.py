@@ -302,6 +302,19 @@ def test_rope_rotation_invariants():
     np.testing.assert_allclose(c[:, 0], np.cos(pos.astype(np.float32)), rtol=1e-6, atol=1e-6)
 
 
+def test_rope_frequency_ladder_special_values():
+    """The frequency ladder of the rotary table (qwen3_5.rs:226-232) at points fixed by the
+    textbook RoPE: the pair halfway up the ladder turns by theta^-1/2 per position, the pairs
+    are geometric with ratio theta^-2/rd, and the halves of each row repeat (cat(freqs, freqs))."""
+    for theta, rd in ((1e4, 8), (1e7, 128), (1.6e5, 64)):
+        c, s = O.rope_cos_sin(rd, theta, np.array([1], np.int32))
+        ang = np.arctan2(s[0].astype(np.float64), c[0].astype(np.float64))
+        half = rd // 2
+        np.testing.assert_allclose(ang[:half], ang[half:], rtol=0, atol=0)
+        np.testing.assert_allclose(ang[rd // 4], theta ** -0.5, rtol=2e-6)
+        np.testing.assert_allclose(ang[1:half] / ang[:half - 1], theta ** (-2.0 / rd), rtol=2e-6)
+
+
 def test_calibrate_semantics():
     p = O.calibrate([1.0, 2.0, 3.0], 1.3)
     e = np.exp((np.array([1.0, 2.0, 3.0]) - 3.0) / 1.3)
