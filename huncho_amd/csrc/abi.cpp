@@ -421,12 +421,22 @@ extern "C" int hk_paged_prefill_attention(hk_ctx* ctx, int dtype, const void* q,
         return hk_fail(ctx, HK_ERR_UNSUPPORTED, "GQA group %d: 1, 2, 4 or 8 are implemented", group);
     const int shift = log2_exact(page_size);
     REQUIRE(shift >= 4 && shift <= 8, "page_size %d must be a power of two in 16..256", page_size);
-    REQUIRE(n_seqs > 0 && n_tokens >= 0 && max_q_len >= 0 && bt_stride > 0 && num_pages > 0, "bad batch geometry");
+    REQUIRE(n_seqs > 0 && n_seqs <= 65535 && n_tokens >= 0 && max_q_len >= 0 && bt_stride > 0 && num_pages > 0,
+            "bad batch geometry");
     REQUIRE(q && k_pool && v_pool && bt && cu && ctxl && o, "null pointer argument");
     REQUIRE(q_head >= head_dim && q_tok >= (long)q_heads * q_head - (q_head - head_dim), "q strides overlap heads");
     REQUIRE(o_head >= head_dim && o_tok >= (long)q_heads * o_head - (o_head - head_dim), "o strides overlap heads");
     REQUIRE(!gate || gate_head >= head_dim, "gate stride too small");
     REQUIRE(scale > 0 && isfinite(scale), "scale must be positive and finite");
+    {  // vector widths of the kernels' loads and stores (elements): q rows, o / gate rows
+        const long qv = dtype == HK_F32 ? 2 : 8, ov = 4, esz = dtype == HK_F32 ? 4 : 2;
+        const uintptr_t qa = (uintptr_t)q, oa = (uintptr_t)o, ga = (uintptr_t)gate;
+        REQUIRE(q_tok % qv == 0 && q_head % qv == 0 && qa % (qv * esz) == 0, "q rows must be %ld-element aligned", qv);
+        REQUIRE(o_tok % ov == 0 && o_head % ov == 0 && oa % (ov * esz) == 0, "o rows must be 4-element aligned");
+        REQUIRE(!gate || (gate_tok % ov == 0 && gate_head % ov == 0 && ga % (ov * esz) == 0),
+                "gate rows must be 4-element aligned");
+        REQUIRE((((uintptr_t)k_pool | (uintptr_t)v_pool) & 15) == 0, "K/V pools must be 16-byte aligned");
+    }
     if (max_q_len == 0 || n_tokens == 0) return HK_OK;
     const int pos_per_block = 128 / group;
     const int n_qblocks = (max_q_len + pos_per_block - 1) / pos_per_block;

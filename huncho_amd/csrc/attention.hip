@@ -7,22 +7,24 @@
 // sequence lives in page block_tables[s][j / P], slot j % P; pool layout
 // [page][kv_head][P][head_dim], the reference's Page tensor [1, Hkv, rows, d]).
 //
-// Design (one workgroup = one sequence x one KV head x 128 query rows):
-//   * the 128 rows are the GQA group's query heads x (128 / group) positions, so every K/V
-//     tile that is gathered into LDS serves all query heads of its KV head;
+// Design of the 16-bit kernel (one workgroup = one sequence x one KV head x a mirrored pair
+// of 128-row query blocks):
+//   * the 128 rows of a block are the GQA group's query heads x (128 / group) positions, so
+//     every K/V tile gathered into LDS serves all query heads of its KV head;
+//   * a workgroup runs q-blocks (n - 1 - z, z) of its sequence back to back on one tile
+//     pipeline, so every workgroup of a sequence does the same n + 1 tiles;
 //   * 4 waves x 32 query rows; S^T = K Q^T on MFMA so that each lane owns one query
 //     column and the softmax row statistics stay in-lane (one lane-swap per tile);
-//   * K rows are loaded into the MFMA A operand in a permuted order so that each lane's
-//     accumulator holds 16 consecutive keys; P then feeds P.V directly as the B operand,
-//     and V is stored transposed in LDS so the A operand of O^T = V^T P^T is one 16-byte
-//     read per MFMA;
-//   * online softmax in base 2 with fp32 statistics; O^T accumulates in fp32 registers;
-//   * the optional output gate o *= sigmoid(gate) (qwen3_5.rs:706-714) is fused into the
-//     epilogue.
-// Grid = (kv_heads, n_seqs, q_blocks) with the q-block index reversed, so the longest
-// (latest) blocks of every sequence dispatch first; blocks past a sequence's end exit.
-// With 8 KV heads the round-robin XCD dispatch keeps each KV head on one XCD, so the
-// q-blocks that re-read a sequence's K/V share that XCD's L2.
+//   * K rows are read into the MFMA A operand in a permuted order so that each lane's
+//     accumulator holds 16 consecutive keys; P then feeds P.V directly as the B operand;
+//   * K and V tiles sit row-major in double-buffered LDS with an XOR chunk swizzle; the V^T
+//     operand of O^T = V^T P^T comes from transposing LDS reads (ds_read_b64_tr_b16);
+//   * online softmax in base 2 with fp32 statistics and lazy rescaling; O^T accumulates in
+//     fp32 registers; the output gate o *= sigmoid(gate) (qwen3_5.rs:706-714) is fused into
+//     the epilogue.
+// Grid = (kv_heads, q-block pairs, sequences): the pairs of one (sequence, KV head) are
+// consecutive in dispatch order on one XCD and share its L2 copy of the K/V pages.
+// The fp32 kernel keeps one workgroup per q-block, grid (kv_heads, sequences, q-blocks).
 #include "common.hpp"
 #include "kernel_args.hpp"
 
@@ -30,8 +32,6 @@ namespace hk {
 
 constexpr int D = 128;
 constexpr int BN = 64;
-constexpr int KS_STRIDE_BF16 = D + 8;   // padded LDS row (elements)
-constexpr int VT_STRIDE_BF16 = BN + 8;
 constexpr int KS_STRIDE_F32 = D + 4;
 constexpr int V_STRIDE_F32 = D + 4;
 
@@ -39,6 +39,7 @@ constexpr int V_STRIDE_F32 = D + 4;
 __device__ __forceinline__ int perm_key(int m) { return ((m >> 2) & 1) * 16 + (m >> 3) * 4 + (m & 3); }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
 
 // Pool page of key `key` through the block table; -1 (and the fault flag) when the table
 // entry lies past bt_stride or outside [0, num_pages).
@@ -55,16 +56,40 @@ __device__ __forceinline__ int page_of(const AttnArgs& a, const int* table, int 
 // ---------------------------------------------------------------------------
 // 16-bit inputs (bf16 or fp16), fp32 accumulation
 // ---------------------------------------------------------------------------
+constexpr int KV_ROW = 128;                        // LDS row: one key's 128 dims (256 B, unpadded)
+constexpr int TILE_ELEMS = BN * KV_ROW;            // one K or V tile: 16 KB
+constexpr size_t ATTN16_LDS = 4 * TILE_ELEMS * 2;  // K and V, double-buffered: 65,536 B
+constexpr float RESCALE_LOG2 = 8.0f;  // exponents may run up to 2^8 above the row max in use
+
+// The 16-byte chunk c of key row r sits at chunk c ^ swz(r). With this swizzle the row
+// writes, the permuted-row K reads of S^T = K Q^T and the transposing V reads of P.V each
+// spread over all LDS banks (no bank holds more words than the access's minimum).
+__device__ __forceinline__ int swz(int r) { return 2 * (r & 3) + 8 * ((r >> 4) & 1); }
+__device__ __forceinline__ int lds_off(int r, int c) { return r * KV_ROW + 8 * (c ^ swz(r)); }
+
+// Pipeline per 64-key tile (one barrier per tile):
+//   issue the global loads of tile t+1 (block-table entry read one tile earlier) and the
+//   block-table read of tile t+2; S^T = K Q^T, online softmax and O^T += V^T P^T on LDS
+//   buffer t % 2; write tile t+1 into buffer (t+1) % 2; barrier.
+// Each thread moves 4 consecutive keys (one page: pages hold >= 16 keys) x one 16-byte chunk
+// of K and of V, so one block-table entry addresses all 8 of its loads. Loads are
+// unconditional (addresses clamped to pool row 0) and masked when written to LDS.
+// Softmax keeps the raw-score row max m and evaluates p = 2^(s c - m c) with one FMA
+// (c = scale log2 e); the O / l rescale happens only when the max grew by more than 2^8
+// (otherwise p <= 2^8 and the fp32 sums lose nothing), which is the same normalised result.
 template <typename T>
 __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     typedef typename Mma16<T>::v8 v8;
     typedef typename Mma16<T>::v4 v4;
-    __shared__ __attribute__((aligned(16))) T Ks[BN * KS_STRIDE_BF16];
-    __shared__ __attribute__((aligned(16))) T Vt[D * VT_STRIDE_BF16];
+    extern __shared__ __attribute__((aligned(16))) char attn_smem[];
+    T* const lds = (T*)attn_smem;  // [buf][K | V][64][128]
 
+    // grid (kv_heads, q-block pairs, sequences): linear workgroup ids run KV head fastest,
+    // and consecutive ids go round-robin to the 8 XCDs, so all q-block pairs of one
+    // (sequence, KV head) run together on one XCD and share its L2 copy of the K/V pages
     const int kvh = blockIdx.x;
-    const int seq = blockIdx.y;
-    const int qb = gridDim.z - 1 - blockIdx.z;
+    const int z = blockIdx.y;
+    const int seq = blockIdx.z;
     const int q0 = a.cu_seqlens_q[seq];
     const int q_len = a.cu_seqlens_q[seq + 1] - q0;
     const int ctx = a.context_lens[seq];
@@ -73,122 +98,195 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
         if (threadIdx.x == 0) atomicOr(a.fault, 1);
         return;
     }
-    if (qb * P >= q_len) return;
+    // this workgroup's q-blocks: the mirrored pair (nq - 1 - z, z), so every workgroup of a
+    // sequence runs nq + 1 key tiles; the longer block goes first
+    const int nq = (q_len + P - 1) / P;
+    if (2 * z >= nq) return;
+    const int qb_a = nq - 1 - z, qb_b = z;
+    const int n_blocks = qb_a == qb_b ? 1 : 2;
     const int off = ctx - q_len;  // absolute position of the first new query
+    const int* table = a.block_tables + (long)seq * a.bt_stride;
+    const int pmask = (1 << a.page_shift) - 1;
+    auto block_tiles = [&](int qb) { return (off + min(q_len, (qb + 1) * P) - 1) / BN + 1; };
+    const int nt_a = block_tiles(qb_a);
+    const int n_sched = nt_a + (n_blocks == 2 ? block_tiles(qb_b) : 0);
+    // schedule step i -> key tile: block a's tiles 0..nt_a-1, then block b's from 0
+    auto sched_tile = [&](int i) { return i < nt_a ? i : i - nt_a; };
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, col = lane & 31;
-
-    // this lane's query row: (head in group, position)
-    const int row = wave * 32 + col;
+    const int row = wave * 32 + col;  // this lane's query row: (head in group, position)
     const int hg = row / P, p = row % P;
-    const int qi = qb * P + p;  // index among the sequence's new queries
-    const bool q_valid = qi < q_len;
     const int head = kvh * a.group + hg;
-    int qpos = off + (q_valid ? qi : q_len - 1);
 
-    // Q fragment: Q[q][ks*16 + g*8 .. +8] for ks = 0..7
-    v8 qf[8];
+    // per-lane LDS offsets (elements): K rows of S^T (row perm_key(col), chunk 2 ks + g) and
+    // V^T transposing reads (16-lane group G: dims 32 db + 16 (G & 1) + 4 (j & 3), keys
+    // 16 (G >> 1) + (j >> 2) + 4 r + 8 h + 32 kb; the key-independent part of the swizzle)
+    int koff[8], vofs[4];
     {
-        const T* qp = (const T*)a.q + (long)(q0 + (q_valid ? qi : 0)) * a.q_tok + (long)head * a.q_head;
+        const int kr_ = perm_key(col);
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            if (q_valid)
-                qf[ks] = *(const v8*)(qp + ks * 16 + g * 8);
-            else
-                qf[ks] = v8{};
-        }
+        for (int ks = 0; ks < 8; ++ks) koff[ks] = lds_off(kr_, 2 * ks + g);
+        const int G = lane >> 4, j = lane & 15;
+        const int vrow = (G >> 1) * 16 + (j >> 2);
+        const int cl = 2 * (G & 1) + ((j & 3) >> 1);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) vofs[db] = vrow * KV_ROW + 8 * ((4 * db + cl) ^ swz(vrow)) + 4 * (j & 1);
     }
 
-    const int last_pos = off + min(q_len, (qb + 1) * P) - 1;  // largest query position in the block
-    const int first_pos = off + qb * P;
-    const int n_tiles = last_pos / BN + 1;
-    const int* table = a.block_tables + (long)seq * a.bt_stride;
-    const int pmask = (1 << a.page_shift) - 1;
-
-    // global -> register prefetch of one K/V tile
-    // K: thread t loads rows t/16 + 16i (i = 0..3), 16-byte column chunk t % 16
-    // V: thread t loads keys 4*(t/16) + i (i = 0..3), 8 dims (t % 16) * 8
+    const int kq = tid >> 4, ch = tid & 15;  // this thread moves keys 4 kq .. 4 kq + 3, chunk ch
+    int ent = 0;          // block-table entry of the next tile to load
+    bool tab_ok = false;  // that tile's key group lies inside the context and the table
+    auto lookup = [&](int tile) {
+        const int key = tile * BN + 4 * kq;
+        const int idx = key >> a.page_shift;
+        ent = table[min(idx, a.bt_stride - 1)];
+        tab_ok = key < ctx && idx < a.bt_stride;
+    };
     uint4 kr[4], vr[4];
+    int nval = 0;  // keys of the loaded group inside the context (0..4)
     auto load_tile = [&](int tile) {
-        const int n0 = tile * BN;
+        const int key = tile * BN + 4 * kq;
+        const bool page_ok = (unsigned)ent < (unsigned)a.num_pages;
+        if (tab_ok && !page_ok) atomicOr(a.fault, 2);
+        const bool use = tab_ok && page_ok;
+        nval = use ? min(4, ctx - key) : 0;
+        const long base = (use ? ((((long)ent * a.kv_heads + kvh) << a.page_shift) + (key & pmask)) * D : 0) + ch * 8;
+        const T* kp = (const T*)a.k_pool + base;
+        const T* vp = (const T*)a.v_pool + base;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int key = n0 + (tid >> 4) + 16 * i;
-            int page = key < ctx ? page_of(a, table, key) : -1;
-            if (page >= 0) {
-                long base = (((long)page * a.kv_heads + kvh) << a.page_shift) + (key & pmask);
-                kr[i] = *(const uint4*)((const T*)a.k_pool + base * D + (tid & 15) * 8);
-            } else {
-                kr[i] = uint4{0, 0, 0, 0};
-            }
-            int vkey = n0 + 4 * (tid >> 4) + i;
-            int vpage = vkey < ctx ? page_of(a, table, vkey) : -1;
-            if (vpage >= 0) {
-                long base = (((long)vpage * a.kv_heads + kvh) << a.page_shift) + (vkey & pmask);
-                vr[i] = *(const uint4*)((const T*)a.v_pool + base * D + (tid & 15) * 8);
-            } else {
-                vr[i] = uint4{0, 0, 0, 0};
-            }
+            kr[i] = *(const uint4*)(kp + i * D);
+            vr[i] = *(const uint4*)(vp + i * D);
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int buf) {
+        T* Kb = lds + buf * 2 * TILE_ELEMS;
+        T* Vb = Kb + TILE_ELEMS;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *(uint4*)(Ks + ((tid >> 4) + 16 * i) * KS_STRIDE_BF16 + (tid & 15) * 8) = kr[i];
-        // transpose V: Vt[d][key]; each thread writes 4 consecutive keys for each of its 8 dims
-        const T* v0 = (const T*)&vr[0];
-        const T* v1 = (const T*)&vr[1];
-        const T* v2 = (const T*)&vr[2];
-        const T* v3 = (const T*)&vr[3];
-        const int kbase = 4 * (tid >> 4), d0 = (tid & 15) * 8;
-#pragma unroll
-        for (int dd = 0; dd < 8; ++dd) {
-            v4 w = {v0[dd], v1[dd], v2[dd], v3[dd]};
-            *(v4*)(Vt + (d0 + dd) * VT_STRIDE_BF16 + kbase) = w;
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t m = i < nval ? ~0u : 0u;
+            const int o = lds_off(4 * kq + i, ch);
+            *(uint4*)(Kb + o) = uint4{kr[i].x & m, kr[i].y & m, kr[i].z & m, kr[i].w & m};
+            *(uint4*)(Vb + o) = uint4{vr[i].x & m, vr[i].y & m, vr[i].z & m, vr[i].w & m};
         }
+    };
+
+    // per-block query state
+    int qi = 0, qpos = 0, first_pos = 0;
+    bool q_valid = false;
+    v8 qf[8];  // Q[q][ks*16 + g*8 .. +8] for ks = 0..7
+    auto load_q = [&](int qb) {  // issued once the previous block's last S^T no longer needs qf
+        const int qi_ = qb * P + p;
+        const bool ok = qi_ < q_len;
+        const T* qp = (const T*)a.q + (long)(q0 + (ok ? qi_ : 0)) * a.q_tok + (long)head * a.q_head;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) qf[ks] = ok ? *(const v8*)(qp + ks * 16 + g * 8) : v8{};
+    };
+    auto begin_block = [&](int qb) {
+        qi = qb * P + p;  // index among the sequence's new queries
+        q_valid = qi < q_len;
+        qpos = off + (q_valid ? qi : q_len - 1);
+        first_pos = off + qb * P;
     };
 
     f32x16 acc_o[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) acc_o[db] = f32x16{};
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_use = -INFINITY, l_run = 0.0f;
+    const float c = a.scale_log2;
 
+    // epilogue of a block: o = O / l (both lane halves hold partial row sums), then the
+    // output gate o = round(o) * round(sigmoid(gate)) as the reference rounds both
+    auto finish_block = [&]() {
+        const float l_tot = l_run + __shfl_xor(l_run, 32);
+        const float inv_l = 1.0f / l_tot;
+        if (q_valid) {
+            T* op = (T*)a.o + (long)(q0 + qi) * a.o_tok + (long)head * a.o_head;
+            v4 gv[4][4];
+            const bool gated = a.gate != nullptr;
+            if (gated) {
+                const T* gp = (const T*)a.gate + (long)(q0 + qi) * a.g_tok + (long)head * a.g_head;
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) gv[db][jj] = *(const v4*)(gp + db * 32 + jj * 8 + g * 4);
+            }
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    float r[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        r[e] = acc_o[db][jj * 4 + e] * inv_l;
+                        if (gated) r[e] = (float)(T)r[e] * (float)(T)sigmoidf_((float)gv[db][jj][e]);
+                    }
+                    *(v4*)(op + db * 32 + jj * 8 + g * 4) = v4{(T)r[0], (T)r[1], (T)r[2], (T)r[3]};
+                }
+        }
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc_o[db] = f32x16{};
+        m_use = -INFINITY;
+        l_run = 0.0f;
+    };
+
+    begin_block(qb_a);
+    load_q(qb_a);
+    lookup(0);
     load_tile(0);
-    for (int tile = 0; tile < n_tiles; ++tile) {
-        __syncthreads();
-        store_tile();
-        __syncthreads();
-        if (tile + 1 < n_tiles) load_tile(tile + 1);
+    if (n_sched > 1) lookup(sched_tile(1));
+    store_tile(0);
+    __syncthreads();
+    for (int i = 0; i < n_sched; ++i) {
+        const int buf = i & 1;
+        if (i + 1 < n_sched) {
+            load_tile(sched_tile(i + 1));
+            if (i + 2 < n_sched) lookup(sched_tile(i + 2));
+        }
+        const T* Kb = lds + buf * 2 * TILE_ELEMS;
+        const T* Vb = Kb + TILE_ELEMS;
 
         // S^T = K Q^T for this wave's 32 queries: two 32-key blocks
         f32x16 s[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             s[kb] = f32x16{};
-            const T* krow = Ks + (kb * 32 + perm_key(col)) * KS_STRIDE_BF16 + g * 8;
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                v8 af = *(const v8*)(krow + ks * 16);
-                s[kb] = Mma16<T>::mma(af, qf[ks], s[kb]);
-            }
+            for (int ks = 0; ks < 8; ++ks)
+                s[kb] = Mma16<T>::mma(*(const v8*)(Kb + kb * 32 * KV_ROW + koff[ks]), qf[ks], s[kb]);
         }
-        // scale to base 2, causal mask (only tiles that reach past the block's first query)
-        const int n0 = tile * BN;
-        const bool need_mask = n0 + BN - 1 > first_pos;
+        if (i == nt_a - 1 && n_blocks == 2) load_q(qb_b);  // lands during this tile's softmax and P.V
+        // causal mask (only tiles that reach past the block's first query), raw-score max
+        const int n0 = sched_tile(i) * BN;
         float mloc = -INFINITY;
+        if (n0 + BN - 1 > first_pos) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                float v = s[kb][j] * a.scale_log2;
-                if (need_mask && n0 + kb * 32 + g * 16 + j > qpos) v = -INFINITY;
-                s[kb][j] = v;
-                mloc = fmaxf(mloc, v);
-            }
-        const float m_new = fmaxf(m_run, wave_max32(mloc));
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
+                for (int j = 0; j < 16; ++j) {
+                    if (n0 + kb * 32 + g * 16 + j > qpos) s[kb][j] = -INFINITY;
+                    mloc = fmaxf(mloc, s[kb][j]);
+                }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, s[kb][j]);
+        }
+        const float m_tile = wave_max32(mloc);
+        const bool grow = (m_tile - m_use) * c > RESCALE_LOG2;
+        if (__any(grow)) {
+            const float m_new = grow ? m_tile : m_use;
+            const float alpha = fast_exp2((m_use - m_new) * c);
+            m_use = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc_o[db][j] *= alpha;
+        }
+        const float mc = m_use * c;
         float lsum = 0.0f;
         v8 pf[4];
 #pragma unroll
@@ -197,55 +295,35 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
             for (int h = 0; h < 2; ++h) {
                 v8 t;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    float e = fast_exp2(s[kb][h * 8 + i] - m_new);
+                for (int k = 0; k < 8; ++k) {
+                    const float e = fast_exp2(fmaf(s[kb][h * 8 + k], c, -mc));
                     lsum += e;
-                    t[i] = (T)e;
+                    t[k] = (T)e;
                 }
                 pf[kb * 2 + h] = t;
             }
-        l_run = l_run * alpha + lsum;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc_o[db][j] *= alpha;
-        // O^T += V^T P^T
+        l_run += lsum;
+        // O^T += V^T P^T: keys kb*32 + g*16 + h*8 + [0..7] of dims db*32 + [0..31]
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-            const T* vrow = Vt + (db * 32 + col) * VT_STRIDE_BF16 + g * 16;
+            const T* vb = Vb + vofs[db];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int kb = c >> 1, h = c & 1;
-                v8 af = *(const v8*)(vrow + kb * 32 + h * 8);
-                acc_o[db] = Mma16<T>::mma(af, pf[c], acc_o[db]);
+            for (int cc = 0; cc < 4; ++cc) {
+                const int kb = cc >> 1, h = cc & 1;
+                const i16x4 lo = lds_read_tr16(vb + (kb * 32 + h * 8) * KV_ROW);
+                const i16x4 hi = lds_read_tr16(vb + (kb * 32 + h * 8 + 4) * KV_ROW);
+                const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc_o[db] = Mma16<T>::mma(af, pf[cc], acc_o[db]);
             }
         }
+        if (i == nt_a - 1) {  // block a done: write it, start block b
+            finish_block();
+            if (n_blocks == 2) begin_block(qb_b);
+        }
+        if (i + 1 < n_sched) store_tile(buf ^ 1);
+        __syncthreads();
     }
-
-    // epilogue: o = O / l (both lane halves hold partial row sums), optional sigmoid gate
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const float inv_l = 1.0f / l_tot;
-    if (!q_valid) return;
-    T* op = (T*)a.o + (long)(q0 + qi) * a.o_tok + (long)head * a.o_head;
-    const T* gp = a.gate ? (const T*)a.gate + (long)(q0 + qi) * a.g_tok + (long)head * a.g_head : nullptr;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int d = db * 32 + jj * 8 + g * 4;
-            float r0 = acc_o[db][jj * 4 + 0] * inv_l, r1 = acc_o[db][jj * 4 + 1] * inv_l;
-            float r2 = acc_o[db][jj * 4 + 2] * inv_l, r3 = acc_o[db][jj * 4 + 3] * inv_l;
-            if (gp) {
-                v4 gv = *(const v4*)(gp + d);
-                // the reference rounds attn and sigmoid(gate) to the activation dtype, then multiplies
-                r0 = (float)(T)r0 * (float)(T)sigmoidf_((float)gv[0]);
-                r1 = (float)(T)r1 * (float)(T)sigmoidf_((float)gv[1]);
-                r2 = (float)(T)r2 * (float)(T)sigmoidf_((float)gv[2]);
-                r3 = (float)(T)r3 * (float)(T)sigmoidf_((float)gv[3]);
-            }
-            v4 w = {(T)r0, (T)r1, (T)r2, (T)r3};
-            *(v4*)(op + d) = w;
-        }
+    if (n_blocks == 2) finish_block();
 }
 
 // ---------------------------------------------------------------------------
@@ -413,12 +491,25 @@ __global__ __launch_bounds__(256, 1) void paged_prefill_attn_f32(AttnArgs a) {
 // ---------------------------------------------------------------------------
 extern "C" int hk_launch_paged_prefill_attention(int dtype, const hk::AttnArgs* args, int n_seqs,
                                                  int n_qblocks, hipStream_t stream) {
-    dim3 grid(args->kv_heads, n_seqs, n_qblocks);
+    static bool configured = false;
+    if (!configured) {
+        if (hipFuncSetAttribute((const void*)hk::paged_prefill_attn_16<hk::bf16>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)hk::ATTN16_LDS) != hipSuccess ||
+            hipFuncSetAttribute((const void*)hk::paged_prefill_attn_16<hk::f16>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)hk::ATTN16_LDS) != hipSuccess)
+            return HK_ERR_DEVICE;
+        configured = true;
+    }
+    // 16-bit: one workgroup per mirrored pair of q-blocks; fp32: one per q-block
+    if (dtype == hk::DT_F32) {
+        hipLaunchKernelGGL(hk::paged_prefill_attn_f32, dim3(args->kv_heads, n_seqs, n_qblocks), dim3(256), 0, stream,
+                           *args);
+        return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+    }
+    const dim3 grid(args->kv_heads, (n_qblocks + 1) / 2, n_seqs);
     if (dtype == hk::DT_BF16)
-        hipLaunchKernelGGL(hk::paged_prefill_attn_16<hk::bf16>, grid, dim3(256), 0, stream, *args);
-    else if (dtype == hk::DT_F16)
-        hipLaunchKernelGGL(hk::paged_prefill_attn_16<hk::f16>, grid, dim3(256), 0, stream, *args);
+        hipLaunchKernelGGL(hk::paged_prefill_attn_16<hk::bf16>, grid, dim3(256), hk::ATTN16_LDS, stream, *args);
     else
-        hipLaunchKernelGGL(hk::paged_prefill_attn_f32, grid, dim3(256), 0, stream, *args);
+        hipLaunchKernelGGL(hk::paged_prefill_attn_16<hk::f16>, grid, dim3(256), hk::ATTN16_LDS, stream, *args);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }

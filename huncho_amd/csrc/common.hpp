@@ -55,6 +55,17 @@ template <> struct Mma16<f16> {
     }
 };
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, output lane 4a + c receives in
+// element e the 16-bit element c of the 8 bytes addressed by source lane a + 4e (checked on
+// gfx950). Reading rows of a row-major [key][dim] tile this way hands each lane 4 keys of
+// one dim: the V^T operand of P.V without a transposed copy.
+__device__ __forceinline__ i16x4 lds_read_tr16(const void* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p);
+}
+
 // Kernel dtype codes shared with the C ABI.
 enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
