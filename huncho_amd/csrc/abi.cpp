@@ -541,6 +541,7 @@ extern "C" int hk_gdn_fused(hk_ctx* ctx, int dtype, const void* mixed, long mixe
     REQUIRE(heads > 0 && k_heads > 0 && heads % k_heads == 0, "heads %d not a multiple of k_heads %d", heads, k_heads);
     REQUIRE(n_seqs > 0 && n_seqs <= 65535 && n_tokens >= 0, "bad batch geometry");
     REQUIRE(mixed && conv_w && ba && base_g && dt_bias && z && norm_w && cu && out, "null pointer argument");
+    REQUIRE(((uintptr_t)conv_w & 15) == 0, "conv weights must be 16-byte aligned");
     const long conv_dim = (2L * k_heads + heads) * 128;
     REQUIRE(mixed_tok >= conv_dim && mixed_tok % 8 == 0 && ((uintptr_t)mixed & 15) == 0,
             "mixed rows must hold conv_dim channels with 16-byte aligned rows");

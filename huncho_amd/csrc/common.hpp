@@ -70,6 +70,26 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const void* p) {
 enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// v_rcp_f32 / v_rsq_f32 (about 1 ulp in fp32) instead of the IEEE division sequence; used
+// where the result is rounded to a 16-bit activation right after.
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_rsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
+__device__ __forceinline__ float fast_sigmoid(float x) { return fast_rcp(1.0f + __expf(-x)); }
+__device__ __forceinline__ float fast_silu(float x) { return x * fast_rcp(1.0f + __expf(-x)); }
+
+// Sum over each aligned group of 16 lanes, left in every lane of the group: DPP quad_perm
+// [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror (every lane adds the same partial
+// sums in the same pairing, so the 16 results are identical).
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum16(float x) {
+    x += dpp_mov<0xB1>(x);
+    x += dpp_mov<0x4E>(x);
+    x += dpp_mov<0x141>(x);
+    x += dpp_mov<0x140>(x);
+    return x;
+}
 
 __device__ __forceinline__ float wave_max32(float v) {
     // combine the two 32-lane halves (lane l and l ^ 32)

@@ -20,12 +20,17 @@
 //               RMSNorm rms(o) * w * silu(z) (193-201) -> out_proj input
 // so one kernel streams each layer's q|k|v|z|b|a once and writes one output row per token.
 //
-// Chunk pipeline, one workgroup (4 waves) per (sequence, value head):
-//   P0  global -> LDS: q, k, v rows (row-major) and k transposed; g scan and beta
+// Chunk pipeline, one workgroup (4 waves) per (sequence, value head), two workgroups per CU
+// (78 KB of LDS, <= 256 registers per lane) so one workgroup's VALU prologue overlaps the
+// other's MFMA phases:
+//   P0  global -> LDS: q, v rows (padded) and k rows (swizzled) (fused: waves 0-2 run the
+//       conv for q, k, v); wave 3: g scan and beta
 //   P1  waves 0-2: K K^T and Q K^T blocks -> A (fp32) and Aqk; wave 3 zeroes the upper
 //       blocks; every wave: K S0, Q S0 for its columns -> R and exp(G) Q S0 in registers
-//   P2  in-place blocked inverse of I + A (four 16x16 diagonal solves, two merges)
-//   P3  delta = T R, O = exp(G) Q S0 + Aqk delta (staged in LDS), S update
+//   P2  in-place blocked inverse of I + A (four 16x16 diagonal solves, two merges; the
+//       merge scratch lives in V's buffer, which is dead by then)
+//   P3  delta = T R, O = exp(G) Q S0 + Aqk delta (staged in LDS), S update with the K^T
+//       operand read through transposing LDS reads
 //   P4  O (or the gated-normed O) -> HBM with 16-byte stores
 #include "common.hpp"
 #include "kernel_args.hpp"
@@ -39,13 +44,20 @@ template <typename T> __device__ __forceinline__ float f(T x) { return (float)x;
 template <typename T> __device__ __forceinline__ float rnd(float x) { return (float)(T)x; }
 
 constexpr int CH = 64, DK = 128, DV = 128;
-constexpr int RS = DK + 8;  // row stride (elements) of Qc / Kc / Vc / O staging
-constexpr int TS = CH + 8;  // row stride of Kt [128][72] and Aq [64][72]
+constexpr int RS = DK + 8;  // row stride (elements) of Qc / Vc / O staging
+constexpr int TS = CH + 8;  // row stride of Aq [64][72]
 constexpr int AS = CH + 4;  // fp32 row stride of A / T [64][68]
-constexpr int XS = 32 + 4;  // fp32 row stride of the merge scratch [32][36]
-constexpr size_t LDS_BYTES = 3 * CH * RS * 2 + DK * TS * 2 + CH * AS * 4 + CH * TS * 2 + 32 * XS * 4 + 2 * CH * 4;
+constexpr int XS = 32 + 4;  // fp32 row stride of the merge scratch [32][36] (in V's buffer)
+// Qc, Vc padded; Kc [64][128] unpadded with an XOR chunk swizzle; A; Aq; g scan; beta:
+// 78,336 B, so two workgroups share a CU (160 KiB of LDS)
+constexpr size_t LDS_BYTES = 2 * CH * RS * 2 + CH * DK * 2 + CH * AS * 4 + CH * TS * 2 + 2 * CH * 4;
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// K rows: 16-byte chunk c of row r sits at chunk c ^ kswz(r). Row writes, the row-major
+// operand reads of K K^T / Q K^T, the permuted reads of K S and the transposing reads of
+// the K^T operand of the state update all reach every LDS bank evenly with this swizzle.
+__device__ __forceinline__ int kswz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+__device__ __forceinline__ float silu(float x) { return fast_silu(x); }
 
 __device__ __forceinline__ float wave_incl_scan(float x, int lane) {
 #pragma unroll
@@ -142,6 +154,14 @@ __device__ __forceinline__ typename Ops<T>::v8 ld_perm(const T* row, int base, i
     v4 hi = *(const v4*)(row + base + 16 * hh + 8 + 4 * g);
     return typename Ops<T>::v8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
+// ld_perm for a swizzled K row (row's swizzle key swk): the same elements as ld_perm at base 32 rb
+template <typename T>
+__device__ __forceinline__ typename Ops<T>::v8 ld_perm_k(const T* row, int swk, int rb, int hh, int g) {
+    typedef typename Ops<T>::v4 v4;
+    v4 lo = *(const v4*)(row + 8 * ((4 * rb + 2 * hh) ^ swk) + 4 * g);
+    v4 hi = *(const v4*)(row + 8 * ((4 * rb + 2 * hh + 1) ^ swk) + 4 * g);
+    return typename Ops<T>::v8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
 template <typename T>
 __device__ __forceinline__ typename Ops<T>::v8 ld_perm_f32(const float* row, int base, int hh, int g) {
     f32x4 lo = *(const f32x4*)(row + base + 16 * hh + 4 * g);
@@ -156,19 +176,22 @@ __device__ __forceinline__ typename Ops<T>::v8 pack(const f32x16& v, int hh) {
     return r;
 }
 
+// Row of accumulator element j minus the lane's 4 g: a compile-time constant, so per-lane
+// addresses are one base (holding the 4 g term) plus an instruction immediate.
+__device__ __forceinline__ constexpr int arow(int j) { return (j >> 2) * 8 + (j & 3); }
+
 template <typename T, bool FUSED>
-__global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) {
+__global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) {
     typedef typename Ops<T>::v8 v8;
     extern __shared__ __attribute__((aligned(16))) char smem[];
     T* Qc = (T*)smem;                       // [64][RS]; later O staging
-    T* Kc = Qc + CH * RS;                   // [64][RS]
-    T* Vc = Kc + CH * RS;                   // [64][RS]
-    T* Kt = Vc + CH * RS;                   // [128][TS]
-    float* Am = (float*)(Kt + DK * TS);     // [64][AS]: A, then T
+    T* Vc = Qc + CH * RS;                   // [64][RS]
+    T* Kc = Vc + CH * RS;                   // [64][DK], chunks swizzled by kswz
+    float* Am = (float*)(Kc + CH * DK);     // [64][AS]: A, then T
     T* Aq = (T*)(Am + CH * AS);             // [64][TS]
-    float* Xs = (float*)(Aq + CH * TS);     // [32][XS]
-    float* Gs = Xs + 32 * XS;
+    float* Gs = (float*)(Aq + CH * TS);
     float* Bs = Gs + CH;
+    float* Xs = (float*)Vc;                 // [32][XS] merge scratch while V is dead (inversion)
 
     const int h = blockIdx.x, seq = blockIdx.y, H = a.H;
     const int t0 = a.cu_seqlens[seq];
@@ -189,46 +212,50 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-            S[rb][j] = a.initial_state ? a.initial_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] : 0.0f;
+            S[rb][j] = a.initial_state ? a.initial_state[sbase + (long)(4 * g) * DV + dvc + (rb * 32 + arow(j)) * DV] : 0.0f;
 
-    float convw[8][4];
-    long mcol = 0;
-    if (FUSED && wave < 3) {
-        const int key_dim = fa.Hk * 128;
-        mcol = wave == 0 ? kh * 128 : wave == 1 ? key_dim + kh * 128 : 2 * key_dim + h * 128;
-        mcol += 8 * sub;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-#pragma unroll
-            for (int tap = 0; tap < 4; ++tap) convw[e][tap] = fa.conv_w[(mcol + e) * 4 + tap];
-    }
+    // fused loader: this lane's 8 q channels; k channels follow at + Hk*128, v channels of
+    // value head h at + 2 Hk*128 + (h - kh)*128
+    const long mcol = (long)kh * 128 + 8 * sub;
 
     for (int c0 = 0; c0 < Tn; c0 += CH) {
         const int Lc = min(CH, Tn - c0);
         __syncthreads();
         // ---------------- P0: inputs -> LDS ----------------
-        if (wave < 3) {
-            T* dst = wave == 0 ? Qc : wave == 1 ? Kc : Vc;
-            if (FUSED) {
-                // raw conv inputs for chunk rows 16rg-3 .. 16rg+15 (sequence position c0 + row);
-                // loads use a clamped position and are zeroed outside [0, Tn) afterwards
-                v8 raw[19];
+        if (FUSED && wave < 3) {
+            // wave ts (q, k, v) convolves chunk rows 16 rg .. 16 rg + 15 of its tensor, channels
+            // 8 sub .. + 7, in two passes of 8 rows, each from an 11-row window of raw conv
+            // inputs (sequence positions c0 + row - 3 ..; clamped loads, zeroed outside [0, Tn))
+            const int ts = wave;
+            const long mc = mcol + ts * (long)fa.Hk * 128 + (ts == 2 ? (long)(h - kh) * 128 : 0);
+            T* dst = ts == 0 ? Qc : ts == 1 ? Kc : Vc;
+            float convw[8][4];  // re-read per chunk (cache hits) rather than held in registers
 #pragma unroll
-                for (int i = 0; i < 19; ++i) {
-                    const int p = c0 + 16 * rg - 3 + i;
+            for (int e = 0; e < 8; ++e) {
+                const f32x4 w4 = *(const f32x4*)(fa.conv_w + (mc + e) * 4);
+#pragma unroll
+                for (int tap = 0; tap < 4; ++tap) convw[e][tap] = w4[tap];
+            }
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int r0 = 16 * rg + 8 * hf;
+                v8 raw[11];
+#pragma unroll
+                for (int i = 0; i < 11; ++i) {
+                    const int p = c0 + r0 - 3 + i;
                     const int pc = p < 0 ? 0 : (p >= Tn ? Tn - 1 : p);
-                    raw[i] = *(const v8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + mcol);
+                    raw[i] = *(const v8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + mc);
                     if (p < 0 || p >= Tn) raw[i] = v8{};
                 }
-                if (fa.hist && c0 == 0 && rg == 0) {
+                if (fa.hist && c0 + r0 == 0) {
 #pragma unroll
                     for (int i = 0; i < 3; ++i)
 #pragma unroll
                         for (int e = 0; e < 8; ++e)
-                            raw[i][e] = ((const T*)fa.hist)[((long)seq * fa.conv_dim + mcol + e) * 3 + i];
+                            raw[i][e] = ((const T*)fa.hist)[((long)seq * fa.conv_dim + mc + e) * 3 + i];
                 }
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
+                for (int i = 0; i < 8; ++i) {
                     float y[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
@@ -237,39 +264,48 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
                         acc += convw[e][1] * f(raw[i + 1][e]);
                         acc += convw[e][2] * f(raw[i + 2][e]);
                         acc += convw[e][3] * f(raw[i + 3][e]);
-                        y[e] = rnd<T>(silu(acc));
+                        y[e] = silu(acc);
                     }
-                    if (wave < 2) {  // l2norm over the head's 128 channels (16 lanes)
+                    if (ts < 2) {  // conv output stored in the activation dtype, then l2norm over
+                                   // the head's 128 channels (16 lanes)
                         float ss = 0.0f;
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+                        for (int e = 0; e < 8; ++e) {
+                            y[e] = rnd<T>(y[e]);
+                            ss += y[e] * y[e];
+                        }
+                        ss = sum16(ss);
+                        const float inv = fast_rsqrt(ss + 1e-6f);
 #pragma unroll
-                        for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-                        const float inv = 1.0f / sqrtf(ss + 1e-6f);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) y[e] = wave == 0 ? (y[e] * inv) * fa.scale : y[e] * inv;
+                        for (int e = 0; e < 8; ++e) y[e] = ts == 0 ? (y[e] * inv) * fa.scale : y[e] * inv;
                     }
-                    const bool live = 16 * rg + i < Lc;
+                    const int r = r0 + i;
+                    const bool live = r < Lc;
                     v8 o;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) o[e] = live ? (T)y[e] : (T)0.0f;
-                    *(v8*)(dst + (16 * rg + i) * RS + 8 * sub) = o;
+                    *(v8*)(dst + (ts == 1 ? r * DK + 8 * (sub ^ kswz(r)) : r * RS + 8 * sub)) = o;
                 }
-            } else {
-                const T* src = wave == 0 ? (const T*)a.q + (long)kh * DK
-                             : wave == 1 ? (const T*)a.k + (long)kh * DK : (const T*)a.v + (long)h * DV;
-                const long tok = wave == 0 ? a.q_tok : wave == 1 ? a.k_tok : a.v_tok;
-                v8 x[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int r = 16 * rg + i;
-                    x[i] = *(const v8*)(src + (long)(t0 + c0 + (r < Lc ? r : Lc - 1)) * tok + 8 * sub);
-                    if (r >= Lc) x[i] = v8{};
-                }
-#pragma unroll
-                for (int i = 0; i < 16; ++i) *(v8*)(dst + (16 * rg + i) * RS + 8 * sub) = x[i];
             }
-        } else {
+        } else if (wave < 3) {
+            T* dst = wave == 0 ? Qc : wave == 1 ? Kc : Vc;
+            const T* src = wave == 0 ? (const T*)a.q + (long)kh * DK
+                         : wave == 1 ? (const T*)a.k + (long)kh * DK : (const T*)a.v + (long)h * DV;
+            const long tok = wave == 0 ? a.q_tok : wave == 1 ? a.k_tok : a.v_tok;
+            v8 x[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = 16 * rg + i;
+                x[i] = *(const v8*)(src + (long)(t0 + c0 + (r < Lc ? r : Lc - 1)) * tok + 8 * sub);
+                if (r >= Lc) x[i] = v8{};
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = 16 * rg + i;
+                *(v8*)(dst + (wave == 1 ? r * DK + 8 * (sub ^ kswz(r)) : r * RS + 8 * sub)) = x[i];
+            }
+        }
+        if (wave == 3) {  // g (inclusive scan over the chunk) and beta
             float gv = 0.0f, bv = 0.0f;
             if (lane < Lc) {
                 const long tt = t0 + c0 + lane;
@@ -277,7 +313,7 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
                     const T* row = (const T*)fa.ba + tt * fa.ba_tok;
                     const float b = f(row[fa.b_col + h]);
                     const float av = f(row[fa.a_col + h]);
-                    bv = rnd<T>(1.0f / (1.0f + __expf(-b)));
+                    bv = rnd<T>(fast_sigmoid(b));
                     gv = fa.base_g[h] * __logf(__expf(av + fa.dt_bias[h]) + 1.0f);
                 } else {
                     gv = a.g[tt * a.gb_tok + h];
@@ -289,37 +325,34 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
         }
         __syncthreads();
         // ---------------- P1: A, Aqk; K S0, Q S0 ----------------
-        {  // k transposed for the state update (read in P3, after the inversion's barriers):
-            // thread t moves rows 4*(t/16)..+3, channels 8*(t%16)..+7
-            typedef typename Ops<T>::v4 v4;
-            const int r0 = 4 * (tid >> 4), d0 = 8 * (tid & 15);
-            v8 k0 = *(const v8*)(Kc + (r0 + 0) * RS + d0);
-            v8 k1 = *(const v8*)(Kc + (r0 + 1) * RS + d0);
-            v8 k2 = *(const v8*)(Kc + (r0 + 2) * RS + d0);
-            v8 k3 = *(const v8*)(Kc + (r0 + 3) * RS + d0);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) *(v4*)(Kt + (d0 + e) * TS + r0) = v4{k0[e], k1[e], k2[e], k3[e]};
-        }
         if (wave < 3) {
             const int tb = wave == 0 ? 0 : 1, sb = wave == 2 ? 1 : 0;
             f32x16 kk = f32x16{}, qk = f32x16{};
-            const T* ka = Kc + (tb * 32 + col) * RS + g * 8;
+            int swk = kswz(col);  // K rows tb*32 + col and sb*32 + col share it
+            asm volatile("" : "+v"(swk));  // recompute the swizzled addresses here, not hoisted and spilled
+            const T* ka = Kc + (tb * 32 + col) * DK;
             const T* qa = Qc + (tb * 32 + col) * RS + g * 8;
-            const T* kbp = Kc + (sb * 32 + col) * RS + g * 8;
+            const T* kbp = Kc + (sb * 32 + col) * DK;
 #pragma unroll
             for (int ks = 0; ks < 8; ++ks) {
-                v8 bv = *(const v8*)(kbp + ks * 16);
-                kk = Ops<T>::mma(*(const v8*)(ka + ks * 16), bv, kk);
+                const int ko = 8 * ((2 * ks + g) ^ swk);
+                v8 bv = *(const v8*)(kbp + ko);
+                kk = Ops<T>::mma(*(const v8*)(ka + ko), bv, kk);
                 qk = Ops<T>::mma(*(const v8*)(qa + ks * 16), bv, qk);
             }
             const int s = sb * 32 + col;
             const float gs = Gs[s];
+            const int t4 = tb * 32 + 4 * g;  // this lane's accumulator rows: t4 + arow(j)
+            const float* gt = Gs + t4;
+            const float* bt = Bs + t4;
+            float* am = Am + t4 * AS + s;
+            T* aq = Aq + t4 * TS + s;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const int t = tb * 32 + acc_row(j, g);
-                const float dec = s <= t ? __expf(Gs[t] - gs) : 0.0f;
-                Am[t * AS + s] = s < t ? Bs[t] * dec * kk[j] : 0.0f;
-                Aq[t * TS + s] = (T)(dec * qk[j]);
+                const int t = t4 + arow(j);
+                const float dec = s <= t ? __expf(gt[arow(j)] - gs) : 0.0f;
+                am[arow(j) * AS] = s < t ? bt[arow(j)] * dec * kk[j] : 0.0f;
+                aq[arow(j) * TS] = (T)(dec * qk[j]);
             }
         } else {
             for (int idx = lane; idx < 32 * 32; idx += 64) {
@@ -334,24 +367,30 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
             Sb[rb][0] = pack<T>(S[rb], 0);
             Sb[rb][1] = pack<T>(S[rb], 1);
         }
-        f32x16 R[2], Og[2];
+        v8 Rb[2][2];  // R = beta (V - exp(G) K S0), packed as the B operand of T R
+        f32x16 Og[2];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
             f32x16 ks = f32x16{}, qs = f32x16{};
-            const T* kr = Kc + (tb * 32 + col) * RS;
+            const T* kr = Kc + (tb * 32 + col) * DK;
             const T* qr = Qc + (tb * 32 + col) * RS;
+            int swk = kswz(col);
+            asm volatile("" : "+v"(swk));
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
-                    ks = Ops<T>::mma(ld_perm<T>(kr, rb * 32, hh, g), Sb[rb][hh], ks);
+                    ks = Ops<T>::mma(ld_perm_k<T>(kr, swk, rb, hh, g), Sb[rb][hh], ks);
                     qs = Ops<T>::mma(ld_perm<T>(qr, rb * 32, hh, g), Sb[rb][hh], qs);
                 }
+            const int t4 = tb * 32 + 4 * g;
+            const float* gt = Gs + t4;
+            const float* bt = Bs + t4;
+            const T* vt = Vc + t4 * RS + dvc;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const int t = tb * 32 + acc_row(j, g);
-                const float eg = __expf(Gs[t]);
-                R[tb][j] = Bs[t] * (f(Vc[t * RS + dvc]) - eg * ks[j]);
+                const float eg = __expf(gt[arow(j)]);
+                Rb[tb][j >> 3][j & 7] = (T)(bt[arow(j)] * (f(vt[arow(j) * RS]) - eg * ks[j]));
                 Og[tb][j] = eg * qs[j];
             }
         }
@@ -359,12 +398,6 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
         // ---------------- P2: T = (I + A)^-1 in place ----------------
         invert_in_place(Am, Xs, wave, lane);
         // ---------------- P3: delta, O, state ----------------
-        v8 Rb[2][2];
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-            Rb[sb][0] = pack<T>(R[sb], 0);
-            Rb[sb][1] = pack<T>(R[sb], 1);
-        }
         f32x16 dl[2];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
@@ -394,27 +427,49 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) Os[(tb * 32 + acc_row(j, g)) * RS + dvc] = (T)Og[tb][j];
+            for (int j = 0; j < 16; ++j) Os[(4 * g) * RS + dvc + (tb * 32 + arow(j)) * RS] = (T)Og[tb][j];
         const float glast = Gs[CH - 1];
         const float eglast = __expf(glast);
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) dl[tb][j] *= __expf(glast - Gs[tb * 32 + acc_row(j, g)]);
+            for (int j = 0; j < 16; ++j) dl[tb][j] *= __expf(glast - Gs[4 * g + tb * 32 + arow(j)]);
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
             Db[tb][0] = pack<T>(dl[tb], 0);
             Db[tb][1] = pack<T>(dl[tb], 1);
         }
+        // S = e^{G_last} S + K^T (e^{G_last - G} delta). The A operand K^T[dk][t] (tokens
+        // 32 tb + 16 hh + 8 x + 4 g + [0..3] for x = 0, 1) comes from transposing reads of K:
+        // in 16-lane group G, lane j reads token 4 (G >> 1) + 8 x + (j >> 2) + 32 tb + 16 hh,
+        // dims 32 rb + 16 (G & 1) + 4 (j & 3) .. + 3
+        {
+            int G = lane >> 4, j = lane & 15;
+            asm volatile("" : "+v"(G), "+v"(j));
+            int tofs[2][4];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+            for (int x = 0; x < 2; ++x)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) S[rb][j] *= eglast;
-            const T* ktr = Kt + (rb * 32 + col) * TS;
+                for (int rb = 0; rb < 4; ++rb) {
+                    const int rr = 8 * x + 4 * (G >> 1) + (j >> 2);  // token row mod 32, without 16 hh
+                    const int sw = ((j >> 2) << 2) | ((2 * x + (G >> 1)) & 3);
+                    tofs[x][rb] = rr * DK + 8 * ((4 * rb + 2 * (G & 1) + ((j & 3) >> 1)) ^ sw) + 4 * (j & 1);
+                }
 #pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
+            for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) S[rb] = Ops<T>::mma(ld_perm<T>(ktr, tb * 32, hh, g), Db[tb][hh], S[rb]);
+                for (int jj = 0; jj < 16; ++jj) S[rb][jj] *= eglast;
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const T* kb = Kc + (tb * 32 + 16 * hh) * DK;
+                        const i16x4 lo = lds_read_tr16(kb + tofs[0][rb]);
+                        const i16x4 hi = lds_read_tr16(kb + tofs[1][rb]);
+                        const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                        S[rb] = Ops<T>::mma(af, Db[tb][hh], S[rb]);
+                    }
+            }
         }
         __syncthreads();
         // ---------------- P4: O -> HBM (gated RMSNorm when fused) ----------------
@@ -432,15 +487,14 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
                         x[e] = f(ov[e]);
                         ss += x[e] * x[e];
                     }
-#pragma unroll
-                    for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+                    ss = sum16(ss);
                     if (r < Lc) {
-                        const float denom = sqrtf(ss / 128.0f + fa.eps);
+                        const float inv = fast_rsqrt(ss * (1.0f / 128.0f) + fa.eps);
                         v8 zv = *(const v8*)((const T*)fa.z + tt * fa.z_tok + (long)h * DV + 8 * rsub);
                         v8 y;
 #pragma unroll
                         for (int e = 0; e < 8; ++e)
-                            y[e] = (T)(((x[e] / denom) * fa.norm_w[8 * rsub + e]) * silu(f(zv[e])));
+                            y[e] = (T)(((x[e] * inv) * fa.norm_w[8 * rsub + e]) * silu(f(zv[e])));
                         *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
                     }
                 } else if (r < Lc) {
@@ -453,29 +507,29 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a.final_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] = S[rb][j];
+            for (int j = 0; j < 16; ++j) a.final_state[sbase + (long)(4 * g) * DV + dvc + (rb * 32 + arow(j)) * DV] = S[rb][j];
     }
-    if (FUSED && fa.tail_out && wave < 3) {
-        // cache tail: the last 3 raw conv inputs of [history, sequence] for this lane's channels
-        if (rg == 0) {
+    if (FUSED && fa.tail_out && wave < 3 && rg == 0) {
+        // cache tail: the last 3 raw conv inputs of [history, sequence]; wave ts writes the
+        // channels of q, k or v (16 lanes x 8 channels)
+        const long mc = mcol + wave * (long)fa.Hk * 128 + (wave == 2 ? (long)(h - kh) * 128 : 0);
 #pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                const int p = Tn - 3 + i;
-                float v[8];
+        for (int i = 0; i < 3; ++i) {
+            const int p = Tn - 3 + i;
+            float v[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = 0.0f;
-                if (p >= 0) {
-                    v8 x = *(const v8*)((const T*)fa.mixed + (long)(t0 + p) * fa.mixed_tok + mcol);
+            for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+            if (p >= 0) {
+                v8 x = *(const v8*)((const T*)fa.mixed + (long)(t0 + p) * fa.mixed_tok + mc);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = f(x[e]);
-                } else if (fa.hist) {
+                for (int e = 0; e < 8; ++e) v[e] = f(x[e]);
+            } else if (fa.hist) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        v[e] = f(((const T*)fa.hist)[((long)seq * fa.conv_dim + mcol + e) * 3 + (p + 3)]);
-                }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ((T*)fa.tail_out)[((long)seq * fa.conv_dim + mcol + e) * 3 + i] = (T)v[e];
+                for (int e = 0; e < 8; ++e)
+                    v[e] = f(((const T*)fa.hist)[((long)seq * fa.conv_dim + mc + e) * 3 + (p + 3)]);
             }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ((T*)fa.tail_out)[((long)seq * fa.conv_dim + mc + e) * 3 + i] = (T)v[e];
         }
     }
 }
