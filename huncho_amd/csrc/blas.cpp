@@ -3,13 +3,19 @@
 // Row-major Y[n][out] = alpha * X[n][in] . W[out][in]^T + beta * C is the column-major
 // product Y^T = W . X^T: m = out, n = n, k = in, op(A) = T on the weight, op(B) = N on the
 // activations. bf16 or fp16 operands with fp32 accumulation (HIPBLAS_COMPUTE_32F), or fp32.
-// Plans (descriptors + the fastest of up to 16 heuristic algorithms, timed once on first
-// use of a shape) are cached per shape; the workspace is owned by the context and allocated
-// on the first GEMM.
+// Plans (descriptors + the fastest algorithm for the shape) are cached per shape. On first
+// use of a shape every solution hipBLASLt offers for the layout (the heuristic's list plus
+// the full solution list, filtered by matmulIsAlgoSupported) is timed once, and the best 8
+// again over 3 launches. The workspace is owned by the context and allocated on the first
+// GEMM.
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <map>
 #include <tuple>
+#include <utility>
+#include <vector>
 
 #include "abi_internal.hpp"
 
@@ -69,12 +75,46 @@ static int blas_init(hk_ctx* ctx) {
     return HK_OK;
 }
 
-// Times every returned candidate (3 launches each, beta = 0 into a scratch output so the
-// caller's buffers are untouched) and returns the index of the fastest; 0 if timing fails.
-template <typename P, typename R>
-static int pick_fastest(hk_ctx* ctx, P& p, R* res, int returned, int dtype, int out, int n, const void* x,
-                        const void* w, void* y, long ldy) {
-    if (returned <= 1) return 0;
+// Candidate algorithms for a plan: the heuristic's ranking first, then every other solution
+// of the full list that supports the problem with the context's workspace.
+static std::vector<std::pair<hipblasLtMatmulAlgo_t, size_t>> candidates(hk_ctx* ctx, Plan& p, hipDataType t,
+                                                                          const hipblasLtMatmulHeuristicResult_t* res,
+                                                                          int returned) {
+    hk_blas* B = ctx->blas;
+    std::vector<std::pair<hipblasLtMatmulAlgo_t, size_t>> out;
+    std::vector<int> seen;
+    for (int i = 0; i < returned; ++i) {
+        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > B->ws_bytes) continue;
+        hipblasLtMatmulAlgo_t algo = res[i].algo;
+        seen.push_back(hipblaslt_ext::getIndexFromAlgo(algo));
+        out.emplace_back(algo, res[i].workspaceSize);
+    }
+    std::vector<hipblasLtMatmulHeuristicResult_t> all;
+    if (hipblaslt_ext::getAllAlgos(B->handle, hipblaslt_ext::GemmType::HIPBLASLT_GEMM, HIPBLAS_OP_T, HIPBLAS_OP_N, t, t,
+                                   t, t, HIPBLAS_COMPUTE_32F, all) != HIPBLAS_STATUS_SUCCESS)
+        return out;
+    const float one = 1.0f, zero = 0.0f;
+    for (auto& r : all) {
+        hipblasLtMatmulAlgo_t algo = r.algo;
+        const int idx = hipblaslt_ext::getIndexFromAlgo(algo);
+        if (std::find(seen.begin(), seen.end(), idx) != seen.end()) continue;
+        size_t ws = 0;
+        if (hipblaslt_ext::matmulIsAlgoSupported(B->handle, p.desc, &one, p.a, p.b, &zero, p.c, p.d, algo, ws) !=
+                HIPBLAS_STATUS_SUCCESS ||
+            ws > B->ws_bytes)
+            continue;
+        seen.push_back(idx);
+        out.emplace_back(algo, ws);
+    }
+    return out;
+}
+
+// Times the candidates (beta = 0 into a scratch output, so the caller's buffers are
+// untouched): one launch each, then the best 8 over 3 launches. Returns the index of the
+// fastest; 0 if timing fails.
+static int pick_fastest(hk_ctx* ctx, Plan& p, std::vector<std::pair<hipblasLtMatmulAlgo_t, size_t>>& cands, int dtype,
+                        int n, const void* x, const void* w, long ldy) {
+    if (cands.size() <= 1) return 0;
     hk_blas* B = ctx->blas;
     void* scratch = nullptr;
     const size_t bytes = (size_t)ldy * n * (dtype == HK_F32 ? 4 : 2);
@@ -83,30 +123,36 @@ static int pick_fastest(hk_ctx* ctx, P& p, R* res, int returned, int dtype, int 
     hipEventCreate(&e0);
     hipEventCreate(&e1);
     const float one = 1.0f, zero = 0.0f;
-    int best = 0;
-    float best_ms = 1e30f;
-    for (int i = 0; i < returned; ++i) {
-        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > B->ws_bytes) continue;
+    auto time_algo = [&](int i, int reps) -> float {
         bool ok = hipblasLtMatmul(B->handle, p.desc, &one, w, p.a, x, p.b, &zero, scratch, p.d, scratch, p.d,
-                                  &res[i].algo, B->workspace, res[i].workspaceSize, ctx->stream) == HIPBLAS_STATUS_SUCCESS;
+                                  &cands[i].first, B->workspace, cands[i].second, ctx->stream) == HIPBLAS_STATUS_SUCCESS;
         hipEventRecord(e0, ctx->stream);
-        for (int r = 0; ok && r < 3; ++r)
+        for (int r = 0; ok && r < reps; ++r)
             ok = hipblasLtMatmul(B->handle, p.desc, &one, w, p.a, x, p.b, &zero, scratch, p.d, scratch, p.d,
-                                 &res[i].algo, B->workspace, res[i].workspaceSize, ctx->stream) == HIPBLAS_STATUS_SUCCESS;
+                                 &cands[i].first, B->workspace, cands[i].second, ctx->stream) == HIPBLAS_STATUS_SUCCESS;
         hipEventRecord(e1, ctx->stream);
         float ms = 0.0f;
-        if (ok && hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess &&
-            ms < best_ms) {
+        if (!ok || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1e30f;
+        return ms / reps;
+    };
+    std::vector<std::pair<float, int>> t1;
+    for (int i = 0; i < (int)cands.size(); ++i) t1.emplace_back(time_algo(i, 1), i);
+    std::sort(t1.begin(), t1.end());
+    int best = t1[0].second;
+    float best_ms = 1e30f;
+    for (int k = 0; k < (int)t1.size() && k < 8; ++k) {
+        if (t1[k].first >= 1e29f) break;
+        const float ms = time_algo(t1[k].second, 3);
+        if (ms < best_ms) {
             best_ms = ms;
-            best = i;
+            best = t1[k].second;
         }
     }
     hipStreamSynchronize(ctx->stream);
+    (void)hipGetLastError();
     hipEventDestroy(e0);
     hipEventDestroy(e1);
     hipFree(scratch);
-    (void)out;
-    (void)y;
     return best;
 }
 
@@ -153,9 +199,18 @@ int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, l
             if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
             return hk_fail(ctx, HK_ERR_UNSUPPORTED, "no hipBLASLt algorithm for %dx%dx%d", out, n, in);
         }
-        int best = pick_fastest(ctx, p, res, returned, dtype, out, n, x, w, y, ldy);
-        p.algo = res[best].algo;
-        p.ws = res[best].workspaceSize;
+        auto cands = candidates(ctx, p, t, res, returned);
+        if (cands.empty()) {
+            hipblasLtMatrixLayoutDestroy(p.a);
+            hipblasLtMatrixLayoutDestroy(p.b);
+            hipblasLtMatrixLayoutDestroy(p.c);
+            hipblasLtMatrixLayoutDestroy(p.d);
+            hipblasLtMatmulDescDestroy(p.desc);
+            return hk_fail(ctx, HK_ERR_UNSUPPORTED, "no usable hipBLASLt algorithm for %dx%dx%d", out, n, in);
+        }
+        const int best = pick_fastest(ctx, p, cands, dtype, n, x, w, ldy);
+        p.algo = cands[best].first;
+        p.ws = cands[best].second;
         it = B->plans.emplace(key, p).first;
     }
     Plan& p = it->second;
