@@ -38,11 +38,19 @@ template <> __device__ __forceinline__ float from_f<float>(float x) { return x; 
 template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) { return (bf16)x; }
 template <> __device__ __forceinline__ f16 from_f<f16>(float x) { return (f16)x; }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// a.x b.x + a.y b.y + c with fp32 accumulation (v_dot2_f32_bf16 / v_dot2_f32_f16); the
+// products of two 16-bit values are exact in fp32
+__device__ __forceinline__ float dot2(bf16x2 a, bf16x2 b, float c) { return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false); }
+__device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
 // 32x32x16 MFMA for the two 16-bit operand types (same lane layout).
 template <typename T> struct Mma16;
 template <> struct Mma16<bf16> {
     typedef bf16x8 v8;
     typedef bf16x4 v4;
+    typedef bf16x2 v2;
     static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
@@ -50,6 +58,7 @@ template <> struct Mma16<bf16> {
 template <> struct Mma16<f16> {
     typedef f16x8 v8;
     typedef f16x4 v4;
+    typedef f16x2 v2;
     static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
     }

@@ -225,16 +225,21 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
         if (FUSED && wave < 3) {
             // wave ts (q, k, v) convolves chunk rows 16 rg .. 16 rg + 15 of its tensor, channels
             // 8 sub .. + 7, in two passes of 8 rows, each from an 11-row window of raw conv
-            // inputs (sequence positions c0 + row - 3 ..; clamped loads, zeroed outside [0, Tn))
+            // inputs (sequence positions c0 + row - 3 ..). Positions past the sequence end are
+            // loaded clamped: they only reach rows past the end, whose beta is 0 and whose
+            // outputs are not stored. Positions before the start are the conv history or 0.
+            typedef typename Ops<T>::v2 v2;
             const int ts = wave;
             const long mc = mcol + ts * (long)fa.Hk * 128 + (ts == 2 ? (long)(h - kh) * 128 : 0);
             T* dst = ts == 0 ? Qc : ts == 1 ? Kc : Vc;
-            float convw[8][4];  // re-read per chunk (cache hits) rather than held in registers
+            // taps (0, 1) and (2, 3) of each channel as 16-bit pairs (the weights are the model
+            // dtype's values, exact in T), re-read per chunk rather than held in registers
+            v2 w01[8], w23[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const f32x4 w4 = *(const f32x4*)(fa.conv_w + (mc + e) * 4);
-#pragma unroll
-                for (int tap = 0; tap < 4; ++tap) convw[e][tap] = w4[tap];
+                w01[e] = v2{(T)w4[0], (T)w4[1]};
+                w23[e] = v2{(T)w4[2], (T)w4[3]};
             }
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
@@ -245,25 +250,22 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
                     const int p = c0 + r0 - 3 + i;
                     const int pc = p < 0 ? 0 : (p >= Tn ? Tn - 1 : p);
                     raw[i] = *(const v8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + mc);
-                    if (p < 0 || p >= Tn) raw[i] = v8{};
                 }
-                if (fa.hist && c0 + r0 == 0) {
+                if (c0 + r0 == 0) {  // window starts 3 positions before the sequence
 #pragma unroll
                     for (int i = 0; i < 3; ++i)
 #pragma unroll
                         for (int e = 0; e < 8; ++e)
-                            raw[i][e] = ((const T*)fa.hist)[((long)seq * fa.conv_dim + mc + e) * 3 + i];
+                            raw[i][e] = fa.hist ? ((const T*)fa.hist)[((long)seq * fa.conv_dim + mc + e) * 3 + i]
+                                                : (T)0.0f;
                 }
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     float y[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        float acc = 0.0f;
-                        acc += convw[e][0] * f(raw[i][e]);
-                        acc += convw[e][1] * f(raw[i + 1][e]);
-                        acc += convw[e][2] * f(raw[i + 2][e]);
-                        acc += convw[e][3] * f(raw[i + 3][e]);
+                        const float acc = dot2(w23[e], v2{raw[i + 2][e], raw[i + 3][e]},
+                                               dot2(w01[e], v2{raw[i][e], raw[i + 1][e]}, 0.0f));
                         y[e] = silu(acc);
                     }
                     if (ts < 2) {  // conv output stored in the activation dtype, then l2norm over
@@ -280,10 +282,9 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
                         for (int e = 0; e < 8; ++e) y[e] = ts == 0 ? (y[e] * inv) * fa.scale : y[e] * inv;
                     }
                     const int r = r0 + i;
-                    const bool live = r < Lc;
                     v8 o;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) o[e] = live ? (T)y[e] : (T)0.0f;
+                    for (int e = 0; e < 8; ++e) o[e] = (T)y[e];
                     *(v8*)(dst + (ts == 1 ? r * DK + 8 * (sub ^ kswz(r)) : r * RS + 8 * sub)) = o;
                 }
             }
@@ -471,35 +472,44 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
                     }
             }
         }
-        __syncthreads();
-        // ---------------- P4: O -> HBM (gated RMSNorm when fused) ----------------
-        {
-            const int rsub = tid & 15, rrow = tid >> 4;  // 16 lanes per row, 16 rows per pass
+        // P4 operands that do not depend on O: the gate norm_w * silu(z) of this thread's rows,
+        // computed before the barrier (rows past the end read a clamped row and are not stored)
+        const int rsub = tid & 15, rrow = tid >> 4;  // 16 lanes per row, 16 rows per pass
+        float gz[4][8];
+        if (FUSED) {
+            v8 zv[4];
 #pragma unroll
             for (int pass = 0; pass < 4; ++pass) {
-                const int r = pass * 16 + rrow;
-                v8 ov = *(const v8*)(Os + r * RS + 8 * rsub);
-                const long tt = t0 + c0 + r;
-                if (FUSED) {
-                    float x[8], ss = 0.0f;
+                const long tt = t0 + c0 + min(pass * 16 + rrow, Lc - 1);
+                zv[pass] = *(const v8*)((const T*)fa.z + tt * fa.z_tok + (long)h * DV + 8 * rsub);
+            }
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        x[e] = f(ov[e]);
-                        ss += x[e] * x[e];
-                    }
-                    ss = sum16(ss);
-                    if (r < Lc) {
-                        const float inv = fast_rsqrt(ss * (1.0f / 128.0f) + fa.eps);
-                        v8 zv = *(const v8*)((const T*)fa.z + tt * fa.z_tok + (long)h * DV + 8 * rsub);
-                        v8 y;
+            for (int pass = 0; pass < 4; ++pass)
 #pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            y[e] = (T)(((x[e] * inv) * fa.norm_w[8 * rsub + e]) * silu(f(zv[e])));
-                        *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
-                    }
-                } else if (r < Lc) {
-                    *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = ov;
+                for (int e = 0; e < 8; ++e) gz[pass][e] = fa.norm_w[8 * rsub + e] * silu(f(zv[pass][e]));
+        }
+        __syncthreads();
+        // ---------------- P4: O -> HBM (gated RMSNorm when fused) ----------------
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int r = pass * 16 + rrow;
+            const v8 ov = *(const v8*)(Os + r * RS + 8 * rsub);
+            const long tt = t0 + c0 + r;
+            if (FUSED) {
+                float x[8], ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    x[e] = f(ov[e]);
+                    ss += x[e] * x[e];
                 }
+                ss = sum16(ss);
+                const float inv = fast_rsqrt(ss * (1.0f / 128.0f) + fa.eps);
+                v8 y;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) y[e] = (T)((x[e] * inv) * gz[pass][e]);
+                if (r < Lc) *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
+            } else if (r < Lc) {
+                *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = ov;
             }
         }
     }
