@@ -135,6 +135,29 @@ int ho_qwen_forward(const ho_qwen_cfg* cfg, const ho_qwen_layer* layers, const f
                     float* hidden_out);
 
 /* y[n][out] = x[n][in] . W[out][in]^T (+ b), fp32 accumulation. */
+/* ---- ModernBERT encoder (ho_bert.c; the Laya backend's candle ModernBERT) ---- */
+void ho_layer_norm(const float* x, const float* w, int rows, int width, float eps, float* y);
+float ho_gelu_erf(float x);
+int ho_bidir_attention(const float* q, const float* k, const float* v, const int32_t* cu_seqlens, int n_seqs,
+                       int heads, int d, int half_window, float scale, float* out);
+typedef struct {
+    int hidden, n_layers, n_heads, head_dim, intermediate, vocab;
+    float eps;
+    int global_every;    /* layer i is global iff i % global_every == 0 */
+    int local_window;    /* local layers see keys with |i - j| <= local_window / 2 */
+    double global_theta, local_theta;
+} ho_bert_cfg;
+typedef struct {
+    const float* attn_norm;       /* [H] or NULL (identity) */
+    const float *wqkv, *wo;       /* [3H][H], [H][H] */
+    const float* mlp_norm;        /* [H] */
+    const float *wi, *wo2;        /* [2I][H], [H][I] */
+} ho_bert_layer;
+/* Final-normed hidden states [T][H] of an unpadded varlen batch (cu_seqlens [n_seqs + 1]). */
+int ho_bert_forward(const ho_bert_cfg* cfg, const ho_bert_layer* layers, const float* embed, const float* emb_norm,
+                    const float* final_norm, const int32_t* ids, const int32_t* cu_seqlens, int n_seqs, int bf16_mode,
+                    float* out);
+
 void ho_linear(const float* x, const float* w, const float* b, int n, int in, int out, float* y);
 
 /* ---- readout and calibration -------------------------------------------

@@ -4,10 +4,12 @@ TEST INFRASTRUCTURE ONLY: the parity checker and the timed CPU baseline. Only te
 __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, and only
 as the checker; the product (huncho_amd, libhuncho_rocm) never does.
 
-Besides the C entry points this module restates, in numpy, the two load-time steps the
-full-model oracle needs:
-  * Config::from_value (crates/huncho-backend/src/qwen3_5.rs:77-166), and
-  * merge_lora_into_map (qwen3_5.rs:1597-1640): W' = W + (alpha/r) * (B @ A) in fp32.
+Besides the C entry points this module restates, in numpy, the load-time steps the
+full-model oracles need:
+  * Config::from_value (crates/huncho-backend/src/qwen3_5.rs:77-166),
+  * merge_lora_into_map (qwen3_5.rs:1597-1640): W' = W + (alpha/r) * (B @ A) in fp32,
+  * the ModernBERT config normalisation and key remapping of the Laya backend
+    (crates/huncho-backend/src/candle.rs:157-231).
 """
 from __future__ import annotations
 
@@ -70,6 +72,13 @@ def lib() -> C.CDLL:
         L.ho_calibrate.restype = C.c_int
         L.ho_calibrate.argtypes = [_f32p, C.c_int, C.c_float, _f32p]
         L.ho_qwen_forward.restype = C.c_int
+        L.ho_layer_norm.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_float, _f32p]
+        L.ho_gelu_erf.restype = C.c_float
+        L.ho_gelu_erf.argtypes = [C.c_float]
+        L.ho_bidir_attention.restype = C.c_int
+        L.ho_bidir_attention.argtypes = [_f32p, _f32p, _f32p, _i32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                         C.c_float, _f32p]
+        L.ho_bert_forward.restype = C.c_int
         _lib = L
     return _lib
 
@@ -442,3 +451,142 @@ def load_tiny_kev(root: Path):
     head = json.loads((root / "head.json").read_text())
     golden = json.loads((root / "golden.json").read_text())
     return cfg, weights, head, golden
+
+
+# ---------------------------------------------------------------------------
+# ModernBERT (Laya backend: crates/huncho-backend/src/candle.rs)
+# ---------------------------------------------------------------------------
+
+def layer_norm(x, w, eps=1e-5):
+    x = f32(x)
+    y = np.empty_like(x)
+    lib().ho_layer_norm(x, f32(w), x.size // x.shape[-1], x.shape[-1], eps, y)
+    return y
+
+
+def bidir_attention(q, k, v, cu_seqlens, half_window=-1, scale=None):
+    """q, k, v [tokens, heads, d]; keys with |i - j| <= half_window (all when < 0)."""
+    q, k, v = f32(q), f32(k), f32(v)
+    tokens, heads, d = q.shape
+    out = np.zeros_like(q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    rc = lib().ho_bidir_attention(q, k, v, i32(cu_seqlens), len(cu_seqlens) - 1, heads, d, int(half_window),
+                                  float(scale), out)
+    if rc != 0:
+        raise ValueError("oracle bidir_attention rejected its inputs")
+    return out
+
+
+@dataclass
+class BertConfig:
+    hidden_size: int
+    num_hidden_layers: int
+    num_attention_heads: int
+    intermediate_size: int
+    vocab_size: int
+    layer_norm_eps: float = 1e-5
+    global_attn_every_n_layers: int = 3
+    local_attention: int = 128
+    global_rope_theta: float = 10000.0
+    local_rope_theta: float = 10000.0
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+    @staticmethod
+    def from_json(v: dict) -> "BertConfig":
+        """candle.rs:157-203 (defaults and the rope_parameters fallbacks included)."""
+        rp = v.get("rope_parameters") or {}
+        g_theta = v.get("global_rope_theta", (rp.get("full_attention") or {}).get("rope_theta", 10000.0))
+        l_theta = v.get("local_rope_theta", (rp.get("sliding_attention") or {}).get("rope_theta", 10000.0))
+        return BertConfig(hidden_size=v.get("hidden_size", 0), num_hidden_layers=v.get("num_hidden_layers", 12),
+                          num_attention_heads=v.get("num_attention_heads", 12),
+                          intermediate_size=v.get("intermediate_size", 3072), vocab_size=v.get("vocab_size", 0),
+                          layer_norm_eps=float(v.get("layer_norm_eps", 1e-5)),
+                          global_attn_every_n_layers=v.get("global_attn_every_n_layers", 3),
+                          local_attention=v.get("local_attention", 128), global_rope_theta=float(g_theta),
+                          local_rope_theta=float(l_theta))
+
+
+def remap_bert_key(name: str):
+    """candle.rs:205-231: `encoder.*` -> `model.*`; `model.*` and Laya head keys kept; the rest dropped."""
+    if name.startswith("encoder."):
+        return "model." + name[len("encoder."):]
+    if name.startswith(("model.", "head.", "type_emb.", "scorer.")):
+        return name
+    return None
+
+
+class _BertCfg(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("n_layers", C.c_int), ("n_heads", C.c_int), ("head_dim", C.c_int),
+                ("intermediate", C.c_int), ("vocab", C.c_int), ("eps", C.c_float), ("global_every", C.c_int),
+                ("local_window", C.c_int), ("global_theta", C.c_double), ("local_theta", C.c_double)]
+
+
+_BERT_FIELDS = [("attn_norm", "attn_norm.weight"), ("wqkv", "attn.Wqkv.weight"), ("wo", "attn.Wo.weight"),
+                ("mlp_norm", "mlp_norm.weight"), ("wi", "mlp.Wi.weight"), ("wo2", "mlp.Wo.weight")]
+
+
+class _BertLayer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n, _ in _BERT_FIELDS]
+
+
+class BertModel:
+    """ModernBERT encoder over `model.*` weights (after remap_bert_key) on the C oracle
+    (ho_bert_forward). bf16=True rounds the weights and every stored intermediate."""
+
+    def __init__(self, cfg: BertConfig, weights: dict, bf16: bool = False):
+        self.cfg = cfg
+        self.bf16 = bf16
+        rnd = round_bf16 if bf16 else f32
+        self.keep = []
+        self.embed = rnd(weights["model.embeddings.tok_embeddings.weight"])
+        self.emb_norm = rnd(weights["model.embeddings.norm.weight"])
+        self.final_norm = rnd(weights["model.final_norm.weight"])
+        layers = (_BertLayer * cfg.num_hidden_layers)()
+        for i in range(cfg.num_hidden_layers):
+            for f, name in _BERT_FIELDS:
+                key = f"model.layers.{i}.{name}"
+                if key not in weights:
+                    if f == "attn_norm":
+                        continue  # identity
+                    raise KeyError(key)
+                a = f32(rnd(weights[key]))
+                self.keep.append(a)
+                setattr(layers[i], f, a.ctypes.data_as(C.c_void_p).value)
+        self.layers = layers
+        self.ccfg = _BertCfg(cfg.hidden_size, cfg.num_hidden_layers, cfg.num_attention_heads, cfg.head_dim,
+                             cfg.intermediate_size, cfg.vocab_size, cfg.layer_norm_eps,
+                             cfg.global_attn_every_n_layers, cfg.local_attention, cfg.global_rope_theta,
+                             cfg.local_rope_theta)
+
+    def forward(self, rows) -> list:
+        """rows: list of token-id sequences -> list of [L, hidden] final-normed hidden states."""
+        lens = [len(r) for r in rows]
+        cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        ids = i32(np.concatenate([np.asarray(r, np.int64) for r in rows]))
+        out = np.empty((int(cu[-1]), self.cfg.hidden_size), np.float32)
+        rc = lib().ho_bert_forward(C.byref(self.ccfg), self.layers, self.embed.ctypes.data_as(C.c_void_p),
+                                   self.emb_norm.ctypes.data_as(C.c_void_p),
+                                   self.final_norm.ctypes.data_as(C.c_void_p), ids.ctypes.data_as(C.c_void_p),
+                                   cu.ctypes.data_as(C.c_void_p), C.c_int(len(rows)), C.c_int(int(self.bf16)),
+                                   out.ctypes.data_as(C.c_void_p))
+        if rc != 0:
+            raise ValueError("oracle ModernBERT forward rejected its inputs (token outside the vocabulary?)")
+        return [out[cu[i]:cu[i + 1]] for i in range(len(rows))]
+
+
+def load_tiny_modernbert(root: Path):
+    """The reference's tiny_modernbert fixture (Laya layout) as fp32 `model.*` arrays."""
+    from safetensors.numpy import load_file
+
+    cfg = BertConfig.from_json(json.loads((root / "config.json").read_text()))
+    raw = load_file(str(root / "model.safetensors"))
+    weights = {}
+    for k, v in raw.items():
+        m = remap_bert_key(k)
+        if m is not None:
+            weights[m] = f32(v)
+    return cfg, weights

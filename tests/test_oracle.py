@@ -9,7 +9,11 @@ Each check is chosen so a plausible mistake in the oracle fails it:
   * invariants and closed forms from the reference's own unit tests: delta-rule split
     continuation and special cases (delta_cpu.rs:203-247), paged == dense attention for any
     page permutation and page size (kv_pages.rs:388-630), future-value poisoning, conv
-    tap order (conv_cpu.rs:92-140), calibration semantics (calibration.rs:315-430).
+    tap order (conv_cpu.rs:92-140), calibration semantics (calibration.rs:315-430);
+  * ModernBERT (no reference golden vectors exist): vectors from an independent
+    implementation of the public definition (tests/golden/make_modernbert_vectors.py) on the
+    reference's tiny_modernbert checkpoint and a seeded 4-layer model, plus planted
+    mistakes (window off by one, tanh GELU, swapped RoPE thetas, missing attention norm).
 """
 import math
 
@@ -339,3 +343,102 @@ def test_rng_streams():
     assert ints.min() >= 64 and ints.max() <= 2048
     assert O.bf16_bits(np.float32([1.0, -2.5, 3.14159274]))[0] == 0x3F80
     assert O.round_bf16(np.float32([1.00390625]))[0] == np.float32(1.0)  # tie rounds to even
+
+
+# ---------------------------------------------------------------------------
+# ModernBERT (Laya backend)
+# ---------------------------------------------------------------------------
+
+def synth4_bert_weights():
+    """The seeded 4-layer ModernBERT of tests/golden/modernbert/cases.json (`model.*` names)."""
+    H, L, I, V = 64, 4, 96, 1000
+    shapes = {"embeddings.tok_embeddings.weight": (V, H), "embeddings.norm.weight": (H,), "final_norm.weight": (H,)}
+    for l in range(L):
+        p = f"layers.{l}."
+        shapes.update({p + "attn_norm.weight": (H,), p + "attn.Wqkv.weight": (3 * H, H), p + "attn.Wo.weight": (H, H),
+                       p + "mlp_norm.weight": (H,), p + "mlp.Wi.weight": (2 * I, H), p + "mlp.Wo.weight": (H, I)})
+    w = {}
+    for idx, name in enumerate(sorted(shapes)):
+        if name.endswith("norm.weight"):
+            mean, std = 1.0, 0.05
+        else:
+            mean, std = 0.0, {"mlp.Wi.weight": 0.5, "mlp.Wo.weight": 0.2}.get(name.split(".", 2)[-1], 0.05)
+        w["model." + name] = O.normal(20261201, 700 + idx, shapes[name], mean, std)
+    cfg = O.BertConfig(hidden_size=H, num_hidden_layers=L, num_attention_heads=4, intermediate_size=I, vocab_size=V,
+                       global_attn_every_n_layers=3, local_attention=16, global_rope_theta=160000.0,
+                       local_rope_theta=10000.0)
+    return cfg, w
+
+
+BERT_TOL = 2e-5  # fp32 oracle vs the golden vectors, absolute on unit-scale LayerNorm outputs
+
+
+@pytest.fixture(scope="module")
+def bert_vectors(golden_dir):
+    from safetensors.numpy import load_file
+
+    return load_file(str(golden_dir / "modernbert" / "vectors.safetensors"))
+
+
+def test_modernbert_oracle_matches_public_definition(golden_dir, bert_vectors):
+    """The oracle's ModernBERT forward against golden vectors from an independent
+    implementation of the public definition (tests/golden/make_modernbert_vectors.py): the
+    reference's tiny_modernbert checkpoint, and a seeded 4-layer model with global and
+    local (window 16) layers and distinct RoPE thetas; fp32, 2e-5 absolute on unit-scale
+    LayerNorm outputs."""
+    cfg, w = O.load_tiny_modernbert(golden_dir / "tiny_modernbert")
+    rows = [bert_vectors[f"tiny.ids{i}"].tolist() for i in range(2)]
+    for got, exp in zip(O.BertModel(cfg, w).forward(rows), (bert_vectors["tiny.hidden0"], bert_vectors["tiny.hidden1"])):
+        assert float(np.abs(got - exp).max()) < BERT_TOL
+    cfg, w = synth4_bert_weights()
+    rows = [bert_vectors[f"synth4.ids{i}"].tolist() for i in range(2)]
+    outs = O.BertModel(cfg, w).forward(rows)
+    for got, exp in zip(outs, (bert_vectors["synth4.hidden0"], bert_vectors["synth4.hidden1"])):
+        assert float(np.abs(got - exp).max()) < BERT_TOL
+
+
+@pytest.mark.parametrize("mistake", ["window_off_by_one", "tanh_gelu", "swapped_thetas", "no_attn_norm"])
+def test_modernbert_vectors_catch_planted_mistakes(bert_vectors, mistake):
+    """Each plausible mistake moves the seeded 4-layer model's output at least 10x past the
+    parity tolerance, so the golden vectors pin these details."""
+    import dataclasses
+
+    cfg, w = synth4_bert_weights()
+    rows = [bert_vectors[f"synth4.ids{i}"].tolist() for i in range(2)]
+    if mistake == "window_off_by_one":
+        cfg = dataclasses.replace(cfg, local_attention=14)
+    elif mistake == "swapped_thetas":
+        cfg = dataclasses.replace(cfg, global_rope_theta=10000.0, local_rope_theta=160000.0)
+    elif mistake == "no_attn_norm":
+        w = {k: v for k, v in w.items() if k != "model.layers.0.attn_norm.weight"}
+    m = O.BertModel(cfg, w)
+    if mistake == "tanh_gelu":  # the tanh approximation in place of the exact erf form
+        outs = _bert_forward_numpy(cfg, w, rows, lambda x: 0.5 * x * (1 + np.tanh(0.7978845608 * (x + 0.044715 * x ** 3))))
+    else:
+        outs = m.forward(rows)
+    err = max(float(np.abs(g - bert_vectors[f"synth4.hidden{i}"]).max()) for i, g in enumerate(outs))
+    assert err > 10 * BERT_TOL, (mistake, err)
+
+
+def _bert_forward_numpy(cfg, w, rows, act):
+    """A numpy restatement with a pluggable activation (used only to plant a mistake)."""
+    H, nh, d, I = cfg.hidden_size, cfg.num_attention_heads, cfg.head_dim, cfg.intermediate_size
+    outs = []
+    for r in rows:
+        T = len(r)
+        pos = np.arange(T, dtype=np.int32)
+        h = O.layer_norm(w["model.embeddings.tok_embeddings.weight"][r], w["model.embeddings.norm.weight"])
+        for l in range(cfg.num_hidden_layers):
+            glob = l % cfg.global_attn_every_n_layers == 0
+            p = f"model.layers.{l}."
+            x = O.layer_norm(h, w[p + "attn_norm.weight"]) if p + "attn_norm.weight" in w else h
+            qkv = O.linear(x, w[p + "attn.Wqkv.weight"]).reshape(T, 3, nh, d)
+            q, k, v = (np.ascontiguousarray(qkv[:, i]) for i in range(3))
+            c, s = O.rope_cos_sin(d, cfg.global_rope_theta if glob else cfg.local_rope_theta, pos)
+            q, k = O.apply_rope(q, d, c, s), O.apply_rope(k, d, c, s)
+            a = O.bidir_attention(q, k, v, [0, T], -1 if glob else cfg.local_attention // 2)
+            h = h + O.linear(a.reshape(T, H), w[p + "attn.Wo.weight"])
+            gi = O.linear(O.layer_norm(h, w[p + "mlp_norm.weight"]), w[p + "mlp.Wi.weight"])
+            h = h + O.linear((act(gi[:, :I]) * gi[:, I:]).astype(np.float32), w[p + "mlp.Wo.weight"])
+        outs.append(O.layer_norm(h, w["model.final_norm.weight"]))
+    return outs
