@@ -54,6 +54,19 @@ class KevLayerWeights(C.Structure):
     _fields_ = [(n, vp) for n in LAYER_FIELDS]
 
 
+class BertConfig(C.Structure):
+    _fields_ = [("hidden", I), ("n_layers", I), ("n_heads", I), ("intermediate", I), ("vocab", I), ("eps", F),
+                ("global_every", I), ("local_window", I), ("global_theta", D), ("local_theta", D),
+                ("max_context", I), ("n_out", I)]
+
+
+BERT_LAYER_FIELDS = ["attn_norm", "wqkv", "wo", "mlp_norm", "wi", "wo2"]
+
+
+class BertLayerWeights(C.Structure):
+    _fields_ = [(n, vp) for n in BERT_LAYER_FIELDS]
+
+
 # name -> (restype, argtypes); every function declared in include/huncho_rocm.h
 SIGNATURES = {
     "hk_device_count": (I, [C.POINTER(I)]),
@@ -89,6 +102,13 @@ SIGNATURES = {
     "hk_kev_model_destroy": (I, [vp]),
     "hk_kev_workspace_size": (I, [vp, I, I, C.POINTER(SZ)]),
     "hk_kev_forward": (I, [vp, vp, vp, i32p, I, vp, I, I, vp, SZ, vp, vp]),
+    "hk_layer_norm": (I, [vp, I, vp, L, vp, F, I, I, vp, L]),
+    "hk_bidir_attention": (I, [vp, I, vp, L, vp, L, vp, L, vp, I, I, I, I, I, I, F, vp, L]),
+    "hk_bert_model_create": (I, [vp, I, C.POINTER(BertConfig), C.POINTER(BertLayerWeights), vp, vp, vp, vp, vp,
+                                 C.POINTER(vp)]),
+    "hk_bert_model_destroy": (I, [vp]),
+    "hk_bert_workspace_size": (I, [vp, I, C.POINTER(SZ)]),
+    "hk_bert_forward": (I, [vp, vp, vp, i32p, I, vp, SZ, vp, vp]),
     "hk_calibrate": (I, [f32p, I, F, f32p]),
     "hk_synth_normal": (I, [U64, U64, vp, SZ, F, F]),
     "hk_synth_normal_bf16": (I, [U64, U64, vp, SZ, F, F]),

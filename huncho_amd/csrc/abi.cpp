@@ -556,3 +556,47 @@ extern "C" int hk_gdn_fused(hk_ctx* ctx, int dtype, const void* mixed, long mixe
     int rc = hk_launch_gdn_v2(dtype, 1, &a, &fa, n_seqs, ctx->stream);
     return rc ? hk_fail(ctx, rc, "fused Gated DeltaNet launch failed") : HK_OK;
 }
+
+// ---------------------------------------------------------------------------
+// ModernBERT ops
+// ---------------------------------------------------------------------------
+
+extern "C" int hk_layer_norm(hk_ctx* ctx, int dtype, const void* x, long x_tok, const float* w, float eps, int rows,
+                             int width, void* y, long y_tok) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = check_dtype(ctx, dtype)) return rc;
+    REQUIRE(x && w && y, "null pointer argument");
+    REQUIRE(rows >= 0 && width > 0 && width <= 2048, "width %d outside 1..2048", width);
+    REQUIRE(x_tok >= width && y_tok >= width, "row strides too small");
+    REQUIRE(eps > 0.0f, "eps must be positive");
+    if (rows == 0) return HK_OK;
+    hipSetDevice(ctx->device);
+    hk::LayerNormArgs a{x, x_tok, w, eps, rows, width, y, y_tok};
+    int rc = hk_launch_layer_norm(dtype, &a, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "layer_norm launch failed") : HK_OK;
+}
+
+extern "C" int hk_bidir_attention(hk_ctx* ctx, int dtype, const void* q, long q_tok, const void* k, long k_tok,
+                                  const void* v, long v_tok, const int32_t* cu, int n_seqs, int n_tokens, int max_len,
+                                  int heads, int head_dim, int half_window, float scale, void* o, long o_tok) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = check_dtype(ctx, dtype)) return rc;
+    if (head_dim != 64) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "head_dim %d: only 64 is implemented", head_dim);
+    REQUIRE(q && k && v && cu && o, "null pointer argument");
+    REQUIRE(heads > 0 && n_seqs > 0 && n_seqs <= 65535 && n_tokens >= 0 && max_len >= 0, "bad batch geometry");
+    REQUIRE(q_tok >= (long)heads * 64 && k_tok >= (long)heads * 64 && v_tok >= (long)heads * 64 &&
+                o_tok >= (long)heads * 64,
+            "token strides too small");
+    REQUIRE(scale > 0 && isfinite(scale), "scale must be positive and finite");
+    if (dtype != HK_F32) {  // 16-byte row loads, 8-byte output stores
+        REQUIRE(q_tok % 8 == 0 && k_tok % 8 == 0 && v_tok % 8 == 0 && o_tok % 4 == 0 &&
+                    (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15) == 0 && ((uintptr_t)o & 7) == 0,
+                "16-bit q/k/v rows must be 16-byte aligned and o rows 8-byte aligned");
+    }
+    if (max_len == 0 || n_tokens == 0) return HK_OK;
+    hipSetDevice(ctx->device);
+    hk::BertAttnArgs a{q, q_tok, k, k_tok, v, v_tok, o, o_tok, cu, n_seqs, n_tokens, heads, half_window,
+                       scale * 1.4426950408889634f, ctx->fault_dev};
+    int rc = hk_launch_bidir_attention(dtype, &a, n_seqs, max_len, ctx->stream);
+    return rc ? hk_fail(ctx, rc, "bidirectional attention launch failed") : HK_OK;
+}

@@ -278,7 +278,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
         const bool grow = (m_tile - m_use) * c > RESCALE_LOG2;
         if (__any(grow)) {
             const float m_new = grow ? m_tile : m_use;
-            const float alpha = fast_exp2((m_use - m_new) * c);
+            // lanes that keep their max keep their sums (alpha 1; also avoids -inf - -inf)
+            const float alpha = grow ? fast_exp2((m_use - m_new) * c) : 1.0f;
             m_use = m_new;
             l_run *= alpha;
 #pragma unroll

@@ -1,0 +1,258 @@
+// bert_model.cpp - the ModernBERT (Laya) encoder forward on one MI355X.
+//
+// The reference executes candle-transformers' ModernBert for the Laya backend
+// (crates/huncho-backend/src/candle.rs:65-117 load, 319-416 forward). For an unpadded varlen
+// batch of independent rows (the reference pads and masks; padding is invisible, so the
+// unpadded rows give the same hidden states):
+//   h = LayerNorm(embed(ids))
+//   layer i (global iff i % global_every == 0, otherwise keys within local_window / 2):
+//     x = attn_norm ? LayerNorm(h) : h
+//     [q | k | v] = x Wqkv^T ; q, k = RoPE(q, k) (theta global or local) ; a = attention
+//     h += a Wo^T ; [x1 | x2] = LayerNorm(h) Wi^T ; h += (gelu(x1) * x2) Wo2^T
+//   out = LayerNorm(h)
+// followed by a mean-pooled linear head over each row. LayerNorms have no bias; residual
+// adds are folded into the GEMM epilogue (beta = 1 onto the residual stream).
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+#include "abi_internal.hpp"
+
+namespace {
+
+struct BertLayer {
+    float* attn_norm = nullptr;  // null: identity
+    float* mlp_norm = nullptr;
+    void *wqkv = nullptr, *wo = nullptr, *wi = nullptr, *wo2 = nullptr;
+};
+
+}  // namespace
+
+struct hk_bert_model {
+    hk_ctx* ctx = nullptr;
+    int dtype = HK_BF16;
+    size_t esz = 2;
+    hk_bert_config cfg{};
+    std::vector<BertLayer> layers;
+    std::vector<void*> owned;
+    void* embed = nullptr;
+    float *emb_norm = nullptr, *final_norm = nullptr;
+    void* head_w = nullptr;
+    float* head_b = nullptr;
+    float *cos_g = nullptr, *sin_g = nullptr, *cos_l = nullptr, *sin_l = nullptr;
+};
+
+static int b_alloc(hk_bert_model* m, size_t bytes, void** out) {
+    if (hipMalloc(out, bytes) != hipSuccess) return hk_fail(m->ctx, HK_ERR_NOMEM, "model allocation of %zu bytes failed", bytes);
+    m->owned.push_back(*out);
+    return HK_OK;
+}
+
+static int b_copy(hk_bert_model* m, const void* src, size_t bytes, void** out) {
+    if (!src) return hk_fail(m->ctx, HK_ERR_INVALID, "missing weight");
+    if (int rc = b_alloc(m, bytes, out)) return rc;
+    return hk_check_hip(m->ctx, hipMemcpy(*out, src, bytes, hipMemcpyDeviceToDevice), "weight copy");
+}
+
+// fp32 device copy of a [count] weight held in the model dtype
+static int b_f32(hk_bert_model* m, const void* src, size_t count, float** out) {
+    if (!src) return hk_fail(m->ctx, HK_ERR_INVALID, "missing norm weight");
+    std::vector<float> v(count);
+    if (m->dtype == HK_F32) {
+        if (int rc = hk_check_hip(m->ctx, hipMemcpy(v.data(), src, count * 4, hipMemcpyDeviceToHost), "weight read"))
+            return rc;
+    } else {
+        std::vector<uint16_t> t(count);
+        if (int rc = hk_check_hip(m->ctx, hipMemcpy(t.data(), src, count * 2, hipMemcpyDeviceToHost), "weight read"))
+            return rc;
+        for (size_t i = 0; i < count; ++i) {
+            if (m->dtype == HK_F16) {
+                v[i] = hk_host_f16_to_f32(t[i]);
+            } else {
+                const uint32_t u = (uint32_t)t[i] << 16;
+                memcpy(&v[i], &u, 4);
+            }
+        }
+    }
+    if (int rc = b_alloc(m, count * 4, (void**)out)) return rc;
+    return hk_check_hip(m->ctx, hipMemcpy(*out, v.data(), count * 4, hipMemcpyHostToDevice), "weight upload");
+}
+
+static int b_table(hk_bert_model* m, double theta, float** cs, float** sn) {
+    const int max_pos = m->cfg.max_context;
+    std::vector<float> c((size_t)max_pos * 32), s((size_t)max_pos * 32);
+    hk_rope_fill_table(64, theta, max_pos, m->dtype, c.data(), s.data());
+    if (int rc = b_alloc(m, c.size() * 4, (void**)cs)) return rc;
+    if (int rc = b_alloc(m, s.size() * 4, (void**)sn)) return rc;
+    if (int rc = hk_check_hip(m->ctx, hipMemcpy(*cs, c.data(), c.size() * 4, hipMemcpyHostToDevice), "rope table"))
+        return rc;
+    return hk_check_hip(m->ctx, hipMemcpy(*sn, s.data(), s.size() * 4, hipMemcpyHostToDevice), "rope table");
+}
+
+extern "C" int hk_bert_model_destroy(hk_bert_model* m) {
+    if (!m) return HK_ERR_INVALID;
+    hipSetDevice(m->ctx->device);
+    hipStreamSynchronize(m->ctx->stream);
+    for (void* p : m->owned) hipFree(p);
+    delete m;
+    return HK_OK;
+}
+
+extern "C" int hk_bert_model_create(hk_ctx* ctx, int dtype, const hk_bert_config* cfg,
+                                    const hk_bert_layer_weights* lw, const void* embed, const void* emb_norm,
+                                    const void* final_norm, const void* head_w, const float* head_b,
+                                    hk_bert_model** out) {
+    if (!ctx || !cfg || !lw || !embed || !emb_norm || !final_norm || !out) return HK_ERR_INVALID;
+    *out = nullptr;
+    if (dtype != HK_BF16 && dtype != HK_F16 && dtype != HK_F32) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d", dtype);
+    const hk_bert_config& c = *cfg;
+    if (c.n_heads <= 0 || c.hidden != c.n_heads * 64)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "head dim must be 64 (hidden %d, heads %d)", c.hidden, c.n_heads);
+    if (c.hidden % 8 || c.hidden > 2048 || c.intermediate <= 0 || c.intermediate % 8 || c.n_layers <= 0 ||
+        c.vocab <= 0 || c.global_every <= 0 || c.local_window < 0 || c.max_context <= 0 || c.n_out < 0 ||
+        !(c.eps > 0.0f))
+        return hk_fail(ctx, HK_ERR_INVALID, "invalid ModernBERT configuration");
+    if (c.n_out > 0 && !head_w) return hk_fail(ctx, HK_ERR_INVALID, "missing head weight");
+    hipSetDevice(ctx->device);
+    hk_bert_model* m = new hk_bert_model();
+    m->ctx = ctx;
+    m->dtype = dtype;
+    m->esz = dtype == HK_F32 ? 4 : 2;
+    m->cfg = c;
+    const int H = c.hidden, I = c.intermediate;
+    const size_t e = m->esz;
+    int rc = HK_OK;
+    auto fail = [&](int code) {
+        hk_bert_model_destroy(m);
+        return code;
+    };
+    for (int l = 0; l < c.n_layers; ++l) {
+        const hk_bert_layer_weights& w = lw[l];
+        BertLayer L;
+        if (w.attn_norm && (rc = b_f32(m, w.attn_norm, H, &L.attn_norm))) return fail(rc);
+        if ((rc = b_f32(m, w.mlp_norm, H, &L.mlp_norm))) return fail(rc);
+        if ((rc = b_copy(m, w.wqkv, (size_t)3 * H * H * e, &L.wqkv))) return fail(rc);
+        if ((rc = b_copy(m, w.wo, (size_t)H * H * e, &L.wo))) return fail(rc);
+        if ((rc = b_copy(m, w.wi, (size_t)2 * I * H * e, &L.wi))) return fail(rc);
+        if ((rc = b_copy(m, w.wo2, (size_t)H * I * e, &L.wo2))) return fail(rc);
+        m->layers.push_back(L);
+    }
+    if ((rc = b_copy(m, embed, (size_t)c.vocab * H * e, &m->embed))) return fail(rc);
+    if ((rc = b_f32(m, emb_norm, H, &m->emb_norm))) return fail(rc);
+    if ((rc = b_f32(m, final_norm, H, &m->final_norm))) return fail(rc);
+    if (c.n_out > 0) {
+        if ((rc = b_copy(m, head_w, (size_t)c.n_out * H * e, &m->head_w))) return fail(rc);
+        if (head_b) {
+            if ((rc = b_alloc(m, c.n_out * 4, (void**)&m->head_b))) return fail(rc);
+            if ((rc = hk_check_hip(ctx, hipMemcpy(m->head_b, head_b, c.n_out * 4, hipMemcpyDeviceToDevice), "head bias")))
+                return fail(rc);
+        }
+    }
+    if ((rc = b_table(m, c.global_theta, &m->cos_g, &m->sin_g)) || (rc = b_table(m, c.local_theta, &m->cos_l, &m->sin_l)))
+        return fail(rc);
+    *out = m;
+    return HK_OK;
+}
+
+namespace {
+
+struct BertBuffers {
+    void *h, *x, *qkv, *att, *gi, *act;
+};
+
+size_t bert_carve(const hk_bert_model* m, char* base, int n, BertBuffers* b) {
+    const hk_bert_config& c = m->cfg;
+    const size_t e = m->esz;
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> void* {
+        void* p = base ? base + off : nullptr;
+        off += (bytes + 255) & ~(size_t)255;
+        return p;
+    };
+    b->h = take((size_t)n * c.hidden * e);
+    b->x = take((size_t)n * c.hidden * e);
+    b->qkv = take((size_t)n * 3 * c.hidden * e);
+    b->att = take((size_t)n * c.hidden * e);
+    b->gi = take((size_t)n * 2 * c.intermediate * e);
+    b->act = take((size_t)n * c.intermediate * e);
+    return off;
+}
+
+}  // namespace
+
+extern "C" int hk_bert_workspace_size(hk_bert_model* m, int n_tokens, size_t* bytes_out) {
+    if (!m || !bytes_out || n_tokens < 0) return HK_ERR_INVALID;
+    BertBuffers b;
+    *bytes_out = bert_carve(m, nullptr, n_tokens, &b);
+    return HK_OK;
+}
+
+#define BRUN(expr)                 \
+    do {                           \
+        int rc__ = (expr);         \
+        if (rc__) return rc__;     \
+    } while (0)
+
+extern "C" int hk_bert_forward(hk_bert_model* m, const int32_t* ids, const int32_t* cu_dev, const int32_t* cu_host,
+                               int n_seqs, void* workspace, size_t workspace_bytes, float* logits, void* hidden_out) {
+    if (!m) return HK_ERR_INVALID;
+    hk_ctx* ctx = m->ctx;
+    const hk_bert_config& c = m->cfg;
+    if (!ids || !cu_dev || !cu_host || !workspace || n_seqs <= 0 || n_seqs > 65535)
+        return hk_fail(ctx, HK_ERR_INVALID, "invalid forward arguments");
+    if (c.n_out > 0 && !logits) return hk_fail(ctx, HK_ERR_INVALID, "logits output required");
+    if (cu_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "cu_seqlens[0] must be 0");
+    int max_len = 0;
+    for (int s = 0; s < n_seqs; ++s) {
+        const int len = cu_host[s + 1] - cu_host[s];
+        if (len <= 0) return hk_fail(ctx, HK_ERR_INVALID, "sequence %d is empty", s);
+        if (len > c.max_context) return hk_fail(ctx, HK_ERR_INVALID, "sequence length %d exceeds max_context %d", len, c.max_context);
+        if (len > max_len) max_len = len;
+    }
+    const int n = cu_host[n_seqs];
+    BertBuffers b;
+    if (bert_carve(m, (char*)workspace, n, &b) > workspace_bytes)
+        return hk_fail(ctx, HK_ERR_INVALID, "workspace too small");
+    hipSetDevice(ctx->device);
+    const int dt = m->dtype;
+    const size_t e = m->esz;
+    const int H = c.hidden, I = c.intermediate, nh = c.n_heads;
+    const float scale_log2 = (float)(1.0 / sqrt(64.0)) * 1.4426950408889634f;
+
+    BRUN(hk_launch_embed(dt, ids, n, m->embed, c.vocab, H, b.x, ctx->fault_dev, ctx->stream)
+             ? hk_fail(ctx, HK_ERR_DEVICE, "embed launch")
+             : 0);
+    BRUN(hk_layer_norm(ctx, dt, b.x, H, m->emb_norm, c.eps, n, H, b.h, H));
+    for (int l = 0; l < c.n_layers; ++l) {
+        const BertLayer& L = m->layers[l];
+        const bool global = l % c.global_every == 0;
+        const void* src = b.h;
+        if (L.attn_norm) {
+            BRUN(hk_layer_norm(ctx, dt, b.h, H, L.attn_norm, c.eps, n, H, b.x, H));
+            src = b.x;
+        }
+        BRUN(hk_gemm_xwt(ctx, dt, n, 3 * H, H, src, H, L.wqkv, H, b.qkv, 3 * H, nullptr, 0, 1.0f, 0.0f));
+        hk::RopeQkArgs ra{b.qkv, 3L * H, global ? m->cos_g : m->cos_l, global ? m->sin_g : m->sin_l, c.max_context, nh,
+                          cu_dev, n_seqs, n, ctx->fault_dev};
+        BRUN(hk_launch_rope_qk(dt, &ra, n_seqs, max_len, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "rope launch") : 0);
+        char* q = (char*)b.qkv;
+        hk::BertAttnArgs aa{q, 3L * H, q + (size_t)H * e, 3L * H, q + (size_t)2 * H * e, 3L * H, b.att, (long)H,
+                            cu_dev, n_seqs, n, nh, global ? -1 : c.local_window / 2, scale_log2, ctx->fault_dev};
+        BRUN(hk_launch_bidir_attention(dt, &aa, n_seqs, max_len, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "attention launch")
+                                                                               : 0);
+        BRUN(hk_gemm_xwt(ctx, dt, n, H, H, b.att, H, L.wo, H, b.h, H, b.h, H, 1.0f, 1.0f));
+        BRUN(hk_layer_norm(ctx, dt, b.h, H, L.mlp_norm, c.eps, n, H, b.x, H));
+        BRUN(hk_gemm_xwt(ctx, dt, n, 2 * I, H, b.x, H, L.wi, H, b.gi, 2 * I, nullptr, 0, 1.0f, 0.0f));
+        hk::GegluArgs ga{b.gi, 2L * I, n, I, b.act, (long)I};
+        BRUN(hk_launch_geglu(dt, &ga, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "geglu launch") : 0);
+        BRUN(hk_gemm_xwt(ctx, dt, n, H, I, b.act, I, L.wo2, I, b.h, H, b.h, H, 1.0f, 1.0f));
+    }
+    void* fin = hidden_out ? hidden_out : b.x;
+    BRUN(hk_layer_norm(ctx, dt, b.h, H, m->final_norm, c.eps, n, H, fin, H));
+    if (c.n_out > 0) {
+        hk::MeanPoolArgs pa{fin, (long)H, cu_dev, n_seqs, n, H, m->head_w, m->head_b, c.n_out, logits, ctx->fault_dev};
+        BRUN(hk_launch_mean_pool_head(dt, &pa, n_seqs, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "head launch") : 0);
+    }
+    return HK_OK;
+}

@@ -144,6 +144,64 @@ struct SwigluArgs {
     void* y;
 };
 
+// ModernBERT encoder (bert.hip)
+struct BertAttnArgs {
+    const void* q;  // [tokens][heads][64] at token stride q_tok (elements)
+    long q_tok;
+    const void* k;
+    long k_tok;
+    const void* v;
+    long v_tok;
+    void* o;
+    long o_tok;
+    const int* cu;
+    int n_seqs, n_tokens, heads;
+    int half_window;   // keys with |i - j| <= half_window; < 0: the whole sequence
+    float scale_log2;  // softmax scale * log2(e)
+    int* fault;
+};
+
+struct LayerNormArgs {
+    const void* x;
+    long x_tok;
+    const float* w;
+    float eps;
+    int rows, width;
+    void* y;
+    long y_tok;
+};
+
+struct GegluArgs {
+    const void* x;  // x1 at [t * x_tok + i], x2 at [t * x_tok + width + i]
+    long x_tok;
+    int rows, width;
+    void* y;
+    long y_tok;
+};
+
+struct RopeQkArgs {
+    void* x;  // rows [q (heads x 64) | k (heads x 64) | ...] at token stride x_tok
+    long x_tok;
+    const float* cos;  // [max_pos][32]
+    const float* sin;
+    int max_pos, heads;
+    const int* cu;
+    int n_seqs, n_tokens;
+    int* fault;
+};
+
+struct MeanPoolArgs {
+    const void* x;
+    long x_tok;
+    const int* cu;
+    int n_seqs, n_tokens, width;
+    const void* head_w;  // [n_out][width], model dtype
+    const float* head_b;  // [n_out] or null
+    int n_out;
+    float* logits;  // [n_seqs][n_out]
+    int* fault;
+};
+
 }  // namespace hk
 
 extern "C" {
@@ -163,4 +221,9 @@ int hk_launch_final_norm_head(int dtype, const void* x, long x_tok, const int* c
                               float eps, int width, const void* head_w, const float* head_b, int n_out, float* logits,
                               void* h_out, hipStream_t st);
 int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st);
+int hk_launch_bidir_attention(int dtype, const hk::BertAttnArgs* a, int n_seqs, int max_len, hipStream_t stream);
+int hk_launch_layer_norm(int dtype, const hk::LayerNormArgs* a, hipStream_t stream);
+int hk_launch_geglu(int dtype, const hk::GegluArgs* a, hipStream_t stream);
+int hk_launch_rope_qk(int dtype, const hk::RopeQkArgs* a, int n_seqs, int max_len, hipStream_t stream);
+int hk_launch_mean_pool_head(int dtype, const hk::MeanPoolArgs* a, int n_seqs, hipStream_t stream);
 }

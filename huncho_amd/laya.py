@@ -1,0 +1,194 @@
+"""ModernBERT (Laya) encoder on libhuncho_rocm (host side, Python).
+
+Mirrors the Laya backend's scoring surface (crates/huncho-backend/src/candle.rs): checkpoint
+keys under `model.*` (the loader remaps the Laya `encoder.*` prefix, 205-231), the config
+normalisation of 157-203 (rope_parameters thetas, local_attention, global_attn_every_n_layers,
+layer_norm_eps), batches of 1..=64 non-empty rows validated before any work (319-335), and
+independent rows: the reference pads and masks, this path runs the rows unpadded (varlen), which
+gives the same per-row hidden states. The readout is a mean-pooled linear head over each row.
+All numerics run in the C ABI.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import abi
+from .abi import HK_BF16, HK_F16, HK_F32, BertConfig, BertLayerWeights
+
+MAX_ROWS = 64
+
+
+@dataclass
+class LayaShape:
+    """A ModernBERT-base-shaped encoder (hidden 768, 22 layers, 12 heads x 64)."""
+    hidden: int = 768
+    n_layers: int = 22
+    n_heads: int = 12
+    intermediate: int = 1152
+    vocab: int = 50368
+    eps: float = 1e-5
+    global_every: int = 3
+    local_window: int = 128
+    global_theta: float = 160000.0
+    local_theta: float = 10000.0
+    max_context: int = 8192
+    n_out: int = 4
+    attn_norm_layer0: bool = True  # the Laya checkpoint carries layers.0.attn_norm
+
+    @staticmethod
+    def from_config_json(v: dict, n_out: int = 0, max_context: int = 8192) -> "LayaShape":
+        """candle.rs:157-203 (defaults and the rope_parameters fallbacks included)."""
+        rp = v.get("rope_parameters") or {}
+        g = v.get("global_rope_theta", (rp.get("full_attention") or {}).get("rope_theta", 10000.0))
+        l = v.get("local_rope_theta", (rp.get("sliding_attention") or {}).get("rope_theta", 10000.0))
+        return LayaShape(hidden=v.get("hidden_size", 0), n_layers=v.get("num_hidden_layers", 12),
+                         n_heads=v.get("num_attention_heads", 12), intermediate=v.get("intermediate_size", 3072),
+                         vocab=v.get("vocab_size", 0), eps=float(v.get("layer_norm_eps", 1e-5)),
+                         global_every=v.get("global_attn_every_n_layers", 3),
+                         local_window=v.get("local_attention", 128), global_theta=float(g), local_theta=float(l),
+                         max_context=max_context, n_out=n_out)
+
+    def weight_shapes(self) -> dict:
+        H, I = self.hidden, self.intermediate
+        shapes = {"model.embeddings.tok_embeddings.weight": (self.vocab, H), "model.embeddings.norm.weight": (H,),
+                  "model.final_norm.weight": (H,)}
+        for i in range(self.n_layers):
+            p = f"model.layers.{i}."
+            if i > 0 or self.attn_norm_layer0:
+                shapes[p + "attn_norm.weight"] = (H,)
+            shapes.update({p + "attn.Wqkv.weight": (3 * H, H), p + "attn.Wo.weight": (H, H),
+                           p + "mlp_norm.weight": (H,), p + "mlp.Wi.weight": (2 * I, H),
+                           p + "mlp.Wo.weight": (H, I)})
+        if self.n_out:
+            shapes["head.weight"] = (self.n_out, H)
+        return shapes
+
+
+def synthetic_weights(shape: LayaShape, seed: int, std: float = 0.02) -> dict:
+    """bf16 bit patterns (uint16): N(1, std) LayerNorm weights, N(0, std) the rest; one seeded
+    stream per tensor in sorted-name order (hk_synth_normal_bf16, stream 3000 + index)."""
+    shapes = shape.weight_shapes()
+    out = {}
+    for idx, name in enumerate(sorted(shapes)):
+        n = int(np.prod(shapes[name]))
+        mean = 1.0 if name.endswith("norm.weight") else 0.0
+        out[name] = abi.synth_normal_bf16(seed, 3000 + idx, n, mean, std).reshape(shapes[name])
+    return out
+
+
+def _to_device(a: np.ndarray, dtype: torch.dtype, device) -> torch.Tensor:
+    if a.dtype == np.uint16:  # bf16 bits
+        t = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+        if dtype != torch.bfloat16:
+            t = t.to(dtype)
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(a, np.float32))
+        if dtype != torch.float32:
+            t = t.to(dtype)
+    return t.to(device).contiguous()
+
+
+_FIELD = {"attn_norm": "attn_norm.weight", "wqkv": "attn.Wqkv.weight", "wo": "attn.Wo.weight",
+          "mlp_norm": "mlp_norm.weight", "wi": "mlp.Wi.weight", "wo2": "mlp.Wo.weight"}
+
+
+class LayaModel:
+    """hk_bert_model plus its workspace, for varlen batches of independent rows."""
+
+    def __init__(self, ctx: abi.Context, shape: LayaShape, weights: dict, dtype: torch.dtype = torch.bfloat16,
+                 device=0):
+        self.ctx, self.shape, self.dtype = ctx, shape, dtype
+        self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        self.hk_dtype = {torch.bfloat16: HK_BF16, torch.float16: HK_F16, torch.float32: HK_F32}[dtype]
+        staged = {k: _to_device(v, dtype, self.device) for k, v in weights.items()}
+        cfg = BertConfig(shape.hidden, shape.n_layers, shape.n_heads, shape.intermediate, shape.vocab, shape.eps,
+                         shape.global_every, shape.local_window, shape.global_theta, shape.local_theta,
+                         shape.max_context, shape.n_out)
+        layers = (BertLayerWeights * shape.n_layers)()
+        for i in range(shape.n_layers):
+            for f, suffix in _FIELD.items():
+                t = staged.get(f"model.layers.{i}.{suffix}")
+                if t is not None:
+                    setattr(layers[i], f, t.data_ptr())
+        head = staged.get("head.weight")
+        hb = weights.get("head.bias")
+        head_b = torch.from_numpy(np.asarray(hb, np.float32)).to(self.device) if hb is not None else None
+        h = C.c_void_p()
+        torch.cuda.synchronize(self.device)
+        ctx.check(abi.lib().hk_bert_model_create(
+            ctx.h, self.hk_dtype, C.byref(cfg), layers, staged["model.embeddings.tok_embeddings.weight"].data_ptr(),
+            staged["model.embeddings.norm.weight"].data_ptr(), staged["model.final_norm.weight"].data_ptr(),
+            head.data_ptr() if head is not None else None, head_b.data_ptr() if head_b is not None else None,
+            C.byref(h)))
+        self.h = h
+        self._keep_bias = head_b
+        del staged
+        self._ws = None
+
+    def close(self):
+        if self.h:
+            abi.lib().hk_bert_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _workspace(self, n_tokens: int) -> torch.Tensor:
+        sz = C.c_size_t()
+        self.ctx.check(abi.lib().hk_bert_workspace_size(self.h, n_tokens, C.byref(sz)))
+        if self._ws is None or self._ws.numel() < sz.value:
+            self._ws = torch.empty(sz.value, dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def validate(self, rows) -> None:
+        """candle.rs:319-335 and validate_input: 1..=64 non-empty rows, ids inside the vocabulary."""
+        if not 1 <= len(rows) <= MAX_ROWS:
+            raise ValueError(f"batch must contain 1..={MAX_ROWS} independent rows (got {len(rows)})")
+        for r in rows:
+            if len(r) == 0:
+                raise ValueError("rows must be non-empty")
+            if len(r) > self.shape.max_context:
+                raise ValueError(f"row of {len(r)} tokens exceeds max_context {self.shape.max_context}")
+            a = np.asarray(r)
+            if a.min() < 0 or a.max() >= self.shape.vocab:
+                raise ValueError("token id outside the vocabulary")
+
+    def prepare(self, lengths) -> dict:
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        n = int(cu[-1])
+        return {"cu_host": cu, "cu": torch.from_numpy(cu).to(self.device), "n_seqs": len(lengths), "n": n,
+                "ws": self._workspace(n),
+                "logits": torch.empty((len(lengths), max(self.shape.n_out, 1)), dtype=torch.float32,
+                                      device=self.device)}
+
+    def forward_ids(self, ids: torch.Tensor, batch: dict, hidden_out: torch.Tensor | None = None) -> None:
+        self.ctx.check(abi.lib().hk_bert_forward(
+            self.h, ids.data_ptr(), batch["cu"].data_ptr(), batch["cu_host"].ctypes.data_as(C.POINTER(C.c_int32)),
+            batch["n_seqs"], batch["ws"].data_ptr(), batch["ws"].numel(), batch["logits"].data_ptr(),
+            hidden_out.data_ptr() if hidden_out is not None else None))
+
+    def forward_batch(self, rows, want_hidden: bool = False):
+        """rows: token-id sequences -> (logits [rows, n_out] fp32 numpy, hidden list or None)."""
+        self.validate(rows)
+        batch = self.prepare([len(r) for r in rows])
+        ids = torch.from_numpy(np.concatenate([np.asarray(r, np.int32) for r in rows])).to(self.device)
+        hidden = torch.empty((batch["n"], self.shape.hidden), dtype=self.dtype, device=self.device) if want_hidden else None
+        self.forward_ids(ids, batch, hidden)
+        torch.cuda.synchronize(self.device)
+        faults = self.ctx.take_faults()
+        if faults:
+            raise RuntimeError(f"device faults 0x{faults:x} during the ModernBERT forward")
+        logits = batch["logits"].cpu().numpy()[:, : self.shape.n_out]
+        hs = None
+        if want_hidden:
+            h = hidden.float().cpu().numpy()
+            cu = batch["cu_host"]
+            hs = [h[cu[i]:cu[i + 1]] for i in range(len(rows))]
+        return logits, hs

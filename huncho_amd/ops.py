@@ -168,3 +168,29 @@ def swiglu(ctx: Context, gu, width):
     out = torch.empty((rows, width), dtype=gu.dtype, device=gu.device)
     ctx.check(abi.lib().hk_swiglu(ctx.h, _dt(gu), _p(gu), gu.stride(0), width, rows, width, _p(out)))
     return out
+
+
+def layer_norm(ctx: Context, x, w, eps, out=None):
+    """LayerNorm without bias over the last dim of x [rows, width]; w fp32 [width]."""
+    _dev(x, w, out)
+    rows, width = x.shape
+    out = torch.empty_like(x) if out is None else out
+    ctx.check(abi.lib().hk_layer_norm(ctx.h, _dt(x), _p(x), x.stride(0), _p(w), eps, rows, width, _p(out),
+                                      out.stride(0)))
+    return out
+
+
+def bidir_attention(ctx: Context, q, k, v, cu_seqlens, max_len, half_window=-1, scale=None, out=None):
+    """q, k, v [tokens, heads, 64] (token-strided views, unit head stride 64); keys with
+    |i - j| <= half_window (all keys of the sequence when < 0). Returns o [tokens, heads, 64]."""
+    _dev(q, k, v, cu_seqlens, out)
+    tokens, heads, d = q.shape
+    assert q.stride(1) == d and k.stride(1) == d and v.stride(1) == d and q.stride(2) == 1
+    if out is None:
+        out = torch.empty((tokens, heads, d), dtype=q.dtype, device=q.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    ctx.check(abi.lib().hk_bidir_attention(
+        ctx.h, _dt(q), _p(q), q.stride(0), _p(k), k.stride(0), _p(v), v.stride(0), _p(cu_seqlens),
+        cu_seqlens.numel() - 1, tokens, int(max_len), heads, d, int(half_window), float(scale), _p(out), out.stride(0)))
+    return out

@@ -235,6 +235,53 @@ int hk_kev_forward(hk_kev_model* m, const int32_t* ids_dev, const int32_t* cu_se
                    int num_pages, void* workspace_dev, size_t workspace_bytes, float* logits_dev,
                    void* hidden_last_dev);
 
+/* ---- ModernBERT encoder (the Laya backend: candle ModernBert, crates/huncho-backend/src/
+ * candle.rs:65-117 load, 319-416 forward; config normalisation 157-203) ----------------------
+ * LayerNorm without bias: y = (x - mean) / sqrt(var + eps) * w, w fp32 [width], width <= 2048. */
+int hk_layer_norm(hk_ctx* ctx, int dtype, const void* x_dev, long x_tok, const float* w_dev, float eps, int rows,
+                  int width, void* y_dev, long y_tok);
+/* Bidirectional softmax attention inside each sequence of an unpadded varlen batch, the
+ * sequence-local part of ModernBERT's attention: q, k, v [tokens][heads][64] at their token
+ * strides, key j visible to query i iff half_window < 0 or |i - j| <= half_window (local
+ * layers: local_attention / 2). o [tokens][heads][64]. max_len >= the longest sequence. */
+int hk_bidir_attention(hk_ctx* ctx, int dtype, const void* q_dev, long q_tok, const void* k_dev, long k_tok,
+                       const void* v_dev, long v_tok, const int32_t* cu_seqlens_dev, int n_seqs, int n_tokens,
+                       int max_len, int heads, int head_dim, int half_window, float scale, void* o_dev, long o_tok);
+
+typedef struct {
+    int hidden, n_layers, n_heads, intermediate, vocab;  /* head dim = hidden / n_heads = 64 */
+    float eps;             /* layer_norm_eps (1e-5) */
+    int global_every;      /* layer i is global iff i % global_every == 0 */
+    int local_window;      /* local_attention: local layers see |i - j| <= local_window / 2 */
+    double global_theta, local_theta;
+    int max_context;       /* longest sequence (RoPE table size) */
+    int n_out;             /* mean-pooled linear head outputs (0 = none) */
+} hk_bert_config;
+
+/* Per-layer weights in the model dtype, [out][in] (checkpoint names model.layers.{i}.*). */
+typedef struct {
+    const void* attn_norm;         /* attn_norm.weight [H], or NULL for an identity */
+    const void *wqkv, *wo;         /* attn.Wqkv.weight [3H][H], attn.Wo.weight [H][H] */
+    const void* mlp_norm;          /* mlp_norm.weight [H] */
+    const void *wi, *wo2;          /* mlp.Wi.weight [2I][H], mlp.Wo.weight [H][I] */
+} hk_bert_layer_weights;
+
+typedef struct hk_bert_model hk_bert_model;
+
+/* Copies the weights (the caller's buffers may be freed afterwards). head_w [n_out][H] in the
+ * model dtype, head_b [n_out] fp32 device or NULL. */
+int hk_bert_model_create(hk_ctx* ctx, int dtype, const hk_bert_config* cfg, const hk_bert_layer_weights* layers_host,
+                         const void* embed_dev, const void* emb_norm_dev, const void* final_norm_dev,
+                         const void* head_w_dev, const float* head_b_dev, hk_bert_model** out);
+int hk_bert_model_destroy(hk_bert_model* m);
+int hk_bert_workspace_size(hk_bert_model* m, int n_tokens, size_t* bytes_out);
+/* Encoder forward of an unpadded varlen batch: ids [n_tokens], cu_seqlens on device and
+ * host. Writes the mean-pooled head's logits [n_seqs][n_out] (fp32) and, if hidden_out_dev
+ * != NULL, the final-normed hidden states [n_tokens][hidden] in the model dtype. */
+int hk_bert_forward(hk_bert_model* m, const int32_t* ids_dev, const int32_t* cu_seqlens_dev,
+                    const int32_t* cu_seqlens_host, int n_seqs, void* workspace_dev, size_t workspace_bytes,
+                    float* logits_dev, void* hidden_out_dev);
+
 /* ---- calibration (crates/huncho-core/src/calibration.rs:42-60, 170-173) --------------------------
  * Host-side: fp32 exp((x - max) / T), fp64 ordered sum and divide, fp32 result. Returns
  * HK_ERR_INVALID for a non-finite logit or a non-positive / non-finite temperature. */
