@@ -1,14 +1,19 @@
-"""Kev-shaped hybrid prefill benchmark on one MI355X.
+"""Prefill / encoder benchmarks on one MI355X.
 
-Workload: the Kev/Qwen3.5 hybrid scoring forward (hidden 1024, 24 layers = 3 Gated DeltaNet :
-1 gated GQA attention, attention 16/8 heads x 128, GDN 16 heads x 128, SwiGLU 3584,
-vocab 151936, decision head over 8 choices) on a batch of 64 sequences x 512 seeded token
-ids, random-init weights N(0, 0.02) in the model dtype, KV pages of 16 tokens from a seeded
-permutation of the pool. One step = one full forward of the 32,768 tokens (every layer,
+Default workload (`--workload kev`): the Kev/Qwen3.5 hybrid scoring forward (hidden 1024,
+24 layers = 3 Gated DeltaNet : 1 gated GQA attention, attention 16/8 heads x 128, GDN 16 heads x
+128, SwiGLU 3584, vocab 151936, decision head over 8 choices) on a batch of 64 sequences x 512
+seeded token ids, random-init weights N(0, 0.02) in the model dtype, KV pages of 16 tokens from a
+seeded permutation of the pool. One step = one full forward of the 32,768 tokens (every layer,
 every token) plus the decision logits; inputs are resident in HBM before timing starts.
 
-Prints one JSON line: whole-job prefill tokens/s, the live-measured roofline of the attention
-kernel (MFMA-bound, bf16 dense peak 2.5 PFLOP/s) and of the delta-rule kernel (HBM-bound,
+`--workload laya`: the ModernBERT-base-shaped encoder (hidden 768, 22 layers, 12 heads x 64,
+global attention every third layer with RoPE theta 160000, the rest a +-64 sliding window with
+theta 10000, GeGLU 1152, mean-pooled head over 4 labels) on an unpadded varlen batch of 16
+sequences with seeded lengths in [256, 4096]. One step = one encoder forward of the whole batch.
+
+Prints one JSON line: whole-job tokens/s, the live-measured roofline of the attention kernel
+(MFMA-bound, bf16 dense peak 2.5 PFLOP/s) and, for Kev, of the delta-rule kernel (HBM-bound,
 8 TB/s), and the CPU oracle's forward timed on this host's cores as a reported baseline.
 """
 from __future__ import annotations
@@ -28,10 +33,11 @@ HBM_PEAK = 8.0e12         # bytes/s
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--workload", default="kev", choices=["kev", "laya"])
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--batch", type=int, default=64)
-    p.add_argument("--seq-len", type=int, default=512)
+    p.add_argument("--batch", type=int, default=0, help="sequences (default 64 for kev, 16 for laya)")
+    p.add_argument("--seq-len", type=int, default=512, help="kev: tokens per sequence")
     p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
     p.add_argument("--kernel-iters", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -117,8 +123,8 @@ def kernel_rooflines(ctx, shape, n_seqs, seq_len, dtype, iters):
     }
 
 
-def cpu_baseline(shape, weights, seq_len, threads):
-    """The CPU oracle's fp32 forward of one sequence of the same model on this host."""
+def cpu_baseline(shape, weights, seq_len, threads, n_seqs=12):
+    """The CPU oracle's fp32 forward of a few sequences of the same model on this host."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import numpy as np
 
@@ -136,14 +142,162 @@ def cpu_baseline(shape, weights, seq_len, threads):
     model = O.QwenModel(cfg, f, bf16=False)
     from huncho_amd import abi
 
-    ids = abi.synth_uniform_int(SEED, 900, seq_len, 0, shape.vocab - 1)
+    seqs = [abi.synth_uniform_int(SEED, 900 + i, seq_len, 0, shape.vocab - 1) for i in range(n_seqs)]
     t0 = time.perf_counter()
-    h = model.forward(ids)
-    _ = h[-1] @ f["decision_head.weight"].T
+    for ids in seqs:
+        h = model.forward(ids)
+        _ = h[-1] @ f["decision_head.weight"].T
     dt = time.perf_counter() - t0
-    return {"value": round(seq_len / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"1 sequence x {seq_len} tokens of the same Kev-shaped model (all 24 layers + head), "
+    return {"value": round(n_seqs * seq_len / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n_seqs} sequences x {seq_len} tokens of the same Kev-shaped model (all 24 layers + head), "
                       f"fp32 CPU oracle forward, {threads} OpenMP threads, {dt:.2f} s"}
+
+
+def laya_lengths(n_seqs):
+    """Seeded varlen batch: lengths uniform in [256, 4096]."""
+    from huncho_amd import abi
+
+    return [int(x) for x in abi.synth_uniform_int(SEED, 950, n_seqs, 256, 4096)]
+
+
+def laya_attention_work(lengths, heads, d, half_window):
+    """Algorithmic FLOPs of one bidirectional attention launch: 4*heads*d per visible
+    (query, key) pair; all L^2 pairs globally, |i-j| <= half_window locally."""
+    import numpy as np
+
+    pairs = 0
+    for L in lengths:
+        if half_window < 0:
+            pairs += L * L
+        else:
+            i = np.arange(L)
+            pairs += int((np.minimum(L - 1, i + half_window) - np.maximum(0, i - half_window) + 1).sum())
+    return 4.0 * heads * d * pairs
+
+
+def laya_kernel_rooflines(ctx, shape, lengths, dtype, iters):
+    """Times the global and the windowed attention kernels alone on the encoder's layout (q, k, v
+    as token-strided views of fused [tokens][3][heads][64] projection rows)."""
+    import numpy as np
+    import torch
+
+    from huncho_amd.ops import bidir_attention
+
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    n = sum(lengths)
+    heads, d = shape.n_heads, shape.hidden // shape.n_heads
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    qkv = torch.randn((n, 3, heads, d), generator=g, device=dev, dtype=torch.float32).to(dtype)
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)).to(dev)
+    out = torch.empty((n, heads, d), dtype=dtype, device=dev)
+    res = {}
+    for name, hw in (("global", -1), ("local", shape.local_window // 2)):
+        t = time_launches(lambda: bidir_attention(ctx, qkv[:, 0], qkv[:, 1], qkv[:, 2], cu, max(lengths), hw,
+                                                  out=out), iters, stream)
+        res[name] = {"seconds": t, "flops": laya_attention_work(lengths, heads, d, hw),
+                     "bytes": n * 4 * heads * d * 2}
+    torch.cuda.synchronize()
+    return res
+
+
+def laya_cpu_baseline(shape, weights, threads, n_rows=3, n_tokens=2048):
+    """The CPU oracle's fp32 encoder forward of a few rows of the same model on this host."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import oracle as O
+    from huncho_amd import abi
+
+    O.set_threads(threads)
+    cfg = O.BertConfig(hidden_size=shape.hidden, num_hidden_layers=shape.n_layers,
+                       num_attention_heads=shape.n_heads, intermediate_size=shape.intermediate,
+                       vocab_size=shape.vocab, global_attn_every_n_layers=shape.global_every,
+                       local_attention=shape.local_window, global_rope_theta=shape.global_theta,
+                       local_rope_theta=shape.local_theta)
+    f = {k: O.bf16_to_f32(v).reshape(v.shape) for k, v in weights.items()}
+    model = O.BertModel(cfg, f)
+    rows = [abi.synth_uniform_int(SEED, 902 + i, n_tokens, 0, shape.vocab - 1).tolist() for i in range(n_rows)]
+    t0 = time.perf_counter()
+    for ids in rows:
+        h = model.forward([ids])[0]
+        _ = f["head.weight"] @ h.mean(0)
+    dt = time.perf_counter() - t0
+    return {"value": round(n_rows * n_tokens / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n_rows} sequences x {n_tokens} tokens of the same ModernBERT-base-shaped encoder (all 22 "
+                      f"layers + mean-pooled head), fp32 CPU oracle forward, {threads} OpenMP threads, {dt:.2f} s"}
+
+
+def run_laya(args, dtype):
+    import numpy as np
+    import torch
+
+    from huncho_amd import abi
+    from huncho_amd.laya import LayaModel, LayaShape, synthetic_weights
+    from huncho_amd.ops import context_for_torch
+
+    shape = LayaShape()
+    n_seqs = args.batch or 16
+    lengths = laya_lengths(n_seqs)
+    n_tokens = sum(lengths)
+    t0 = time.perf_counter()
+    weights = synthetic_weights(shape, SEED)
+    log(f"synthetic weights in {time.perf_counter() - t0:.1f} s; {n_seqs} rows, {n_tokens} tokens")
+    ctx = context_for_torch(0)
+    info = ctx.device_info()
+    model = LayaModel(ctx, shape, weights, dtype)
+    batch = model.prepare(lengths)
+    ids = torch.from_numpy(abi.synth_uniform_int(SEED, 951, n_tokens, 0, shape.vocab - 1)).to("cuda")
+    log(f"model ready on {info.name.decode()} ({info.compute_units} CUs); warmup {args.warmup}")
+    for _ in range(args.warmup):
+        model.forward_ids(ids, batch)
+    torch.cuda.synchronize()
+    if ctx.take_faults():
+        raise RuntimeError("device faults during warmup")
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        model.forward_ids(ids, batch)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    log(f"{ms:.2f} ms/step; first row logits {np.round(batch['logits'].cpu().numpy()[0], 4).tolist()}")
+    kr = laya_kernel_rooflines(ctx, shape, lengths, dtype, args.kernel_iters)
+    gl, lo = kr["global"], kr["local"]
+    achieved = gl["flops"] / gl["seconds"] / 1e12
+    log(f"global attention {gl['seconds'] * 1e6:.1f} us/launch, windowed {lo['seconds'] * 1e6:.1f} us/launch")
+    line = {
+        "metric": "encoder tokens/s (ModernBERT-base-shaped varlen bf16); attn TFLOP/s as % of MFMA peak",
+        "value": round(n_tokens / (elapsed / args.steps), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic (seeded lengths and token ids, random-init N(0,0.02) weights)",
+        "config": {"workload": "laya_modernbert_encoder", "n_seqs": n_seqs, "lengths": "uniform [256, 4096]",
+                   "tokens_per_step": n_tokens, "layers": shape.n_layers, "hidden": shape.hidden,
+                   "heads": "12 x 64", "global_every": shape.global_every, "local_window": shape.local_window,
+                   "mlp": f"GeGLU {shape.intermediate}", "vocab": shape.vocab, "head": f"mean-pool -> {shape.n_out}"},
+        "roofline": {"kernel": "bidir_attn_16 (global layer)", "bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": MFMA_PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": None,
+                     "us_per_launch": round(gl["seconds"] * 1e6, 2), "flops_per_launch": gl["flops"]},
+        "roofline_local_attention": {"kernel": "bidir_attn_16 (window +-64)", "bound": "mfma",
+                                     "achieved": round(lo["flops"] / lo["seconds"] / 1e12, 2),
+                                     "peak": MFMA_PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                                     "frac": round(lo["flops"] / lo["seconds"] / MFMA_PEAK_BF16, 4),
+                                     "us_per_launch": round(lo["seconds"] * 1e6, 2), "flops_per_launch": lo["flops"],
+                                     "hbm_frac": round(lo["bytes"] / lo["seconds"] / HBM_PEAK, 4)},
+        "device": {"name": info.name.decode(), "cus": info.compute_units, "clock_mhz": info.clock_khz // 1000},
+    }
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        log(f"CPU baseline with {threads} threads")
+        line["cpu_baseline"] = laya_cpu_baseline(shape, weights, threads)
+    print(json.dumps(line), flush=True)
 
 
 def main():
@@ -152,6 +306,16 @@ def main():
         print(f"bench.py measures one GPU: every GPU host here has one, and this path shards by "
               f"independent sequences with no collectives (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
+    import torch
+
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    if args.workload == "laya":
+        run_laya(args, dtype)
+    else:
+        run_kev(args, dtype)
+
+
+def run_kev(args, dtype):
     import numpy as np
     import torch
 
@@ -159,8 +323,8 @@ def main():
     from huncho_amd.kev import KevModel, KevShape, synthetic_weights
     from huncho_amd.ops import context_for_torch
 
-    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
     shape = KevShape()
+    args.batch = args.batch or 64
     t0 = time.perf_counter()
     weights = synthetic_weights(shape, SEED)
     log(f"synthetic weights in {time.perf_counter() - t0:.1f} s")
@@ -230,6 +394,7 @@ def main():
         log(f"CPU baseline with {threads} threads")
         line["cpu_baseline"] = cpu_baseline(shape, weights, args.seq_len, threads)
     print(json.dumps(line), flush=True)
+
 
 
 if __name__ == "__main__":

@@ -5,10 +5,12 @@
 //                      64, optional window |i - j| <= w (local layers), q/k/v read straight
 //                      from the fused Wqkv rows [tokens][3][heads][64]
 //   bidir_attn_f32     the same in fp32 (the reference's execution precision)
-//   layer_norm<T>      LayerNorm without bias, fp32 statistics
-//   geglu<T>           gelu(x1) * x2 with the exact erf GELU
-//   rope_qk<T>         NeoX rotate-half RoPE on the q and k parts of the Wqkv rows, in place
-//   mean_pool_head<T>  per-sequence mean of the final hidden rows, then a linear head (fp32)
+//   layer_norm<T,VEC>  LayerNorm without bias, fp32 statistics
+//   geglu<T,VEC>       gelu(x1) * x2 with the exact erf GELU
+//   rope_qk<T,VEC>     NeoX rotate-half RoPE on the q and k parts of the Wqkv rows, in place
+//   mean_pool_partial<T>, mean_pool_head<T>
+//                      per-sequence mean of the final hidden rows (two deterministic passes),
+//                      then a linear head (fp32)
 //
 // bidir_attn_16 design: one workgroup = one (sequence, head, 128 query positions); 4 waves x
 // 32 queries; S^T = K Q^T on v_mfma_f32_32x32x16 (each lane owns a query column, K rows
@@ -271,98 +273,194 @@ __global__ __launch_bounds__(64) void bidir_attn_f32(BertAttnArgs a) {
     for (int e = 0; e < D; ++e) op[e] = o[e] * inv;
 }
 
+// 16-byte vector of T: 8 x 16-bit or 4 x fp32 elements.
+template <typename T> struct Vec16 { typedef typename Mma16<T>::v8 type; static constexpr int N = 8; };
+template <> struct Vec16<float> { typedef f32x4 type; static constexpr int N = 4; };
+
+__device__ __forceinline__ float wave_sum(float s) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+    return s;
+}
+
 // LayerNorm without bias over rows of `width` (<= 2048): one wave per row, two passes over
-// registers (mean, then the centred sum of squares), statistics in fp32.
-template <typename T>
+// registers (mean, then the centred sum of squares), statistics in fp32. VEC: 16-byte loads
+// and stores (width a multiple of the vector, rows and weights 16-byte aligned).
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void layer_norm(LayerNormArgs a) {
+    typedef typename Vec16<T>::type V;
+    constexpr int N = VEC ? Vec16<T>::N : 1;
+    constexpr int KM = 2048 / (64 * N);
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= a.rows) return;
     const T* x = (const T*)a.x + (long)row * a.x_tok;
     T* y = (T*)a.y + (long)row * a.y_tok;
-    float v[32];
+    const int chunks = a.width / N;
+    float v[KM][N];
     float s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const int i = lane + 64 * k;
-        v[k] = i < a.width ? to_f(x[i]) : 0.0f;
-        s += v[k];
-    }
+    for (int k = 0; k < KM; ++k) {
+        const int c = lane + 64 * k;
+        if constexpr (VEC) {
+            V t = c < chunks ? *(const V*)(x + c * N) : V{};
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
-    const float mean = s / (float)a.width;
+            for (int e = 0; e < N; ++e) v[k][e] = (float)t[e];
+        } else {
+            v[k][0] = c < chunks ? to_f(x[c]) : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < N; ++e) s += v[k][e];
+    }
+    const float mean = wave_sum(s) / (float)a.width;
     float q = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const int i = lane + 64 * k;
-        const float d = i < a.width ? v[k] - mean : 0.0f;
-        q += d * d;
+    for (int k = 0; k < KM; ++k) {
+        const bool in = lane + 64 * k < chunks;
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            const float d = in ? v[k][e] - mean : 0.0f;
+            q += d * d;
+        }
     }
+    const float inv = fast_rsqrt(wave_sum(q) / (float)a.width + a.eps);
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) q += __shfl_xor(q, o);
-    const float inv = fast_rsqrt(q / (float)a.width + a.eps);
+    for (int k = 0; k < KM; ++k) {
+        const int c = lane + 64 * k;
+        if (c >= chunks) continue;
+        if constexpr (VEC) {
+            V t;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const int i = lane + 64 * k;
-        if (i < a.width) y[i] = from_f<T>(((v[k] - mean) * inv) * a.w[i]);
+            for (int h = 0; h < N; h += 4) {
+                const f32x4 w = *(const f32x4*)(a.w + c * N + h);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t[h + e] = from_f<T>(((v[k][h + e] - mean) * inv) * w[e]);
+            }
+            *(V*)(y + c * N) = t;
+        } else {
+            y[c] = from_f<T>(((v[k][0] - mean) * inv) * a.w[c]);
+        }
     }
 }
 
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
 
-// y[t][i] = gelu(x[t][i]) * x[t][I + i], fp32 arithmetic
-template <typename T>
+// y[t][i] = gelu(x[t][i]) * x[t][I + i], fp32 arithmetic; VEC: N elements per thread with
+// 16-byte accesses.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void geglu(GegluArgs a) {
-    const long n = (long)a.rows * a.width;
+    typedef typename Vec16<T>::type V;
+    constexpr int N = VEC ? Vec16<T>::N : 1;
+    const int wn = a.width / N;
+    const long n = (long)a.rows * wn;
     for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
-        const long t = idx / a.width;
-        const int i = (int)(idx % a.width);
+        const long t = idx / wn;
+        const int i = (int)(idx % wn) * N;
         const T* row = (const T*)a.x + t * a.x_tok;
-        ((T*)a.y)[t * a.y_tok + i] = from_f<T>(gelu_erf(to_f(row[i])) * to_f(row[a.width + i]));
+        T* out = (T*)a.y + t * a.y_tok + i;
+        if constexpr (VEC) {
+            const V g = *(const V*)(row + i), u = *(const V*)(row + a.width + i);
+            V r;
+#pragma unroll
+            for (int e = 0; e < N; ++e) r[e] = from_f<T>(gelu_erf((float)g[e]) * (float)u[e]);
+            *(V*)out = r;
+        } else {
+            *out = from_f<T>(gelu_erf(to_f(row[i])) * to_f(row[a.width + i]));
+        }
     }
 }
 
 // RoPE on q (columns 0 .. heads*64) and k (heads*64 .. 2*heads*64) of each row, in place:
 // x[i] = x[i] cos - x[i + 32] sin, x[i + 32] = x[i + 32] cos + x[i] sin (i < 32), at the
-// token's position within its sequence. Grid (position blocks of 8, sequences).
-template <typename T>
+// token's position within its sequence. Grid (position blocks of 8, sequences); each work
+// item rotates N consecutive pairs of one head (16-byte accesses when VEC).
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void rope_qk(RopeQkArgs a) {
+    typedef typename Vec16<T>::type V;
+    constexpr int N = VEC ? Vec16<T>::N : 1;
+    constexpr int UPH = 32 / N;  // work items per head
     const int seq = blockIdx.y;
     const int t0 = a.cu[seq], L = a.cu[seq + 1] - t0;
     if (t0 < 0 || L < 0 || t0 + L > a.n_tokens) {
-        if (threadIdx.x == 0) atomicOr(a.fault, 1);
+        if (threadIdx.x == 0 && blockIdx.x == 0) atomicOr(a.fault, 1);
         return;
     }
-    const int pairs = 2 * a.heads * 32;  // (q | k) x heads x 32 rotation pairs per token
-    for (int pp = blockIdx.x * 8; pp < min(L, blockIdx.x * 8 + 8); ++pp) {
-        if (pp >= a.max_pos) {
-            if (threadIdx.x == 0) atomicOr(a.fault, 4);
-            return;
-        }
-        T* row = (T*)a.x + (long)(t0 + pp) * a.x_tok;
-        for (int k = threadIdx.x; k < pairs; k += blockDim.x) {
-            const int hh = k / 32, i = k % 32;  // hh < heads: q heads; >= heads: k heads
-            T* xh = row + hh * 64;
-            const float c = a.cos[(long)pp * 32 + i], s = a.sin[(long)pp * 32 + i];
-            const float x1 = to_f(xh[i]), x2 = to_f(xh[i + 32]);
-            xh[i] = from_f<T>(x1 * c - x2 * s);
-            xh[i + 32] = from_f<T>(x2 * c + x1 * s);
+    const int p0 = blockIdx.x * 8, rows = min(L - p0, 8);
+    if (rows <= 0) return;
+    if (p0 + rows > a.max_pos) {
+        if (threadIdx.x == 0) atomicOr(a.fault, 4);
+        return;
+    }
+    const int per_tok = 2 * a.heads * UPH;
+    for (int u = threadIdx.x; u < rows * per_tok; u += blockDim.x) {
+        const int pp = p0 + u / per_tok, w = u % per_tok;
+        const int hh = w / UPH, i0 = (w % UPH) * N;
+        T* xh = (T*)a.x + (long)(t0 + pp) * a.x_tok + hh * 64 + i0;
+        const float* cs = a.cos + (long)pp * 32 + i0;
+        const float* sn = a.sin + (long)pp * 32 + i0;
+        if constexpr (VEC) {
+            V x1 = *(const V*)xh, x2 = *(const V*)(xh + 32), r1, r2;
+#pragma unroll
+            for (int h = 0; h < N; h += 4) {
+                const f32x4 c = *(const f32x4*)(cs + h), sv = *(const f32x4*)(sn + h);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float a1 = (float)x1[h + e], a2 = (float)x2[h + e];
+                    r1[h + e] = from_f<T>(a1 * c[e] - a2 * sv[e]);
+                    r2[h + e] = from_f<T>(a2 * c[e] + a1 * sv[e]);
+                }
+            }
+            *(V*)xh = r1;
+            *(V*)(xh + 32) = r2;
+        } else {
+            const float c = cs[0], sv = sn[0];
+            const float x1 = to_f(xh[0]), x2 = to_f(xh[32]);
+            xh[0] = from_f<T>(x1 * c - x2 * sv);
+            xh[32] = from_f<T>(x2 * c + x1 * sv);
         }
     }
 }
 
-// logits[s][o] = head_b[o] + sum_i head_w[o][i] * mean_t x[t][i] over the sequence's rows
+// Mean pooling in two deterministic passes. Pass 1, grid (sequences, POOL_PARTS): part j of a
+// sequence of L rows sums rows [L j / P, L (j + 1) / P), P = min(POOL_PARTS, L), into the fp32
+// slot row t0 + j of `pool` (slots never overlap another sequence's, since P <= L).
+constexpr int POOL_PARTS = 32;
+
+template <typename T>
+__global__ __launch_bounds__(256) void mean_pool_partial(MeanPoolArgs a) {
+    const int seq = blockIdx.x, j = blockIdx.y;
+    const int t0 = a.cu[seq], L = a.cu[seq + 1] - t0;
+    if (t0 < 0 || L <= 0 || t0 + L > a.n_tokens) {
+        if (threadIdx.x == 0 && j == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    const int P = min(POOL_PARTS, L);
+    if (j >= P) return;
+    const long ta = t0 + (long)L * j / P, tb = t0 + (long)L * (j + 1) / P;
+    const T* x = (const T*)a.x;
+    for (int i = threadIdx.x; i < a.width; i += blockDim.x) {
+        float s0 = 0.0f, s1 = 0.0f;
+        long t = ta;
+        for (; t + 1 < tb; t += 2) {
+            s0 += to_f(x[t * a.x_tok + i]);
+            s1 += to_f(x[(t + 1) * a.x_tok + i]);
+        }
+        if (t < tb) s0 += to_f(x[t * a.x_tok + i]);
+        a.pool[(long)(t0 + j) * a.width + i] = s0 + s1;
+    }
+}
+
+// Pass 2, one workgroup per sequence: the parts summed in order, divided by L, then
+// logits[s][o] = head_b[o] + sum_i head_w[o][i] * mean_i (fp32).
 template <typename T>
 __global__ __launch_bounds__(256) void mean_pool_head(MeanPoolArgs a) {
     extern __shared__ float pooled[];  // [width]
     const int seq = blockIdx.x;
     const int t0 = a.cu[seq], L = a.cu[seq + 1] - t0;
-    if (t0 < 0 || L <= 0 || t0 + L > a.n_tokens) {
-        if (threadIdx.x == 0) atomicOr(a.fault, 1);
-        return;
-    }
+    if (t0 < 0 || L <= 0 || t0 + L > a.n_tokens) return;  // reported by pass 1
+    const int P = min(POOL_PARTS, L);
     for (int i = threadIdx.x; i < a.width; i += blockDim.x) {
         float s = 0.0f;
-        for (int t = 0; t < L; ++t) s += to_f(((const T*)a.x)[(long)(t0 + t) * a.x_tok + i]);
+        for (int j = 0; j < P; ++j) s += a.pool[(long)(t0 + j) * a.width + i];
         pooled[i] = s / (float)L;
     }
     __syncthreads();
@@ -370,8 +468,7 @@ __global__ __launch_bounds__(256) void mean_pool_head(MeanPoolArgs a) {
     for (int o = wave; o < a.n_out; o += blockDim.x / 64) {
         float s = 0.0f;
         for (int i = lane; i < a.width; i += 64) s += to_f(((const T*)a.head_w)[(long)o * a.width + i]) * pooled[i];
-#pragma unroll
-        for (int k = 32; k >= 1; k >>= 1) s += __shfl_xor(s, k);
+        s = wave_sum(s);
         if (lane == 0) a.logits[(long)seq * a.n_out + o] = s + (a.head_b ? a.head_b[o] : 0.0f);
     }
 }
@@ -413,24 +510,52 @@ extern "C" int hk_launch_bidir_attention(int dtype, const hk::BertAttnArgs* a, i
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+#define HK_BERT_DISPATCH_VEC(dtype, vec, KERNEL, grid, block, lds, stream, args)                              \
+    do {                                                                                                   \
+        if ((dtype) == hk::DT_BF16) {                                                                      \
+            if (vec) hipLaunchKernelGGL((hk::bert::KERNEL<hk::bf16, true>), grid, block, lds, stream, args); \
+            else hipLaunchKernelGGL((hk::bert::KERNEL<hk::bf16, false>), grid, block, lds, stream, args);    \
+        } else if ((dtype) == hk::DT_F16) {                                                                \
+            if (vec) hipLaunchKernelGGL((hk::bert::KERNEL<hk::f16, true>), grid, block, lds, stream, args);  \
+            else hipLaunchKernelGGL((hk::bert::KERNEL<hk::f16, false>), grid, block, lds, stream, args);     \
+        } else {                                                                                           \
+            if (vec) hipLaunchKernelGGL((hk::bert::KERNEL<float, true>), grid, block, lds, stream, args);    \
+            else hipLaunchKernelGGL((hk::bert::KERNEL<float, false>), grid, block, lds, stream, args);       \
+        }                                                                                                  \
+    } while (0)
+
+static int vec_elems(int dtype) { return dtype == hk::DT_F32 ? 4 : 8; }
+
 extern "C" int hk_launch_layer_norm(int dtype, const hk::LayerNormArgs* a, hipStream_t stream) {
-    HK_BERT_DISPATCH(dtype, layer_norm, dim3((a->rows + 3) / 4), dim3(256), 0, stream, *a);
+    if (a->rows == 0) return HK_OK;
+    const int N = vec_elems(dtype);
+    const bool vec = a->width % N == 0 && a->x_tok % N == 0 && a->y_tok % N == 0 && aligned16(a->x) &&
+                     aligned16(a->y) && aligned16(a->w);
+    HK_BERT_DISPATCH_VEC(dtype, vec, layer_norm, dim3((a->rows + 3) / 4), dim3(256), 0, stream, *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
 extern "C" int hk_launch_geglu(int dtype, const hk::GegluArgs* a, hipStream_t stream) {
-    const long n = (long)a->rows * a->width;
+    const int N = vec_elems(dtype);
+    const bool vec = a->width % N == 0 && a->x_tok % N == 0 && a->y_tok % N == 0 && aligned16(a->x) && aligned16(a->y);
+    const long n = (long)a->rows * (a->width / (vec ? N : 1));
+    if (n == 0) return HK_OK;
     const int blocks = (int)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
-    HK_BERT_DISPATCH(dtype, geglu, dim3(blocks > 0 ? blocks : 1), dim3(256), 0, stream, *a);
+    HK_BERT_DISPATCH_VEC(dtype, vec, geglu, dim3(blocks), dim3(256), 0, stream, *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
 extern "C" int hk_launch_rope_qk(int dtype, const hk::RopeQkArgs* a, int n_seqs, int max_len, hipStream_t stream) {
-    HK_BERT_DISPATCH(dtype, rope_qk, dim3((max_len + 7) / 8, n_seqs), dim3(256), 0, stream, *a);
+    if (max_len == 0) return HK_OK;
+    const bool vec = a->x_tok % vec_elems(dtype) == 0 && aligned16(a->x) && aligned16(a->cos) && aligned16(a->sin);
+    HK_BERT_DISPATCH_VEC(dtype, vec, rope_qk, dim3((max_len + 7) / 8, n_seqs), dim3(256), 0, stream, *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
 extern "C" int hk_launch_mean_pool_head(int dtype, const hk::MeanPoolArgs* a, int n_seqs, hipStream_t stream) {
+    HK_BERT_DISPATCH(dtype, mean_pool_partial, dim3(n_seqs, hk::bert::POOL_PARTS), dim3(256), 0, stream, *a);
     HK_BERT_DISPATCH(dtype, mean_pool_head, dim3(n_seqs), dim3(256), a->width * sizeof(float), stream, *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }

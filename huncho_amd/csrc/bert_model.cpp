@@ -159,6 +159,7 @@ namespace {
 
 struct BertBuffers {
     void *h, *x, *qkv, *att, *gi, *act;
+    float* pool;
 };
 
 size_t bert_carve(const hk_bert_model* m, char* base, int n, BertBuffers* b) {
@@ -176,6 +177,7 @@ size_t bert_carve(const hk_bert_model* m, char* base, int n, BertBuffers* b) {
     b->att = take((size_t)n * c.hidden * e);
     b->gi = take((size_t)n * 2 * c.intermediate * e);
     b->act = take((size_t)n * c.intermediate * e);
+    b->pool = (float*)take(c.n_out > 0 ? (size_t)n * c.hidden * sizeof(float) : 0);
     return off;
 }
 
@@ -251,7 +253,8 @@ extern "C" int hk_bert_forward(hk_bert_model* m, const int32_t* ids, const int32
     void* fin = hidden_out ? hidden_out : b.x;
     BRUN(hk_layer_norm(ctx, dt, b.h, H, m->final_norm, c.eps, n, H, fin, H));
     if (c.n_out > 0) {
-        hk::MeanPoolArgs pa{fin, (long)H, cu_dev, n_seqs, n, H, m->head_w, m->head_b, c.n_out, logits, ctx->fault_dev};
+        hk::MeanPoolArgs pa{fin, (long)H, cu_dev, n_seqs, n, H, m->head_w, m->head_b, c.n_out, logits, ctx->fault_dev,
+                            b.pool};
         BRUN(hk_launch_mean_pool_head(dt, &pa, n_seqs, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "head launch") : 0);
     }
     return HK_OK;

@@ -200,6 +200,7 @@ struct MeanPoolArgs {
     int n_out;
     float* logits;  // [n_seqs][n_out]
     int* fault;
+    float* pool;  // [n_tokens][width] fp32 partial sums (slot rows t0 .. t0 + min(32, L) - 1)
 };
 
 }  // namespace hk

@@ -68,11 +68,13 @@ def test_bidir_attention_varlen(ctx, dtype, half_window):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_layer_norm(ctx, dtype):
+@pytest.mark.parametrize("width", [768, 100])
+def test_layer_norm(ctx, dtype, width):
+    """Widths that take the 16-byte vector path (768) and the scalar path (100)."""
     from huncho_amd.ops import layer_norm
 
-    x = _round(abi.synth_normal(SEED, 40, 37 * 768, 0.3, 2.0), dtype).reshape(37, 768)
-    w = O.round_bf16(abi.synth_normal(SEED, 41, 768, 1.0, 0.1))
+    x = _round(abi.synth_normal(SEED, 40, 37 * width, 0.3, 2.0), dtype).reshape(37, width)
+    w = O.round_bf16(abi.synth_normal(SEED, 41, width, 1.0, 0.1))
     y = layer_norm(ctx, torch.from_numpy(x).to(dtype).cuda(), torch.from_numpy(w).cuda(), 1e-5)
     ref = O.layer_norm(x, w, 1e-5)
     err = rel_err(y.float().cpu().numpy(), ref)
