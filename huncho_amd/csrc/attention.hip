@@ -60,6 +60,7 @@ constexpr int KV_ROW = 128;                        // LDS row: one key's 128 dim
 constexpr int TILE_ELEMS = BN * KV_ROW;            // one K or V tile: 16 KB
 constexpr size_t ATTN16_LDS = 4 * TILE_ELEMS * 2;  // K and V, double-buffered: 65,536 B
 constexpr float RESCALE_LOG2 = 8.0f;  // exponents may run up to 2^8 above the row max in use
+constexpr int VMCNT0 = 0x0F70;        // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 
 // The 16-byte chunk c of key row r sits at chunk c ^ swz(r). With this swizzle the row
 // writes, the permuted-row K reads of S^T = K Q^T and the transposing V reads of P.V each
@@ -73,14 +74,18 @@ __device__ __forceinline__ int lds_off(int r, int c) { return r * KV_ROW + 8 * (
 //   buffer t % 2; write tile t+1 into buffer (t+1) % 2; barrier.
 // Each thread moves 4 consecutive keys (one page: pages hold >= 16 keys) x one 16-byte chunk
 // of K and of V, so one block-table entry addresses all 8 of its loads. Loads are
-// unconditional (addresses clamped to pool row 0) and masked when written to LDS.
+// unconditional (addresses clamped to pool row 0) and masked when written to LDS (only
+// waves holding keys past the context pay for the masking).
 // Softmax keeps the raw-score row max m and evaluates p = 2^(s c - m c) with one FMA
 // (c = scale log2 e); the O / l rescale happens only when the max grew by more than 2^8
 // (otherwise p <= 2^8 and the fp32 sums lose nothing), which is the same normalised result.
+// The row sum l adds the probabilities as rounded for P.V (v_dot2 against ones), so the
+// weights applied to V sum to one.
 template <typename T>
 __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     typedef typename Mma16<T>::v8 v8;
     typedef typename Mma16<T>::v4 v4;
+    typedef typename Mma16<T>::v2 v2;
     extern __shared__ __attribute__((aligned(16))) char attn_smem[];
     T* const lds = (T*)attn_smem;  // [buf][K | V][64][128]
 
@@ -93,7 +98,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     const int q0 = a.cu_seqlens_q[seq];
     const int q_len = a.cu_seqlens_q[seq + 1] - q0;
     const int ctx = a.context_lens[seq];
-    const int P = a.pos_per_block;
+    const int P = a.pos_per_block;  // 128 / group: a power of two
+    const int p_shift = __builtin_ctz(P);
     if (q0 < 0 || q_len < 0 || q0 + q_len > a.n_tokens || q_len > ctx) {
         if (threadIdx.x == 0) atomicOr(a.fault, 1);
         return;
@@ -163,12 +169,21 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     auto store_tile = [&](int buf) {
         T* Kb = lds + buf * 2 * TILE_ELEMS;
         T* Vb = Kb + TILE_ELEMS;
+        if (__all(nval == 4)) {  // every key of the wave's rows lies in the context: no masking
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t m = i < nval ? ~0u : 0u;
-            const int o = lds_off(4 * kq + i, ch);
-            *(uint4*)(Kb + o) = uint4{kr[i].x & m, kr[i].y & m, kr[i].z & m, kr[i].w & m};
-            *(uint4*)(Vb + o) = uint4{vr[i].x & m, vr[i].y & m, vr[i].z & m, vr[i].w & m};
+            for (int i = 0; i < 4; ++i) {
+                const int o = lds_off(4 * kq + i, ch);
+                *(uint4*)(Kb + o) = kr[i];
+                *(uint4*)(Vb + o) = vr[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = i < nval ? ~0u : 0u;
+                const int o = lds_off(4 * kq + i, ch);
+                *(uint4*)(Kb + o) = uint4{kr[i].x & m, kr[i].y & m, kr[i].z & m, kr[i].w & m};
+                *(uint4*)(Vb + o) = uint4{vr[i].x & m, vr[i].y & m, vr[i].z & m, vr[i].w & m};
+            }
         }
     };
 
@@ -198,37 +213,144 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
 
     // epilogue of a block: o = O / l (both lane halves hold partial row sums), then the
     // output gate o = round(o) * round(sigmoid(gate)) as the reference rounds both
-    auto finish_block = [&]() {
+    // Epilogue of block qb: o = O / l (both lane halves hold partial row sums), rounded to T,
+    // then the output gate o = round(o) * round(sigmoid(gate)) as the reference rounds both.
+    // O leaves its accumulator layout through LDS (the free K/V buffer `stg`, row-major with a
+    // row XOR chunk swizzle), so the gate loads and output stores move whole 256-byte rows
+    // (16 lanes x 16 bytes) instead of 32 rows x 16 bytes per instruction; the gate loads are
+    // issued first and land while O is staged.
+    auto finish_block = [&](int qb, int stg) {
+        const bool gated = a.gate != nullptr;
+        T* const sb = lds + stg * 2 * TILE_ELEMS;  // [128 rows][128] T, 32 KB
+        v8 gch[8];
+        int orow[8];  // token index of each chunk's row (-1: past the sequence)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int id = tid + 256 * k, R = id >> 4, ch = id & 15;
+            const int qi_ = qb * P + (R & (P - 1));
+            const int hd = kvh * a.group + (R >> p_shift);
+            orow[k] = qi_ < q_len ? q0 + qi_ : -1;
+            const T* gp = (const T*)a.gate + (long)(q0 + min(qi_, q_len - 1)) * a.g_tok + (long)hd * a.g_head + ch * 8;
+            gch[k] = gated ? *(const v8*)gp : v8{};
+        }
         const float l_tot = l_run + __shfl_xor(l_run, 32);
         const float inv_l = 1.0f / l_tot;
-        if (q_valid) {
-            T* op = (T*)a.o + (long)(q0 + qi) * a.o_tok + (long)head * a.o_head;
-            v4 gv[4][4];
-            const bool gated = a.gate != nullptr;
-            if (gated) {
-                const T* gp = (const T*)a.gate + (long)(q0 + qi) * a.g_tok + (long)head * a.g_head;
 #pragma unroll
-                for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) gv[db][jj] = *(const v4*)(gp + db * 32 + jj * 8 + g * 4);
+            for (int jj = 0; jj < 4; ++jj) {
+                const int c16 = db * 4 + jj;
+                *(v4*)(sb + row * KV_ROW + 8 * (c16 ^ (row & 15)) + 4 * g) =
+                    v4{(T)(acc_o[db][jj * 4] * inv_l), (T)(acc_o[db][jj * 4 + 1] * inv_l),
+                       (T)(acc_o[db][jj * 4 + 2] * inv_l), (T)(acc_o[db][jj * 4 + 3] * inv_l)};
             }
+        __syncthreads();
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+        for (int k = 0; k < 8; ++k) {
+            const int id = tid + 256 * k, R = id >> 4, ch = id & 15;
+            v8 ov = *(const v8*)(sb + R * KV_ROW + 8 * (ch ^ (R & 15)));
+            if (gated) {
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    float r[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        r[e] = acc_o[db][jj * 4 + e] * inv_l;
-                        if (gated) r[e] = (float)(T)r[e] * (float)(T)sigmoidf_((float)gv[db][jj][e]);
-                    }
-                    *(v4*)(op + db * 32 + jj * 8 + g * 4) = v4{(T)r[0], (T)r[1], (T)r[2], (T)r[3]};
-                }
+                for (int e = 0; e < 8; ++e) ov[e] = (T)((float)ov[e] * (float)(T)fast_sigmoid((float)gch[k][e]));
+            }
+            if (orow[k] >= 0)
+                *(v8*)((T*)a.o + (long)orow[k] * a.o_tok + (long)(kvh * a.group + (R >> p_shift)) * a.o_head + ch * 8) = ov;
         }
+        __syncthreads();  // staging reads done before the buffer takes a K/V tile again
 #pragma unroll
         for (int db = 0; db < 4; ++db) acc_o[db] = f32x16{};
         m_use = -INFINITY;
         l_run = 0.0f;
+    };
+
+    // one 64-key tile of the schedule: prefetch the next tile (and the table entry after it),
+    // S^T, online softmax, O^T += V^T P^T, stage the prefetched tile, barrier
+    auto step = [&](int i) {
+        const int buf = i & 1;
+        if (i + 1 < n_sched) {
+            load_tile(sched_tile(i + 1));
+            if (i + 2 < n_sched) lookup(sched_tile(i + 2));
+        }
+        const T* Kb = lds + buf * 2 * TILE_ELEMS;
+        const T* Vb = Kb + TILE_ELEMS;
+
+        // S^T = K Q^T for this wave's 32 queries: two 32-key halves. Each half then takes its
+        // own online-softmax step, so the softmax of half 0 can run while the MFMAs of half 1
+        // execute, and the softmax of half 1 while the P.V of half 0 executes.
+        f32x16 s[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            s[kb] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+                s[kb] = Mma16<T>::mma(*(const v8*)(Kb + kb * 32 * KV_ROW + koff[ks]), qf[ks], s[kb]);
+        }
+        const int n0 = sched_tile(i) * BN;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            // causal mask (only halves that reach past the block's first query), raw-score max
+            float mloc = -INFINITY;
+            if (n0 + kb * 32 + 31 > first_pos) {
+                const int lim = qpos - n0 - kb * 32 - g * 16;  // key offset j is visible iff j <= lim
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    if (j > lim) s[kb][j] = -INFINITY;
+                    mloc = fmaxf(mloc, s[kb][j]);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, s[kb][j]);
+            }
+            const float m_half = wave_max32(mloc);
+            const bool grow = (m_half - m_use) * c > RESCALE_LOG2;
+            if (__any(grow)) {
+                const float m_new = grow ? m_half : m_use;
+                // lanes that keep their max keep their sums (alpha 1; also avoids -inf - -inf)
+                const float alpha = grow ? fast_exp2((m_use - m_new) * c) : 1.0f;
+                m_use = m_new;
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc_o[db][j] *= alpha;
+            }
+            const float mc = m_use * c;
+            v8 pf[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                v8 t;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) t[k] = (T)fast_exp2(fmaf(s[kb][h * 8 + k], c, -mc));
+                pf[h] = t;
+            }
+            // row sums of the rounded probabilities that P.V consumes (v_dot2 against ones)
+            {
+                const v2 one2 = {(T)1.0f, (T)1.0f};
+                float l0 = 0.0f, l1 = 0.0f;
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int q = 0; q < 8; q += 4) {
+                        l0 = dot2(v2{pf[h][q], pf[h][q + 1]}, one2, l0);
+                        l1 = dot2(v2{pf[h][q + 2], pf[h][q + 3]}, one2, l1);
+                    }
+                l_run += l0 + l1;
+            }
+            // O^T += V^T P^T: keys kb*32 + g*16 + h*8 + [0..7] of dims db*32 + [0..31]
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const T* vb = Vb + vofs[db];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const i16x4 lo = lds_read_tr16(vb + (kb * 32 + h * 8) * KV_ROW);
+                    const i16x4 hi = lds_read_tr16(vb + (kb * 32 + h * 8 + 4) * KV_ROW);
+                    const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc_o[db] = Mma16<T>::mma(af, pf[h], acc_o[db]);
+                }
+            }
+        }
+        if (i + 1 < n_sched) store_tile(buf ^ 1);
+        __syncthreads();
     };
 
     begin_block(qb_a);
@@ -238,93 +360,18 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     if (n_sched > 1) lookup(sched_tile(1));
     store_tile(0);
     __syncthreads();
-    for (int i = 0; i < n_sched; ++i) {
-        const int buf = i & 1;
-        if (i + 1 < n_sched) {
-            load_tile(sched_tile(i + 1));
-            if (i + 2 < n_sched) lookup(sched_tile(i + 2));
-        }
-        const T* Kb = lds + buf * 2 * TILE_ELEMS;
-        const T* Vb = Kb + TILE_ELEMS;
-
-        // S^T = K Q^T for this wave's 32 queries: two 32-key blocks
-        f32x16 s[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            s[kb] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks)
-                s[kb] = Mma16<T>::mma(*(const v8*)(Kb + kb * 32 * KV_ROW + koff[ks]), qf[ks], s[kb]);
-        }
-        if (i == nt_a - 1 && n_blocks == 2) load_q(qb_b);  // lands during this tile's softmax and P.V
-        // causal mask (only tiles that reach past the block's first query), raw-score max
-        const int n0 = sched_tile(i) * BN;
-        float mloc = -INFINITY;
-        if (n0 + BN - 1 > first_pos) {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    if (n0 + kb * 32 + g * 16 + j > qpos) s[kb][j] = -INFINITY;
-                    mloc = fmaxf(mloc, s[kb][j]);
-                }
-        } else {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, s[kb][j]);
-        }
-        const float m_tile = wave_max32(mloc);
-        const bool grow = (m_tile - m_use) * c > RESCALE_LOG2;
-        if (__any(grow)) {
-            const float m_new = grow ? m_tile : m_use;
-            // lanes that keep their max keep their sums (alpha 1; also avoids -inf - -inf)
-            const float alpha = grow ? fast_exp2((m_use - m_new) * c) : 1.0f;
-            m_use = m_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) acc_o[db][j] *= alpha;
-        }
-        const float mc = m_use * c;
-        float lsum = 0.0f;
-        v8 pf[4];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                v8 t;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const float e = fast_exp2(fmaf(s[kb][h * 8 + k], c, -mc));
-                    lsum += e;
-                    t[k] = (T)e;
-                }
-                pf[kb * 2 + h] = t;
-            }
-        l_run += lsum;
-        // O^T += V^T P^T: keys kb*32 + g*16 + h*8 + [0..7] of dims db*32 + [0..31]
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const T* vb = Vb + vofs[db];
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                const int kb = cc >> 1, h = cc & 1;
-                const i16x4 lo = lds_read_tr16(vb + (kb * 32 + h * 8) * KV_ROW);
-                const i16x4 hi = lds_read_tr16(vb + (kb * 32 + h * 8 + 4) * KV_ROW);
-                const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                acc_o[db] = Mma16<T>::mma(af, pf[cc], acc_o[db]);
-            }
-        }
-        if (i == nt_a - 1) {  // block a done: write it, start block b
-            finish_block();
-            if (n_blocks == 2) begin_block(qb_b);
-        }
-        if (i + 1 < n_sched) store_tile(buf ^ 1);
-        __syncthreads();
+    // The two blocks run as two loops whose bodies issue only the tile and table loads:
+    // Q, gate and output traffic stays between them, so the compiler's wait counting never
+    // holds a tile's S^T behind the next tile's prefetch.
+    for (int i = 0; i < nt_a; ++i) step(i);
+    if (n_blocks == 2) load_q(qb_b);  // lands while block a's output is written
+    finish_block(qb_a, (nt_a - 1) & 1);  // the buffer of block a's last tile is free
+    if (n_blocks == 2) {
+        begin_block(qb_b);
+        __builtin_amdgcn_s_waitcnt(VMCNT0);  // Q of block b and block a's stores, once
+        for (int i = nt_a; i < n_sched; ++i) step(i);
+        finish_block(qb_b, 0);
     }
-    if (n_blocks == 2) finish_block();
 }
 
 // ---------------------------------------------------------------------------

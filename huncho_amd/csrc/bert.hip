@@ -84,13 +84,14 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
     // thread t moves key rows t / 8 and t / 8 + 32 of a tile, 16-byte chunk t % 8, of K and V;
     // keys past the sequence end read its last row (finite; their scores are masked)
     const int lr = tid >> 3, lc = tid & 7;
-    uint4 kr[2], vr[2];
+    // (native vector registers: a copied uint4 struct array stays in scratch memory)
+    v8 kr[2], vr[2];
     auto load_tile = [&](int tile) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int key = min(tile * BN + lr + 32 * i, L - 1);
-            kr[i] = *(const uint4*)((const T*)a.k + (long)(t0 + key) * a.k_tok + (long)h * D + lc * 8);
-            vr[i] = *(const uint4*)((const T*)a.v + (long)(t0 + key) * a.v_tok + (long)h * D + lc * 8);
+            kr[i] = *(const v8*)((const T*)a.k + (long)(t0 + key) * a.k_tok + (long)h * D + lc * 8);
+            vr[i] = *(const v8*)((const T*)a.v + (long)(t0 + key) * a.v_tok + (long)h * D + lc * 8);
         }
     };
     auto store_tile = [&](int buf) {
@@ -98,8 +99,8 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
         T* Vb = Kb + TILE;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            *(uint4*)(Kb + k_off(lr + 32 * i, lc)) = kr[i];
-            *(uint4*)(Vb + v_off(lr + 32 * i, lc)) = vr[i];
+            *(v8*)(Kb + k_off(lr + 32 * i, lc)) = kr[i];
+            *(v8*)(Vb + v_off(lr + 32 * i, lc)) = vr[i];
         }
     };
 
