@@ -41,6 +41,10 @@ def parse():
     p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
     p.add_argument("--kernel-iters", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--kernels-only", action="store_true",
+                   help="time only the roofline kernels (no model; for counter collection)")
+    p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                   help="copy BYTES device-to-device 3 times and exit (HBM counter calibration)")
     p.add_argument("--cpu-threads", type=int, default=0)
     return p.parse_args()
 
@@ -264,6 +268,8 @@ def run_laya(args, dtype):
     gl, lo = kr["global"], kr["local"]
     achieved = gl["flops"] / gl["seconds"] / 1e12
     log(f"global attention {gl['seconds'] * 1e6:.1f} us/launch, windowed {lo['seconds'] * 1e6:.1f} us/launch")
+    measured = load_traffic("laya") if (n_seqs, args.dtype) == (16, "bf16") else {}
+    traffic_of = lambda k: sum(measured[k]) if k in measured else None
     line = {
         "metric": "encoder tokens/s (ModernBERT-base-shaped varlen bf16); attn TFLOP/s as % of MFMA peak",
         "value": round(n_tokens / (elapsed / args.steps), 1),
@@ -283,7 +289,7 @@ def run_laya(args, dtype):
                    "mlp": f"GeGLU {shape.intermediate}", "vocab": shape.vocab, "head": f"mean-pool -> {shape.n_out}"},
         "roofline": {"kernel": "bidir_attn_16 (global layer)", "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": MFMA_PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": None,
+                     "frac": round(achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": traffic_of("global"),
                      "us_per_launch": round(gl["seconds"] * 1e6, 2), "flops_per_launch": gl["flops"]},
         "roofline_local_attention": {"kernel": "bidir_attn_16 (window +-64)", "bound": "mfma",
                                      "achieved": round(lo["flops"] / lo["seconds"] / 1e12, 2),
@@ -308,11 +314,51 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {src.numel() * 4} bytes 3 times")
+        return
     dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    if args.kernels_only:
+        from huncho_amd.ops import context_for_torch
+
+        ctx = context_for_torch(0)
+        if args.workload == "laya":
+            from huncho_amd.laya import LayaShape
+
+            kr = laya_kernel_rooflines(ctx, LayaShape(), laya_lengths(args.batch or 16), dtype, args.kernel_iters)
+        else:
+            from huncho_amd.kev import KevShape
+
+            kr = kernel_rooflines(ctx, KevShape(), args.batch or 64, args.seq_len, dtype, args.kernel_iters)
+        print(json.dumps({k: round(v["seconds"] * 1e6, 2) for k, v in kr.items()}), flush=True)
+        return
     if args.workload == "laya":
         run_laya(args, dtype)
     else:
         run_kev(args, dtype)
+
+
+def load_traffic(workload):
+    """HBM bytes per launch of the roofline kernels, measured with rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes scaled by a copy of known size (profiles/hbm_traffic.txt, one line per
+    `workload kernel fetch_bytes=F write_bytes=W`). Missing file or entry: {}."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.txt")
+    out = {}
+    if not os.path.exists(path):
+        return out
+    for line in open(path):
+        parts = line.split()
+        if len(parts) < 4 or line.startswith("#") or parts[0] != workload:
+            continue
+        kv = dict(p.split("=", 1) for p in parts[2:] if "=" in p)
+        if "fetch_bytes" in kv and "write_bytes" in kv:
+            out[parts[1]] = (int(kv["fetch_bytes"]), int(kv["write_bytes"]))
+    return out
 
 
 def run_kev(args, dtype):
@@ -359,6 +405,8 @@ def run_kev(args, dtype):
     attn_achieved = a["flops"] / a["seconds"] / 1e12
     gdn_achieved = gd["bytes"] / gd["seconds"] / 1e9
     log(f"attention {a['seconds'] * 1e6:.1f} us/launch, delta rule {gd['seconds'] * 1e6:.1f} us/launch")
+    measured = load_traffic("kev") if (args.batch, args.seq_len, args.dtype) == (64, 512, "bf16") else {}
+    traffic_of = lambda k: sum(measured[k]) if k in measured else None
     line = {
         "metric": "prefill tokens/s (Kev-shaped 64x512 bf16); attn TFLOP/s as % of MFMA peak",
         "value": round(n_tokens / (elapsed / args.steps), 1),
@@ -379,12 +427,13 @@ def run_kev(args, dtype):
                    "decision_head": shape.n_out},
         "roofline": {"kernel": "paged_prefill_attn", "bound": "mfma", "achieved": round(attn_achieved, 2),
                      "peak": MFMA_PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(attn_achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": None,
+                     "frac": round(attn_achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": traffic_of("attention"),
                      "us_per_launch": round(a["seconds"] * 1e6, 2), "flops_per_launch": a["flops"],
                      "hbm_frac": round(a["bytes"] / a["seconds"] / HBM_PEAK, 4)},
         "roofline_delta_rule": {"kernel": "gdn_chunk", "bound": "hbm", "achieved": round(gdn_achieved, 1),
                                 "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                                "frac": round(gd["bytes"] / gd["seconds"] / HBM_PEAK, 4), "traffic": None,
+                                "frac": round(gd["bytes"] / gd["seconds"] / HBM_PEAK, 4),
+                                "traffic": traffic_of("delta_rule"),
                                 "us_per_launch": round(gd["seconds"] * 1e6, 2), "bytes_per_launch": gd["bytes"],
                                 "tflops": round(gd["flops"] / gd["seconds"] / 1e12, 2)},
         "device": {"name": info.name.decode(), "cus": info.compute_units, "clock_mhz": info.clock_khz // 1000},

@@ -44,7 +44,13 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
     extern __shared__ __attribute__((aligned(16))) char bert_smem[];
     T* const lds = (T*)bert_smem;  // [buf][K | V][64][64]
 
-    const int qb = blockIdx.x, h = blockIdx.y, seq = blockIdx.z;
+    // XCD-aware order: workgroup i runs on XCD i % 8 as that XCD's (i / 8)-th. (sequence, head)
+    // groups are striped over the XCDs (group x, x + 8, ... on XCD x) and all q-blocks of a
+    // group run on its XCD back to back, sharing that XCD's L2 copy of the group's K/V rows
+    const int slot = blockIdx.x >> 3;
+    const int grp = (blockIdx.x & 7) + 8 * (slot / a.qblocks);
+    if (grp >= a.heads * a.n_seqs) return;
+    const int qb = slot % a.qblocks, h = grp % a.heads, seq = grp / a.heads;
     const int t0 = a.cu[seq];
     const int L = a.cu[seq + 1] - t0;
     if (t0 < 0 || L < 0 || t0 + L > a.n_tokens) {
@@ -503,11 +509,17 @@ extern "C" int hk_launch_bidir_attention(int dtype, const hk::BertAttnArgs* a, i
             return HK_ERR_DEVICE;
         configured = true;
     }
-    const dim3 grid((max_len + 127) / 128, a->heads, n_seqs);
+    hk::BertAttnArgs b = *a;
+    b.qblocks = (max_len + 127) / 128;
+    const long groups = (long)b.heads * n_seqs;
+    const long items = (groups + 7) / 8 * 8 * b.qblocks;  // 8 XCDs x ceil(groups / 8) x q-blocks
+    if (items == 0) return HK_OK;
+    if (items > (1L << 30)) return HK_ERR_UNSUPPORTED;
+    const dim3 grid((unsigned)items);
     if (dtype == hk::DT_BF16)
-        hipLaunchKernelGGL(hk::bert::bidir_attn_16<hk::bf16>, grid, dim3(256), hk::bert::LDS16, stream, *a);
+        hipLaunchKernelGGL(hk::bert::bidir_attn_16<hk::bf16>, grid, dim3(256), hk::bert::LDS16, stream, b);
     else
-        hipLaunchKernelGGL(hk::bert::bidir_attn_16<hk::f16>, grid, dim3(256), hk::bert::LDS16, stream, *a);
+        hipLaunchKernelGGL(hk::bert::bidir_attn_16<hk::f16>, grid, dim3(256), hk::bert::LDS16, stream, b);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 

@@ -159,6 +159,7 @@ struct BertAttnArgs {
     int half_window;   // keys with |i - j| <= half_window; < 0: the whole sequence
     float scale_log2;  // softmax scale * log2(e)
     int* fault;
+    int qblocks;  // query blocks per (sequence, head) in the 16-bit grid (set by the launcher)
 };
 
 struct LayerNormArgs {
