@@ -277,14 +277,13 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
         // S^T = K Q^T for this wave's 32 queries: two 32-key halves. Each half then takes its
         // own online-softmax step, so the softmax of half 0 can run while the MFMAs of half 1
         // execute, and the softmax of half 1 while the P.V of half 0 executes.
-        f32x16 s[2];
+        // (the two accumulation chains alternate, so consecutive MFMAs are independent)
+        f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            s[kb] = f32x16{};
+        for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks)
+            for (int kb = 0; kb < 2; ++kb)
                 s[kb] = Mma16<T>::mma(*(const v8*)(Kb + kb * 32 * KV_ROW + koff[ks]), qf[ks], s[kb]);
-        }
         const int n0 = sched_tile(i) * BN;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -336,18 +335,18 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
                     }
                 l_run += l0 + l1;
             }
-            // O^T += V^T P^T: keys kb*32 + g*16 + h*8 + [0..7] of dims db*32 + [0..31]
+            // O^T += V^T P^T: keys kb*32 + g*16 + h*8 + [0..7] of dims db*32 + [0..31] (the four
+            // output blocks alternate, so consecutive MFMAs are independent)
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const T* vb = Vb + vofs[db];
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int db = 0; db < 4; ++db) {
+                    const T* vb = Vb + vofs[db];
                     const i16x4 lo = lds_read_tr16(vb + (kb * 32 + h * 8) * KV_ROW);
                     const i16x4 hi = lds_read_tr16(vb + (kb * 32 + h * 8 + 4) * KV_ROW);
                     const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                     acc_o[db] = Mma16<T>::mma(af, pf[h], acc_o[db]);
                 }
-            }
         }
         if (i + 1 < n_sched) store_tile(buf ^ 1);
         __syncthreads();

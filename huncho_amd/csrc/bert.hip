@@ -124,14 +124,13 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
         if (it + 1 < n_tiles) load_tile(tile + 1);
         const T* Kb = lds + buf * 2 * TILE;
         const T* Vb = Kb + TILE;
-        f32x16 s[2];
+        // (the two accumulation chains alternate, so consecutive MFMAs are independent)
+        f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            s[kb] = f32x16{};
+        for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
+            for (int kb = 0; kb < 2; ++kb)
                 s[kb] = Mma16<T>::mma(*(const v8*)(Kb + kb * 32 * D + kro[ks]), qf[ks], s[kb]);
-        }
         // mask keys past the sequence end or outside this query's window; tiles that lie
         // inside every query's window skip the compare
         const int n0 = tile * BN;
@@ -185,18 +184,18 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
                 pf[kb * 2 + hh] = t;
             }
         l_run += lsum;
+        // (the two output blocks alternate, so consecutive MFMAs are independent)
 #pragma unroll
-        for (int db = 0; db < 2; ++db) {
-            const T* vb = Vb + vro[db];
+        for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
+            for (int db = 0; db < 2; ++db) {
+                const T* vb = Vb + vro[db];
                 const int kb = cc >> 1, hh = cc & 1;
                 const i16x4 lo = lds_read_tr16(vb + (kb * 32 + hh * 8) * D);
                 const i16x4 hi = lds_read_tr16(vb + (kb * 32 + hh * 8 + 4) * D);
                 const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 acc_o[db] = Mma16<T>::mma(af, pf[cc], acc_o[db]);
             }
-        }
         if (it + 1 < n_tiles) store_tile(buf ^ 1);
         __syncthreads();
     }
