@@ -399,16 +399,15 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
         // ---------------- P2: T = (I + A)^-1 in place ----------------
         invert_in_place(Am, Xs, wave, lane);
         // ---------------- P3: delta, O, state ----------------
-        f32x16 dl[2];
+        // (independent accumulation chains alternate in every product below)
+        f32x16 dl[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            dl[tb] = f32x16{};
-            const float* tr = Am + (tb * 32 + col) * AS;
+        for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
+            for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) dl[tb] = Ops<T>::mma(ld_perm_f32<T>(tr, sb * 32, hh, g), Rb[sb][hh], dl[tb]);
-        }
+                for (int tb = 0; tb < 2; ++tb)
+                    dl[tb] = Ops<T>::mma(ld_perm_f32<T>(Am + (tb * 32 + col) * AS, sb * 32, hh, g), Rb[sb][hh], dl[tb]);
         v8 Db[2][2];
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
@@ -417,13 +416,12 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
         }
         T* Os = Qc;  // Q is no longer read in this chunk
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            const T* ar = Aq + (tb * 32 + col) * TS;
+        for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
+            for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) Og[tb] = Ops<T>::mma(ld_perm<T>(ar, sb * 32, hh, g), Db[sb][hh], Og[tb]);
-        }
+                for (int tb = 0; tb < 2; ++tb)
+                    Og[tb] = Ops<T>::mma(ld_perm<T>(Aq + (tb * 32 + col) * TS, sb * 32, hh, g), Db[sb][hh], Og[tb]);
         // every wave finished reading Qc (K S0 / Q S0) before the inversion's barriers
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
@@ -457,20 +455,21 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
                     tofs[x][rb] = rr * DK + 8 * ((4 * rb + 2 * (G & 1) + ((j & 3) >> 1)) ^ sw) + 4 * (j & 1);
                 }
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
                 for (int jj = 0; jj < 16; ++jj) S[rb][jj] *= eglast;
 #pragma unroll
-                for (int tb = 0; tb < 2; ++tb)
+            for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb) {
                         const T* kb = Kc + (tb * 32 + 16 * hh) * DK;
                         const i16x4 lo = lds_read_tr16(kb + tofs[0][rb]);
                         const i16x4 hi = lds_read_tr16(kb + tofs[1][rb]);
                         const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                         S[rb] = Ops<T>::mma(af, Db[tb][hh], S[rb]);
                     }
-            }
         }
         // P4 operands that do not depend on O: the gate norm_w * silu(z) of this thread's rows,
         // computed before the barrier (rows past the end read a clamped row and are not stored)
