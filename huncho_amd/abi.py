@@ -102,6 +102,15 @@ SIGNATURES = {
     "hk_kev_model_destroy": (I, [vp]),
     "hk_kev_workspace_size": (I, [vp, I, I, C.POINTER(SZ)]),
     "hk_kev_forward": (I, [vp, vp, vp, i32p, I, vp, I, I, vp, SZ, vp, vp]),
+    "hk_kev_cache_create": (I, [vp, I, I, C.POINTER(vp)]),
+    "hk_kev_cache_destroy": (I, [vp]),
+    "hk_kev_cache_open": (I, [vp, C.POINTER(C.c_uint64)]),
+    "hk_kev_cache_fork": (I, [vp, C.c_uint64, C.POINTER(C.c_uint64)]),
+    "hk_kev_cache_release": (I, [vp, C.c_uint64]),
+    "hk_kev_cache_tokens": (I, [vp, C.c_uint64, C.POINTER(I)]),
+    "hk_kev_cache_stats": (I, [vp, C.POINTER(I), C.POINTER(I)]),
+    "hk_kev_cache_workspace_size": (I, [vp, I, I, C.POINTER(SZ)]),
+    "hk_kev_forward_cached": (I, [vp, C.POINTER(C.c_uint64), I, vp, vp, i32p, vp, SZ, vp, vp]),
     "hk_layer_norm": (I, [vp, I, vp, L, vp, F, I, I, vp, L]),
     "hk_bidir_attention": (I, [vp, I, vp, L, vp, L, vp, L, vp, I, I, I, I, I, I, F, vp, L]),
     "hk_bert_model_create": (I, [vp, I, C.POINTER(BertConfig), C.POINTER(BertLayerWeights), vp, vp, vp, vp, vp,

@@ -529,11 +529,15 @@ extern "C" int hk_swiglu(hk_ctx* ctx, int dtype, const void* gu, long gu_tok, lo
     return rc ? hk_fail(ctx, rc, "swiglu launch failed") : HK_OK;
 }
 
-extern "C" int hk_gdn_fused(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
-                            const void* conv_hist, void* conv_tail_out, const void* ba, long ba_tok, int b_col,
-                            int a_col, const float* base_g, const float* dt_bias, const void* z, long z_tok,
-                            const float* norm_w, float eps, const int32_t* cu, int n_seqs, int n_tokens, int heads,
-                            int k_heads, const float* initial_state, float* final_state, void* out, long out_tok) {
+// The fused layer with optional per-sequence row tables for the state and the conv history
+// (device arrays of n_seqs pointers; used by the cached model forward).
+int hk_gdn_fused_rows(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
+                      const void* conv_hist, void* conv_tail_out, const void* ba, long ba_tok, int b_col, int a_col,
+                      const float* base_g, const float* dt_bias, const void* z, long z_tok, const float* norm_w,
+                      float eps, const int32_t* cu, int n_seqs, int n_tokens, int heads, int k_heads,
+                      const float* initial_state, float* final_state, void* out, long out_tok,
+                      const float* const* init_rows, float* const* final_rows, const void* const* hist_rows,
+                      void* const* tail_rows) {
     if (!ctx) return HK_ERR_INVALID;
     if (dtype != HK_BF16 && dtype != HK_F16)
         return hk_fail(ctx, HK_ERR_UNSUPPORTED, "fused Gated DeltaNet layer: 16-bit dtypes only (got %d)", dtype);
@@ -550,11 +554,21 @@ extern "C" int hk_gdn_fused(hk_ctx* ctx, int dtype, const void* mixed, long mixe
     REQUIRE(b_col >= 0 && a_col >= 0 && b_col + heads <= ba_tok && a_col + heads <= ba_tok, "b/a columns outside a row");
     hipSetDevice(ctx->device);
     hk::GdnArgs a{nullptr, nullptr, nullptr, 0, 0, 0, heads / k_heads, nullptr, nullptr, 0, cu, initial_state,
-                  final_state, out, out_tok, heads, n_tokens, ctx->fault_dev};
+                  final_state, out, out_tok, heads, n_tokens, ctx->fault_dev, init_rows, final_rows};
     hk::GdnFusedArgs fa{mixed, mixed_tok, conv_w, (int)conv_dim, conv_hist, conv_tail_out, ba, ba_tok, b_col, a_col,
-                        base_g, dt_bias, 1.0f / sqrtf(128.0f), k_heads, z, z_tok, norm_w, eps};
+                        base_g, dt_bias, 1.0f / sqrtf(128.0f), k_heads, z, z_tok, norm_w, eps, hist_rows, tail_rows};
     int rc = hk_launch_gdn_v2(dtype, 1, &a, &fa, n_seqs, ctx->stream);
     return rc ? hk_fail(ctx, rc, "fused Gated DeltaNet launch failed") : HK_OK;
+}
+
+extern "C" int hk_gdn_fused(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
+                            const void* conv_hist, void* conv_tail_out, const void* ba, long ba_tok, int b_col,
+                            int a_col, const float* base_g, const float* dt_bias, const void* z, long z_tok,
+                            const float* norm_w, float eps, const int32_t* cu, int n_seqs, int n_tokens, int heads,
+                            int k_heads, const float* initial_state, float* final_state, void* out, long out_tok) {
+    return hk_gdn_fused_rows(ctx, dtype, mixed, mixed_tok, conv_w, conv_k, conv_hist, conv_tail_out, ba, ba_tok, b_col,
+                             a_col, base_g, dt_bias, z, z_tok, norm_w, eps, cu, n_seqs, n_tokens, heads, k_heads,
+                             initial_state, final_state, out, out_tok, nullptr, nullptr, nullptr, nullptr);
 }
 
 // ---------------------------------------------------------------------------

@@ -203,7 +203,18 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, col = lane & 31;
     const int dvc = wave * 32 + col;
     const int kh = h / a.qk_rep;
-    const long sbase = ((long)seq * H + h) * DK * DV;
+    // this sequence's state rows and conv rows (per-row pointer tables or contiguous arrays)
+    const float* const s0 = a.init_rows ? a.init_rows[seq]
+                                        : (a.initial_state ? a.initial_state + (long)seq * H * DK * DV : nullptr);
+    float* const s1 = a.final_rows ? a.final_rows[seq]
+                                   : (a.final_state ? a.final_state + (long)seq * H * DK * DV : nullptr);
+    const T* const hist = !FUSED ? nullptr
+                          : fa.hist_rows ? (const T*)fa.hist_rows[seq]
+                                         : (fa.hist ? (const T*)fa.hist + (long)seq * fa.conv_dim * 3 : nullptr);
+    T* const tail = !FUSED ? nullptr
+                    : fa.tail_rows ? (T*)fa.tail_rows[seq]
+                                   : (fa.tail_out ? (T*)fa.tail_out + (long)seq * fa.conv_dim * 3 : nullptr);
+    const long sbase = (long)h * DK * DV;
     // loader mapping (waves 0..2): slice = wave (q, k, v); 8 channels 8*sub..; rows 16*rg..
     const int sub = lane & 15, rg = lane >> 4;
 
@@ -212,7 +223,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-            S[rb][j] = a.initial_state ? a.initial_state[sbase + (long)(4 * g) * DV + dvc + (rb * 32 + arow(j)) * DV] : 0.0f;
+            S[rb][j] = s0 ? s0[sbase + (long)(4 * g) * DV + dvc + (rb * 32 + arow(j)) * DV] : 0.0f;
 
     // fused loader: this lane's 8 q channels; k channels follow at + Hk*128, v channels of
     // value head h at + 2 Hk*128 + (h - kh)*128
@@ -256,8 +267,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
                     for (int i = 0; i < 3; ++i)
 #pragma unroll
                         for (int e = 0; e < 8; ++e)
-                            raw[i][e] = fa.hist ? ((const T*)fa.hist)[((long)seq * fa.conv_dim + mc + e) * 3 + i]
-                                                : (T)0.0f;
+                            raw[i][e] = hist ? hist[((long)mc + e) * 3 + i] : (T)0.0f;
                 }
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
@@ -512,13 +522,13 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
             }
         }
     }
-    if (a.final_state) {
+    if (s1) {
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a.final_state[sbase + (long)(4 * g) * DV + dvc + (rb * 32 + arow(j)) * DV] = S[rb][j];
+            for (int j = 0; j < 16; ++j) s1[sbase + (long)(4 * g) * DV + dvc + (rb * 32 + arow(j)) * DV] = S[rb][j];
     }
-    if (FUSED && fa.tail_out && wave < 3 && rg == 0) {
+    if (FUSED && tail && wave < 3 && rg == 0) {
         // cache tail: the last 3 raw conv inputs of [history, sequence]; wave ts writes the
         // channels of q, k or v (16 lanes x 8 channels)
         const long mc = mcol + wave * (long)fa.Hk * 128 + (wave == 2 ? (long)(h - kh) * 128 : 0);
@@ -532,13 +542,12 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
                 v8 x = *(const v8*)((const T*)fa.mixed + (long)(t0 + p) * fa.mixed_tok + mc);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = f(x[e]);
-            } else if (fa.hist) {
+            } else if (hist) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    v[e] = f(((const T*)fa.hist)[((long)seq * fa.conv_dim + mc + e) * 3 + (p + 3)]);
+                for (int e = 0; e < 8; ++e) v[e] = f(hist[((long)mc + e) * 3 + (p + 3)]);
             }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) ((T*)fa.tail_out)[((long)seq * fa.conv_dim + mc + e) * 3 + i] = (T)v[e];
+            for (int e = 0; e < 8; ++e) tail[((long)mc + e) * 3 + i] = (T)v[e];
         }
     }
 }

@@ -44,6 +44,10 @@ struct GdnArgs {
     int H;
     int n_tokens;
     int* fault;
+    // per-sequence state rows [H][dk][dv] (replace initial_state / final_state when set; a
+    // null entry is a zero initial state / no final state)
+    const float* const* init_rows;
+    float* const* final_rows;
 };
 
 // Gated DeltaNet layer body read straight from the fused in_proj output (gdn_v2 FUSED mode).
@@ -65,6 +69,10 @@ struct GdnFusedArgs {
     long z_tok;
     const float* norm_w;   // [128] gated-norm weight
     float eps;
+    // per-sequence conv rows [conv_dim][3] (replace hist / tail_out when set; a null entry is
+    // a zero history / no tail)
+    const void* const* hist_rows;
+    void* const* tail_rows;
 };
 
 struct KvArgs {

@@ -1,0 +1,342 @@
+// kev_cache.cpp - device prefix cache for the Kev model: cached sequences ("handles") that
+// continue with new tokens, fork into private branches and are released.
+//
+// Semantics follow the reference backend (crates/huncho-core/src/backend.rs:333-437,
+// crates/huncho-backend/src/qwen3_5.rs:2655-2757, 2818-2847) and its paged KV cache
+// (qwen3_5/kv_pages.rs:18-98, 307-341):
+//   * a handle holds the K/V of its tokens in fixed-size pages of a shared pool, the Gated
+//     DeltaNet recurrent state of every linear layer and the conv tail (last K-1 raw conv
+//     inputs) of every linear layer;
+//   * fork shares the parent's pages (reference counted) and copies its recurrent state and
+//     conv tails; a page that is full is immutable, so only a shared, partially filled tail
+//     page is copied before a branch appends to it (copy on write);
+//   * a continuation commits only after the whole forward succeeded: new pages are taken
+//     from the free list, the state is written to the handle's second state buffer, and the
+//     token count, page list and active state buffer change only when the call returns OK;
+//   * at most max_handles live handles (the reference allows 64, qwen3_5.rs:3257-3265).
+#include <string.h>
+
+#include <unordered_map>
+#include <vector>
+
+#include "kev_internal.hpp"
+
+namespace {
+
+struct KevHandle {
+    int tokens = 0;
+    std::vector<int> pages;                 // pool pages in sequence order
+    float* state[2] = {nullptr, nullptr};   // [n_gdn][H][128][128] fp32
+    void* conv[2] = {nullptr, nullptr};     // [n_gdn][conv_dim][3], model dtype
+    int cur = 0;                            // buffer holding the committed state
+};
+
+}  // namespace
+
+struct hk_kev_cache {
+    hk_kev_model* m = nullptr;
+    int max_pages = 0, max_handles = 0, P = 0, n_attn = 0, n_gdn = 0, bt_stride = 0;
+    size_t page_bytes = 0;                 // one page of one pool
+    size_t state_layer = 0, conv_layer = 0;  // per layer (bytes) inside a state / conv buffer
+    std::vector<void*> k_pools, v_pools;   // per attention layer [max_pages][Hkv][P][hd]
+    std::vector<int> refs;                 // per page
+    std::vector<int> free_list;
+    std::unordered_map<uint64_t, KevHandle> handles;
+    uint64_t next_id = 1;
+};
+
+static void free_handle_buffers(KevHandle& h) {
+    for (int i = 0; i < 2; ++i) {
+        if (h.state[i]) hipFree(h.state[i]);
+        if (h.conv[i]) hipFree(h.conv[i]);
+        h.state[i] = nullptr;
+        h.conv[i] = nullptr;
+    }
+}
+
+static int alloc_handle_buffers(hk_kev_cache* c, KevHandle& h) {
+    for (int i = 0; i < 2; ++i) {
+        if (hipMalloc((void**)&h.state[i], c->state_layer * c->n_gdn) != hipSuccess ||
+            hipMalloc(&h.conv[i], c->conv_layer * c->n_gdn) != hipSuccess) {
+            free_handle_buffers(h);
+            return hk_fail(c->m->ctx, HK_ERR_NOMEM, "cache handle state allocation failed");
+        }
+    }
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_create(hk_kev_model* m, int max_pages, int max_handles, hk_kev_cache** out) {
+    if (!m || !out) return HK_ERR_INVALID;
+    hk_ctx* ctx = m->ctx;
+    const hk_kev_config& cfg = m->cfg;
+    if (m->dtype == HK_F32 || cfg.conv_k != 4)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "the prefix cache needs a 16-bit model with conv kernel 4");
+    if (max_pages <= 0 || max_handles <= 0 || max_handles > 4096)
+        return hk_fail(ctx, HK_ERR_INVALID, "max_pages %d / max_handles %d out of range", max_pages, max_handles);
+    hk_kev_cache* c = new hk_kev_cache();
+    c->m = m;
+    c->max_pages = max_pages;
+    c->max_handles = max_handles;
+    c->P = cfg.page_size;
+    c->bt_stride = (cfg.max_context + c->P - 1) / c->P;
+    for (int l = 0; l < cfg.n_layers; ++l) (m->layers[l].type == 0 ? c->n_gdn : c->n_attn)++;
+    c->page_bytes = (size_t)cfg.n_kv_heads * c->P * cfg.head_dim * m->esz;
+    c->state_layer = (size_t)cfg.lin_n_v_heads * 128 * 128 * sizeof(float);
+    c->conv_layer = (size_t)m->conv_dim * 3 * m->esz;
+    hipSetDevice(ctx->device);
+    for (int i = 0; i < c->n_attn; ++i) {
+        void *k = nullptr, *v = nullptr;
+        if (hipMalloc(&k, c->page_bytes * max_pages) != hipSuccess ||
+            hipMalloc(&v, c->page_bytes * max_pages) != hipSuccess) {
+            if (k) hipFree(k);
+            for (void* p : c->k_pools) hipFree(p);
+            for (void* p : c->v_pools) hipFree(p);
+            delete c;
+            return hk_fail(ctx, HK_ERR_NOMEM, "page pool allocation failed");
+        }
+        c->k_pools.push_back(k);
+        c->v_pools.push_back(v);
+    }
+    c->refs.assign(max_pages, 0);
+    for (int p = max_pages - 1; p >= 0; --p) c->free_list.push_back(p);
+    *out = c;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_destroy(hk_kev_cache* c) {
+    if (!c) return HK_ERR_INVALID;
+    hipSetDevice(c->m->ctx->device);
+    hipStreamSynchronize(c->m->ctx->stream);
+    for (auto& kv : c->handles) free_handle_buffers(kv.second);
+    for (void* p : c->k_pools) hipFree(p);
+    for (void* p : c->v_pools) hipFree(p);
+    delete c;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_open(hk_kev_cache* c, uint64_t* handle_out) {
+    if (!c || !handle_out) return HK_ERR_INVALID;
+    hk_ctx* ctx = c->m->ctx;
+    if ((int)c->handles.size() >= c->max_handles)
+        return hk_fail(ctx, HK_ERR_NOMEM, "cache holds its maximum of %d live handles", c->max_handles);
+    hipSetDevice(ctx->device);
+    KevHandle h;
+    if (int rc = alloc_handle_buffers(c, h)) return rc;
+    const uint64_t id = c->next_id++;
+    c->handles.emplace(id, std::move(h));
+    *handle_out = id;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_fork(hk_kev_cache* c, uint64_t parent, uint64_t* child_out) {
+    if (!c || !child_out) return HK_ERR_INVALID;
+    hk_ctx* ctx = c->m->ctx;
+    auto it = c->handles.find(parent);
+    if (it == c->handles.end()) return hk_fail(ctx, HK_ERR_INVALID, "unknown cache handle %llu", (unsigned long long)parent);
+    if ((int)c->handles.size() >= c->max_handles)
+        return hk_fail(ctx, HK_ERR_NOMEM, "cache holds its maximum of %d live handles", c->max_handles);
+    hipSetDevice(ctx->device);
+    KevHandle h;
+    if (int rc = alloc_handle_buffers(c, h)) return rc;
+    const KevHandle& p = it->second;
+    h.tokens = p.tokens;
+    h.pages = p.pages;
+    if (p.tokens > 0) {
+        if (hipMemcpyAsync(h.state[0], p.state[p.cur], c->state_layer * c->n_gdn, hipMemcpyDeviceToDevice,
+                           ctx->stream) != hipSuccess ||
+            hipMemcpyAsync(h.conv[0], p.conv[p.cur], c->conv_layer * c->n_gdn, hipMemcpyDeviceToDevice, ctx->stream) !=
+                hipSuccess) {
+            free_handle_buffers(h);
+            return hk_fail(ctx, HK_ERR_DEVICE, "fork state copy failed");
+        }
+    }
+    for (int pg : h.pages) ++c->refs[pg];
+    const uint64_t id = c->next_id++;
+    c->handles.emplace(id, std::move(h));
+    *child_out = id;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_release(hk_kev_cache* c, uint64_t handle) {
+    if (!c) return HK_ERR_INVALID;
+    hk_ctx* ctx = c->m->ctx;
+    auto it = c->handles.find(handle);
+    if (it == c->handles.end()) return hk_fail(ctx, HK_ERR_INVALID, "unknown cache handle %llu", (unsigned long long)handle);
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);  // queued work may still read the pages or the state
+    for (int pg : it->second.pages)
+        if (--c->refs[pg] == 0) c->free_list.push_back(pg);
+    free_handle_buffers(it->second);
+    c->handles.erase(it);
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_tokens(hk_kev_cache* c, uint64_t handle, int* tokens_out) {
+    if (!c || !tokens_out) return HK_ERR_INVALID;
+    auto it = c->handles.find(handle);
+    if (it == c->handles.end())
+        return hk_fail(c->m->ctx, HK_ERR_INVALID, "unknown cache handle %llu", (unsigned long long)handle);
+    *tokens_out = it->second.tokens;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_stats(hk_kev_cache* c, int* live_handles, int* free_pages) {
+    if (!c || !live_handles || !free_pages) return HK_ERR_INVALID;
+    *live_handles = (int)c->handles.size();
+    *free_pages = (int)c->free_list.size();
+    return HK_OK;
+}
+
+// Per-call tables after the model workspace: block tables, context lengths and the Gated
+// DeltaNet row tables (4 per linear layer).
+static size_t table_bytes(const hk_kev_cache* c, int n_seqs) {
+    const size_t bt = (size_t)n_seqs * c->bt_stride * sizeof(int32_t);
+    const size_t lens = (size_t)n_seqs * sizeof(int32_t);
+    const size_t rows = (size_t)c->n_gdn * 4 * n_seqs * sizeof(void*);
+    return ((bt + 255) & ~(size_t)255) + ((lens + 255) & ~(size_t)255) + ((rows + 255) & ~(size_t)255);
+}
+
+extern "C" int hk_kev_cache_workspace_size(hk_kev_cache* c, int n_tokens, int n_seqs, size_t* bytes_out) {
+    if (!c || !bytes_out || n_tokens < 0 || n_seqs <= 0) return HK_ERR_INVALID;
+    *bytes_out = ((kev_workspace_bytes(c->m, n_tokens, n_seqs, 0) + 255) & ~(size_t)255) + table_bytes(c, n_seqs);
+    return HK_OK;
+}
+
+extern "C" int hk_kev_forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids,
+                                     const int32_t* cu_dev, const int32_t* cu_host, void* workspace,
+                                     size_t workspace_bytes, float* logits, void* hidden_last) {
+    if (!c) return HK_ERR_INVALID;
+    hk_kev_model* m = c->m;
+    hk_ctx* ctx = m->ctx;
+    const hk_kev_config& cfg = m->cfg;
+    if (!handles_host || !ids || !cu_dev || !cu_host || !workspace || n_seqs <= 0 || n_seqs > 64)
+        return hk_fail(ctx, HK_ERR_INVALID, "invalid cached forward arguments (1..64 rows)");
+    if (cu_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "cu_seqlens[0] must be 0");
+    // validate every row before any work (qwen3_5.rs:2656-2725)
+    std::vector<KevHandle*> hs(n_seqs);
+    for (int s = 0; s < n_seqs; ++s) {
+        auto it = c->handles.find(handles_host[s]);
+        if (it == c->handles.end())
+            return hk_fail(ctx, HK_ERR_INVALID, "unknown cache handle %llu", (unsigned long long)handles_host[s]);
+        for (int r = 0; r < s; ++r)
+            if (handles_host[r] == handles_host[s]) return hk_fail(ctx, HK_ERR_INVALID, "row %d repeats a handle", s);
+        hs[s] = &it->second;
+        const int len = cu_host[s + 1] - cu_host[s];
+        if (len <= 0) return hk_fail(ctx, HK_ERR_INVALID, "cached continuation requires nonempty tokens (row %d)", s);
+        if (hs[s]->tokens + len > cfg.max_context)
+            return hk_fail(ctx, HK_ERR_INVALID, "sequence length %d exceeds max_context %d", hs[s]->tokens + len,
+                           cfg.max_context);
+    }
+    const int n = cu_host[n_seqs];
+    const size_t model_ws = (kev_workspace_bytes(m, n, n_seqs, 0) + 255) & ~(size_t)255;
+    if (model_ws + table_bytes(c, n_seqs) > workspace_bytes)
+        return hk_fail(ctx, HK_ERR_INVALID, "workspace too small: %zu < %zu", workspace_bytes,
+                       model_ws + table_bytes(c, n_seqs));
+    // page plan: a shared, partially filled tail page is replaced by a private copy; new pages
+    // come from the free list; nothing changes in the cache until the forward succeeded
+    std::vector<std::vector<int>> plan(n_seqs);
+    std::vector<int> cow_src(n_seqs, -1), taken;
+    int need = 0;
+    for (int s = 0; s < n_seqs; ++s) {
+        const KevHandle& h = *hs[s];
+        const int total = h.tokens + (cu_host[s + 1] - cu_host[s]);
+        const bool cow = h.tokens % c->P != 0 && c->refs[h.pages.back()] > 1;
+        need += (total + c->P - 1) / c->P - (int)h.pages.size() + (cow ? 1 : 0);
+    }
+    if (need > (int)c->free_list.size())
+        return hk_fail(ctx, HK_ERR_NOMEM, "page pool exhausted: %d pages needed, %zu free", need, c->free_list.size());
+    hipSetDevice(ctx->device);
+    for (int s = 0; s < n_seqs; ++s) {
+        const KevHandle& h = *hs[s];
+        const int total = h.tokens + (cu_host[s + 1] - cu_host[s]);
+        plan[s] = h.pages;
+        if (h.tokens % c->P != 0 && c->refs[h.pages.back()] > 1) {
+            cow_src[s] = h.pages.back();
+            plan[s].back() = c->free_list.back();
+            c->free_list.pop_back();
+            taken.push_back(plan[s].back());
+        }
+        while ((int)plan[s].size() < (total + c->P - 1) / c->P) {
+            plan[s].push_back(c->free_list.back());
+            c->free_list.pop_back();
+            taken.push_back(plan[s].back());
+        }
+    }
+    auto rollback = [&](int rc) {
+        for (int pg : taken) c->free_list.push_back(pg);
+        return rc;
+    };
+    for (int s = 0; s < n_seqs; ++s) {
+        if (cow_src[s] < 0) continue;
+        // the private copy replaces the handle's last page (new pages may follow it in the plan)
+        const int copy = plan[s][hs[s]->pages.size() - 1];
+        for (int l = 0; l < c->n_attn; ++l) {
+            const size_t src = (size_t)cow_src[s] * c->page_bytes, dst = (size_t)copy * c->page_bytes;
+            if (hipMemcpyAsync((char*)c->k_pools[l] + dst, (char*)c->k_pools[l] + src, c->page_bytes,
+                               hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess ||
+                hipMemcpyAsync((char*)c->v_pools[l] + dst, (char*)c->v_pools[l] + src, c->page_bytes,
+                               hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess)
+                return rollback(hk_fail(ctx, HK_ERR_DEVICE, "copy-on-write page copy failed"));
+        }
+    }
+    // per-call tables: block tables, context lengths, row tables (state in: committed buffer,
+    // or none for an empty handle; state out: the other buffer)
+    std::vector<int32_t> bt((size_t)n_seqs * c->bt_stride, 0), lens(n_seqs);
+    std::vector<const void*> rows((size_t)c->n_gdn * 4 * n_seqs);
+    for (int s = 0; s < n_seqs; ++s) {
+        const KevHandle& h = *hs[s];
+        for (size_t i = 0; i < plan[s].size(); ++i) bt[(size_t)s * c->bt_stride + i] = plan[s][i];
+        lens[s] = h.tokens + (cu_host[s + 1] - cu_host[s]);
+        for (int g = 0; g < c->n_gdn; ++g) {
+            const void** r = rows.data() + (size_t)g * 4 * n_seqs;
+            r[s] = h.tokens > 0 ? (const char*)h.state[h.cur] + g * c->state_layer : nullptr;
+            r[n_seqs + s] = (const char*)h.state[h.cur ^ 1] + g * c->state_layer;
+            r[2 * n_seqs + s] = h.tokens > 0 ? (const char*)h.conv[h.cur] + g * c->conv_layer : nullptr;
+            r[3 * n_seqs + s] = (const char*)h.conv[h.cur ^ 1] + g * c->conv_layer;
+        }
+    }
+    char* tbase = (char*)workspace + model_ws;
+    int32_t* bt_dev = (int32_t*)tbase;
+    int32_t* lens_dev = (int32_t*)(tbase + ((bt.size() * 4 + 255) & ~(size_t)255));
+    const void** rows_dev = (const void**)((char*)lens_dev + ((lens.size() * 4 + 255) & ~(size_t)255));
+    if (hipMemcpyAsync(bt_dev, bt.data(), bt.size() * 4, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipMemcpyAsync(lens_dev, lens.data(), lens.size() * 4, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipMemcpyAsync(rows_dev, rows.data(), rows.size() * sizeof(void*), hipMemcpyHostToDevice, ctx->stream) !=
+            hipSuccess)
+        return rollback(hk_fail(ctx, HK_ERR_DEVICE, "cache table upload failed"));
+    KevCacheView view;
+    view.ctx_lens_dev = lens_dev;
+    view.k_pools = c->k_pools;
+    view.v_pools = c->v_pools;
+    for (int g = 0; g < c->n_gdn; ++g) {
+        const void** r = rows_dev + (size_t)g * 4 * n_seqs;
+        view.init_rows.push_back((const float* const*)r);
+        view.final_rows.push_back((float* const*)(r + n_seqs));
+        view.hist_rows.push_back((const void* const*)(r + 2 * n_seqs));
+        view.tail_rows.push_back((void* const*)(r + 3 * n_seqs));
+    }
+    int rc = kev_forward_impl(m, ids, cu_dev, cu_host, n_seqs, bt_dev, c->bt_stride, c->max_pages, workspace, model_ws,
+                              logits, hidden_last, &view);
+    if (rc) return rollback(rc);
+    // commit only after the forward finished without device faults
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess)
+        return rollback(hk_fail(ctx, HK_ERR_DEVICE, "cached forward failed on the device"));
+    int faults = 0;
+    if (hipMemcpy(&faults, ctx->fault_dev, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+        return rollback(hk_fail(ctx, HK_ERR_DEVICE, "fault word read failed"));
+    if (faults) {
+        const int zero = 0;
+        hipMemcpy(ctx->fault_dev, &zero, sizeof(int), hipMemcpyHostToDevice);
+        return rollback(hk_fail(ctx, HK_ERR_DEVICE, "device faults 0x%x during the cached forward; nothing committed",
+                                faults));
+    }
+    for (int s = 0; s < n_seqs; ++s) {
+        KevHandle& h = *hs[s];
+        if (cow_src[s] >= 0) --c->refs[cow_src[s]];  // still held by the other sharers
+        for (size_t i = h.pages.size() - (cow_src[s] >= 0 ? 1 : 0); i < plan[s].size(); ++i) ++c->refs[plan[s][i]];
+        h.pages = std::move(plan[s]);
+        h.tokens = lens[s];
+        h.cur ^= 1;
+    }
+    return HK_OK;
+}

@@ -1,0 +1,66 @@
+// kev_internal.hpp - the Kev model object and the forward entry shared by kev_model.cpp
+// (fresh batches) and kev_cache.cpp (cached continuation, forks).
+#pragma once
+
+#include <vector>
+
+#include "abi_internal.hpp"
+
+namespace hk_kev {
+
+struct Layer {
+    int type = 0;
+    float *in_norm = nullptr, *post_norm = nullptr;
+    void *w_gu = nullptr, *w_down = nullptr;
+    void *w_in = nullptr, *w_out = nullptr;
+    float *conv_w = nullptr, *norm_w = nullptr, *base_g = nullptr, *dt_bias = nullptr;
+    void *w_qkv = nullptr, *w_o = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr;
+};
+
+}  // namespace hk_kev
+
+struct hk_kev_model {
+    hk_ctx* ctx = nullptr;
+    int dtype = HK_BF16;
+    size_t esz = 2;
+    hk_kev_config cfg{};
+    std::vector<int> layer_types;
+    std::vector<hk_kev::Layer> layers;
+    std::vector<void*> owned;
+    void* embed = nullptr;
+    float* final_norm = nullptr;
+    void* head_w = nullptr;
+    float* head_b = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    // derived sizes
+    int key_dim = 0, value_dim = 0, conv_dim = 0, gdn_rows = 0, attn_rows = 0;
+};
+
+// Per-call view of cached state for a continuation forward (all pointers owned by the cache).
+struct KevCacheView {
+    const int32_t* ctx_lens_dev;         // [n_seqs] cached + new tokens per sequence
+    std::vector<void*> k_pools, v_pools;  // one pool per attention layer, in layer order
+    // one device array of n_seqs pointers per Gated DeltaNet layer, in layer order
+    std::vector<const float* const*> init_rows;
+    std::vector<float* const*> final_rows;
+    std::vector<const void* const*> hist_rows;
+    std::vector<void* const*> tail_rows;
+};
+
+// The scoring forward (fresh batch when view == nullptr). Returns an HK_* status.
+int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev, const int32_t* cu_host, int n_seqs,
+                     const int32_t* bt, int bt_stride, int num_pages, void* workspace, size_t workspace_bytes,
+                     float* logits, void* hidden_last, const KevCacheView* view);
+// Workspace bytes of a forward over n tokens in n_seqs sequences with num_pages workspace pages
+// (0 when the pools belong to a cache).
+size_t kev_workspace_bytes(const hk_kev_model* m, int n, int n_seqs, int num_pages);
+
+// The fused Gated DeltaNet layer with optional per-sequence row tables (abi.cpp).
+int hk_gdn_fused_rows(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
+                      const void* conv_hist, void* conv_tail_out, const void* ba, long ba_tok, int b_col, int a_col,
+                      const float* base_g, const float* dt_bias, const void* z, long z_tok, const float* norm_w,
+                      float eps, const int32_t* cu, int n_seqs, int n_tokens, int heads, int k_heads,
+                      const float* initial_state, float* final_state, void* out, long out_tok,
+                      const float* const* init_rows, float* const* final_rows, const void* const* hist_rows,
+                      void* const* tail_rows);

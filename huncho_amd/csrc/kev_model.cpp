@@ -22,19 +22,11 @@
 
 #include <vector>
 
-#include "abi_internal.hpp"
+#include "kev_internal.hpp"
 
 namespace {
 
-struct Layer {
-    int type = 0;
-    float *in_norm = nullptr, *post_norm = nullptr;
-    void *w_gu = nullptr, *w_down = nullptr;
-    void *w_in = nullptr, *w_out = nullptr;
-    float *conv_w = nullptr, *norm_w = nullptr, *base_g = nullptr, *dt_bias = nullptr;
-    void *w_qkv = nullptr, *w_o = nullptr;
-    float *q_norm = nullptr, *k_norm = nullptr;
-};
+using hk_kev::Layer;
 
 inline float bf16_to_f32(uint16_t b) {
     uint32_t u = (uint32_t)b << 16;
@@ -44,23 +36,6 @@ inline float bf16_to_f32(uint16_t b) {
 }
 
 }  // namespace
-
-struct hk_kev_model {
-    hk_ctx* ctx = nullptr;
-    int dtype = HK_BF16;
-    size_t esz = 2;
-    hk_kev_config cfg{};
-    std::vector<int> layer_types;
-    std::vector<Layer> layers;
-    std::vector<void*> owned;
-    void* embed = nullptr;
-    float* final_norm = nullptr;
-    void* head_w = nullptr;
-    float* head_b = nullptr;
-    float *rope_cos = nullptr, *rope_sin = nullptr;
-    // derived sizes
-    int key_dim = 0, value_dim = 0, conv_dim = 0, gdn_rows = 0, attn_rows = 0;
-};
 
 static int dev_alloc(hk_kev_model* m, size_t bytes, void** out) {
     if (hipMalloc(out, bytes) != hipSuccess) return hk_fail(m->ctx, HK_ERR_NOMEM, "model allocation of %zu bytes failed", bytes);
@@ -95,14 +70,20 @@ static int small_f32(hk_kev_model* m, const void* src, size_t count, float** out
     return upload_f32(m, v, out);
 }
 
-// Stacks row-major [rows_i][in] weights into one [sum rows][in] buffer.
-static int fuse_rows(hk_kev_model* m, std::initializer_list<std::pair<const void*, int>> parts, int in, void** out) {
+// Stacks row-major [rows_i][in] weights into one [sum rows][in] buffer, followed by zero rows
+// up to pad_rows rows when pad_rows is larger.
+static int fuse_rows(hk_kev_model* m, std::initializer_list<std::pair<const void*, int>> parts, int in, void** out,
+                     size_t pad_rows = 0) {
     size_t rows = 0;
     for (auto& p : parts) {
         if (!p.first) return hk_fail(m->ctx, HK_ERR_INVALID, "missing projection weight");
         rows += p.second;
     }
-    if (int rc = dev_alloc(m, rows * in * m->esz, out)) return rc;
+    const size_t total = pad_rows > rows ? pad_rows : rows;
+    if (int rc = dev_alloc(m, total * in * m->esz, out)) return rc;
+    if (total > rows &&
+        hipMemset((char*)*out + rows * in * m->esz, 0, (total - rows) * in * m->esz) != hipSuccess)
+        return hk_fail(m->ctx, HK_ERR_DEVICE, "weight padding failed");
     size_t off = 0;
     for (auto& p : parts) {
         size_t bytes = (size_t)p.second * in * m->esz;
@@ -150,7 +131,8 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
     m->key_dim = c.lin_n_k_heads * c.lin_key_dim;
     m->value_dim = c.lin_n_v_heads * c.lin_v_dim;
     m->conv_dim = 2 * m->key_dim + m->value_dim;
-    m->gdn_rows = m->conv_dim + m->value_dim + 2 * c.lin_n_v_heads;
+    // fused in_proj rows padded to a multiple of 8 (16-byte aligned rows for the fused layer)
+    m->gdn_rows = (m->conv_dim + m->value_dim + 2 * c.lin_n_v_heads + 7) / 8 * 8;
     m->attn_rows = 2 * c.n_heads * c.head_dim + 2 * c.n_kv_heads * c.head_dim;
     const int H = c.hidden, I = c.intermediate;
     int rc = HK_OK;
@@ -172,7 +154,7 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
         if (L.type == 0) {
             const int Hv = c.lin_n_v_heads;
             if ((rc = fuse_rows(m, {{w.in_qkv, m->conv_dim}, {w.in_z, m->value_dim}, {w.in_b, Hv}, {w.in_a, Hv}}, H,
-                                &L.w_in)))
+                                &L.w_in, m->gdn_rows)))
                 return fail(rc);
             if ((rc = fuse_rows(m, {{w.out_proj, H}}, m->value_dim, &L.w_out))) return fail(rc);
             if ((rc = small_f32(m, w.conv_w, (size_t)m->conv_dim * c.conv_k, &L.conv_w, same))) return fail(rc);
@@ -265,6 +247,12 @@ Buffers carve(const hk_kev_model* m, Workspace& ws, int n, int n_seqs, int num_p
 
 }  // namespace
 
+size_t kev_workspace_bytes(const hk_kev_model* m, int n, int n_seqs, int num_pages) {
+    Workspace ws;
+    carve(m, ws, n, n_seqs, num_pages);
+    return ws.off;
+}
+
 extern "C" int hk_kev_workspace_size(hk_kev_model* m, int n_tokens, int n_seqs, size_t* bytes_out) {
     if (!m || !bytes_out || n_tokens < 0 || n_seqs <= 0) return HK_ERR_INVALID;
     // pools sized for every sequence's pages; callers that share pages may pass fewer
@@ -285,6 +273,13 @@ extern "C" int hk_kev_workspace_size(hk_kev_model* m, int n_tokens, int n_seqs, 
 extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev, const int32_t* cu_host,
                               int n_seqs, const int32_t* bt, int bt_stride, int num_pages, void* workspace,
                               size_t workspace_bytes, float* logits, void* hidden_last) {
+    return kev_forward_impl(m, ids, cu_dev, cu_host, n_seqs, bt, bt_stride, num_pages, workspace, workspace_bytes,
+                            logits, hidden_last, nullptr);
+}
+
+int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev, const int32_t* cu_host, int n_seqs,
+                     const int32_t* bt, int bt_stride, int num_pages, void* workspace, size_t workspace_bytes,
+                     float* logits, void* hidden_last, const KevCacheView* view) {
     if (!m) return HK_ERR_INVALID;
     hk_ctx* ctx = m->ctx;
     const hk_kev_config& c = m->cfg;
@@ -297,14 +292,14 @@ extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t
         const int len = cu_host[s + 1] - cu_host[s];
         if (len <= 0) return hk_fail(ctx, HK_ERR_INVALID, "sequence %d is empty", s);
         if (len > c.max_context) return hk_fail(ctx, HK_ERR_INVALID, "sequence length %d exceeds max_context %d", len, c.max_context);
-        if ((len + c.page_size - 1) / c.page_size > bt_stride)
+        if (!view && (len + c.page_size - 1) / c.page_size > bt_stride)
             return hk_fail(ctx, HK_ERR_INVALID, "sequence %d needs more pages than bt_stride", s);
         if (len > max_len) max_len = len;
     }
     const int n = cu_host[n_seqs];
     Workspace ws;
     ws.base = (char*)workspace;
-    Buffers b = carve(m, ws, n, n_seqs, num_pages);
+    Buffers b = carve(m, ws, n, n_seqs, view ? 0 : num_pages);
     if (ws.off > workspace_bytes) return hk_fail(ctx, HK_ERR_INVALID, "workspace too small: %zu < %zu", workspace_bytes, ws.off);
     hipSetDevice(ctx->device);
     const int dt = m->dtype;
@@ -312,7 +307,20 @@ extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t
     const int H = c.hidden, I = c.intermediate, hd = c.head_dim;
     const int Hq = c.n_heads, Hkv = c.n_kv_heads, Hv = c.lin_n_v_heads, Hk = c.lin_n_k_heads;
 
-    RUN(hk_launch_seq_lens(cu_dev, n_seqs, b.ctx_lens, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "seq_lens") : 0);
+    const int32_t* ctx_lens = view ? view->ctx_lens_dev : b.ctx_lens;
+    if (view) {
+        if (dt == HK_F32 || c.conv_k != 4 || m->gdn_rows % 8 != 0)
+            return hk_fail(ctx, HK_ERR_UNSUPPORTED, "cached continuation needs the fused 16-bit Gated DeltaNet path");
+        int n_attn = 0, n_gdn = 0;
+        for (int l = 0; l < c.n_layers; ++l) (m->layers[l].type == 0 ? n_gdn : n_attn)++;
+        if ((int)view->k_pools.size() != n_attn || (int)view->v_pools.size() != n_attn ||
+            (int)view->init_rows.size() != n_gdn || (int)view->final_rows.size() != n_gdn ||
+            (int)view->hist_rows.size() != n_gdn || (int)view->tail_rows.size() != n_gdn)
+            return hk_fail(ctx, HK_ERR_INVALID, "cache view does not match the model's layers");
+    } else {
+        RUN(hk_launch_seq_lens(cu_dev, n_seqs, b.ctx_lens, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "seq_lens") : 0);
+    }
+    int ai = 0, gi = 0;  // attention / Gated DeltaNet layer ordinals
     RUN(hk_launch_embed(dt, ids, n, m->embed, c.vocab, H, b.x, ctx->fault_dev, ctx->stream)
             ? hk_fail(ctx, HK_ERR_DEVICE, "embed launch")
             : 0);
@@ -325,9 +333,11 @@ extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t
             const int b_col = m->conv_dim + m->value_dim, a_col = b_col + Hv;
             if (dt != HK_F32 && c.conv_k == 4 && rows % 8 == 0) {
                 // one kernel: conv + SiLU + l2norm + beta/g + chunked delta rule + gated RMSNorm
-                RUN(hk_gdn_fused(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, nullptr, b.big, rows, b_col, a_col,
-                                 L.base_g, L.dt_bias, (char*)b.big + (size_t)m->conv_dim * e, rows, L.norm_w, c.eps,
-                                 cu_dev, n_seqs, n, Hv, Hk, nullptr, nullptr, b.o, (long)Hv * 128));
+                RUN(hk_gdn_fused_rows(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, nullptr, b.big, rows, b_col,
+                                      a_col, L.base_g, L.dt_bias, (char*)b.big + (size_t)m->conv_dim * e, rows, L.norm_w,
+                                      c.eps, cu_dev, n_seqs, n, Hv, Hk, nullptr, nullptr, b.o, (long)Hv * 128,
+                                      view ? view->init_rows[gi] : nullptr, view ? view->final_rows[gi] : nullptr,
+                                      view ? view->hist_rows[gi] : nullptr, view ? view->tail_rows[gi] : nullptr));
             } else {
                 RUN(hk_gdn_prep(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, b.big, rows, b_col, a_col, L.base_g,
                                 L.dt_bias, cu_dev, n_seqs, n, Hv, Hk, b.q, b.k, b.v, b.g, b.beta, nullptr));
@@ -339,18 +349,22 @@ extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t
             }
             RUN(hk_gemm_xwt(ctx, dt, n, H, m->value_dim, b.o, m->value_dim, L.w_out, m->value_dim, b.x, H, b.x, H, 1.0f,
                             1.0f));
+            ++gi;
         } else {
+            void* k_pool = view ? view->k_pools[ai] : b.k_pool;
+            void* v_pool = view ? view->v_pools[ai] : b.v_pool;
+            ++ai;
             const int rows = m->attn_rows;
             RUN(hk_gemm_xwt(ctx, dt, n, rows, H, b.h, H, L.w_qkv, H, b.big, rows, nullptr, 0, 1.0f, 0.0f));
             char* qg = (char*)b.big;
             char* kin = qg + (size_t)2 * Hq * hd * e;
             char* vin = kin + (size_t)Hkv * hd * e;
             RUN(hk_qk_norm_rope_kv_write(ctx, dt, qg, rows, 2 * hd, kin, rows, vin, rows, L.q_norm, L.k_norm, c.eps,
-                                         m->rope_cos, m->rope_sin, c.rotary_dim, c.max_context, cu_dev, b.ctx_lens,
+                                         m->rope_cos, m->rope_sin, c.rotary_dim, c.max_context, cu_dev, ctx_lens,
                                          n_seqs, n, bt, bt_stride, num_pages, c.page_size, Hq, Hkv, hd, qg, rows,
-                                         2 * hd, b.k_pool, b.v_pool));
-            RUN(hk_paged_prefill_attention(ctx, dt, qg, rows, 2 * hd, b.k_pool, b.v_pool, num_pages, c.page_size, bt,
-                                           bt_stride, cu_dev, b.ctx_lens, n_seqs, n, max_len, Hq, Hkv, hd,
+                                         2 * hd, k_pool, v_pool));
+            RUN(hk_paged_prefill_attention(ctx, dt, qg, rows, 2 * hd, k_pool, v_pool, num_pages, c.page_size, bt,
+                                           bt_stride, cu_dev, ctx_lens, n_seqs, n, max_len, Hq, Hkv, hd,
                                            (float)(1.0 / sqrt((double)hd)), qg + (size_t)hd * e, rows, 2 * hd, b.o,
                                            (long)Hq * hd, hd));
             RUN(hk_gemm_xwt(ctx, dt, n, H, Hq * hd, b.o, Hq * hd, L.w_o, Hq * hd, b.x, H, b.x, H, 1.0f, 1.0f));

@@ -11,6 +11,7 @@ hk_calibrate). All numerics run in the C ABI; this module moves bytes and holds 
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 
@@ -160,6 +161,8 @@ class KevModel:
         self._ws_key = None
 
     def close(self):
+        for cache in list(getattr(self, "_caches", ())):  # caches use the model: close them first
+            cache.close()
         if getattr(self, "h", None):
             abi.lib().hk_kev_model_destroy(self.h)
             self.h = None
@@ -234,4 +237,114 @@ class KevModel:
         if faults:
             raise abi.HkError(abi.HK_ERR_INVALID, f"device fault flags {faults:#x}")
         probs = np.stack([abi.calibrate(row, temperature) for row in logits])
+        return logits, probs
+
+
+class KevCache:
+    """Device prefix cache of a KevModel (hk_kev_cache): the Backend trait's cache surface
+    (crates/huncho-core/src/backend.rs:333-437) for Qwen3_5Backend (qwen3_5.rs:2655-2757,
+    2780-2847). Handles are opaque integers. `continue_rows` is `forward` with `fork_from`:
+    the handles' state commits only when the call succeeds; `fork_batch` is
+    `forward_fork_batch`: private branches of one parent, released afterwards."""
+
+    def __init__(self, model: KevModel, max_pages: int, max_handles: int = 64):
+        self.model = model
+        self.ctx = model.ctx
+        h = C.c_void_p()
+        self.ctx.check(abi.lib().hk_kev_cache_create(model.h, max_pages, max_handles, C.byref(h)))
+        self.h = h
+        self._ws = None
+        if not hasattr(model, "_caches"):
+            model._caches = weakref.WeakSet()
+        model._caches.add(self)
+
+    def close(self):
+        if getattr(self, "h", None):
+            abi.lib().hk_kev_cache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def open(self) -> int:
+        out = C.c_uint64()
+        self.ctx.check(abi.lib().hk_kev_cache_open(self.h, C.byref(out)))
+        return out.value
+
+    def fork(self, parent: int) -> int:
+        out = C.c_uint64()
+        self.ctx.check(abi.lib().hk_kev_cache_fork(self.h, parent, C.byref(out)))
+        return out.value
+
+    def release(self, handle: int) -> None:
+        self.ctx.check(abi.lib().hk_kev_cache_release(self.h, handle))
+
+    def tokens(self, handle: int) -> int:
+        out = C.c_int()
+        self.ctx.check(abi.lib().hk_kev_cache_tokens(self.h, handle, C.byref(out)))
+        return out.value
+
+    def stats(self):
+        live, free = C.c_int(), C.c_int()
+        self.ctx.check(abi.lib().hk_kev_cache_stats(self.h, C.byref(live), C.byref(free)))
+        return live.value, free.value
+
+    def _workspace(self, n_tokens: int, n_seqs: int) -> torch.Tensor:
+        sz = C.c_size_t()
+        self.ctx.check(abi.lib().hk_kev_cache_workspace_size(self.h, n_tokens, n_seqs, C.byref(sz)))
+        if self._ws is None or self._ws.numel() < sz.value:
+            self._ws = torch.empty(sz.value, dtype=torch.uint8, device=self.model.device)
+        return self._ws
+
+    def continue_rows(self, handles, rows, temperature: float = 1.0, want_hidden: bool = False):
+        """Appends rows[i] to handles[i] (distinct handles, nonempty rows) and returns the decision
+        logits of each row's last token, calibrated probabilities and (optionally) the final-normed
+        last-token hidden rows."""
+        if not 1 <= len(rows) <= MAX_ROWS or len(handles) != len(rows):
+            raise ValueError(f"1..{MAX_ROWS} rows, one handle each")
+        flat = np.concatenate([np.asarray(r, np.int64) for r in rows])
+        if flat.size and (flat.min() < 0 or flat.max() >= self.model.shape.vocab):
+            raise ValueError("token id outside the vocabulary")
+        lengths = [len(r) for r in rows]
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        n, dev = int(cu[-1]), self.model.device
+        ids = torch.from_numpy(flat.astype(np.int32)).to(dev)
+        cu_dev = torch.from_numpy(cu).to(dev)
+        ws = self._workspace(n, len(rows))
+        logits = torch.empty((len(rows), max(self.model.shape.n_out, 1)), dtype=torch.float32, device=dev)
+        hidden = torch.empty((len(rows), self.model.shape.hidden), dtype=self.model.dtype, device=dev) if want_hidden else None
+        hs = (C.c_uint64 * len(handles))(*handles)
+        self.ctx.check(abi.lib().hk_kev_forward_cached(
+            self.h, hs, len(rows), ids.data_ptr(), cu_dev.data_ptr(), cu.ctypes.data_as(C.POINTER(C.c_int32)),
+            ws.data_ptr(), ws.numel(), logits.data_ptr(), hidden.data_ptr() if hidden is not None else None))
+        out = logits.cpu().numpy()[:, : self.model.shape.n_out]
+        probs = np.stack([abi.calibrate(r, temperature) for r in out]) if self.model.shape.n_out else None
+        return out, probs, (hidden.float().cpu().numpy() if hidden is not None else None)
+
+    def prefill(self, tokens) -> int:
+        """A new handle holding `tokens` (Backend::prefill)."""
+        h = self.open()
+        try:
+            self.continue_rows([h], [tokens])
+        except Exception:
+            self.release(h)
+            raise
+        return h
+
+    def fork_batch(self, parent: int, suffixes, temperature: float = 1.0):
+        """forward_fork_batch: one private branch of `parent` per suffix, evaluated together; the
+        parent is left unchanged and every branch is released, on success or failure."""
+        if not 1 <= len(suffixes) <= MAX_ROWS - 1:
+            raise ValueError(f"1..{MAX_ROWS - 1} suffix rows")
+        branches = []
+        try:
+            for _ in suffixes:
+                branches.append(self.fork(parent))
+            logits, probs, _ = self.continue_rows(branches, suffixes, temperature)
+        finally:
+            for b in branches:
+                self.release(b)
         return logits, probs

@@ -235,6 +235,39 @@ int hk_kev_forward(hk_kev_model* m, const int32_t* ids_dev, const int32_t* cu_se
                    int num_pages, void* workspace_dev, size_t workspace_bytes, float* logits_dev,
                    void* hidden_last_dev);
 
+/* ---- prefix cache: cached sequences that continue, fork and are released (the Backend trait's
+ * cache surface, crates/huncho-core/src/backend.rs:333-437: prefill / fork / release_cache;
+ * crates/huncho-backend/src/qwen3_5.rs:2655-2757 forward with fork_from, 2818-2847; pages and
+ * copy-on-write tails as qwen3_5/kv_pages.rs:18-98, 307-341). A handle holds its tokens' K/V in
+ * pages of a pool shared by all handles (reference counted), plus the recurrent state and conv
+ * tail of every Gated DeltaNet layer. Handles are process-unique, never reused (lib.rs:64-76).
+ * 16-bit models only. Calls on one cache are not thread-safe (the engine serialises them). --- */
+typedef struct hk_kev_cache hk_kev_cache;
+/* Pools of max_pages pages (page_size tokens of every KV head of every attention layer) and at
+ * most max_handles live handles (the reference: 64). */
+int hk_kev_cache_create(hk_kev_model* m, int max_pages, int max_handles, hk_kev_cache** out);
+int hk_kev_cache_destroy(hk_kev_cache* c);
+/* A new empty handle (zero tokens, zero state). */
+int hk_kev_cache_open(hk_kev_cache* c, uint64_t* handle_out);
+/* A private branch of `parent`: shares its pages, copies its recurrent state and conv tails.
+ * Later continuations of either never change the other (a shared partial page is copied
+ * before it is appended to). */
+int hk_kev_cache_fork(hk_kev_cache* c, uint64_t parent, uint64_t* child_out);
+/* Frees the handle's state; its pages return to the pool when no other handle holds them. */
+int hk_kev_cache_release(hk_kev_cache* c, uint64_t handle);
+int hk_kev_cache_tokens(hk_kev_cache* c, uint64_t handle, int* tokens_out);
+int hk_kev_cache_stats(hk_kev_cache* c, int* live_handles, int* free_pages);
+int hk_kev_cache_workspace_size(hk_kev_cache* c, int n_tokens, int n_seqs, size_t* bytes_out);
+/* Continues up to 64 distinct handles with their new tokens (row s: ids[cu[s] .. cu[s+1]),
+ * nonempty, appended after the handle's cached tokens) and writes each row's decision logits
+ * (and, if hidden_last_dev != NULL, final-normed last-token hidden rows) as hk_kev_forward does.
+ * Synchronises the context's stream: the handles' tokens, pages and state change only when the
+ * call returns HK_OK (device faults included: nothing is committed). HK_ERR_NOMEM when the pool
+ * has too few free pages. */
+int hk_kev_forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids_dev,
+                          const int32_t* cu_seqlens_dev, const int32_t* cu_seqlens_host, void* workspace_dev,
+                          size_t workspace_bytes, float* logits_dev, void* hidden_last_dev);
+
 /* ---- ModernBERT encoder (the Laya backend: candle ModernBert, crates/huncho-backend/src/
  * candle.rs:65-117 load, 319-416 forward; config normalisation 157-203) ----------------------
  * LayerNorm without bias: y = (x - mean) / sqrt(var + eps) * w, w fp32 [width], width <= 2048. */
