@@ -137,13 +137,16 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
         const bool inside = n0 + BN - 1 < L && (w < 0 || (n0 >= blk_hi - w && n0 + BN - 1 <= blk_lo + w));
         float mloc = -INFINITY;
         if (!inside) {
+            // visible keys of this query: [lo, hi] (the window clipped to the sequence), as
+            // offsets kb * 32 + jj from this lane's first key n0 + 16 g; one unsigned compare each
+            const int lo = (w < 0 ? 0 : max(0, p - w)) - n0 - g * 16;
+            const int hi = (w < 0 ? L - 1 : min(L - 1, p + w)) - n0 - g * 16;
+            const unsigned span = (unsigned)(hi - lo);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int jj = 0; jj < 16; ++jj) {
-                    const int key = n0 + kb * 32 + g * 16 + jj;
-                    const int dist = key > p ? key - p : p - key;
-                    if (key >= L || (w >= 0 && dist > w)) s[kb][jj] = -INFINITY;
+                    if ((unsigned)(kb * 32 + jj - lo) > span) s[kb][jj] = -INFINITY;
                     mloc = fmaxf(mloc, s[kb][jj]);
                 }
         } else {
@@ -168,7 +171,6 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
         // a query whose keys so far were all masked still has m_use = -inf: its scores are
         // all -inf and exp2 gives 0 with any finite offset
         const float mc = m_use == -INFINITY ? 0.0f : m_use * c;
-        float lsum = 0.0f;
         v8 pf[4];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -176,13 +178,24 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
             for (int hh = 0; hh < 2; ++hh) {
                 v8 t;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const float e = fast_exp2(fmaf(s[kb][hh * 8 + k], c, -mc));
-                    lsum += e;
-                    t[k] = (T)e;
-                }
+                for (int k = 0; k < 8; ++k) t[k] = (T)fast_exp2(fmaf(s[kb][hh * 8 + k], c, -mc));
                 pf[kb * 2 + hh] = t;
             }
+        // row sums of the rounded probabilities that P.V consumes (v_dot2 against ones)
+        float lsum;
+        {
+            typedef typename Mma16<T>::v2 v2;
+            const v2 one2 = {(T)1.0f, (T)1.0f};
+            float l0 = 0.0f, l1 = 0.0f;
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+                for (int q = 0; q < 8; q += 4) {
+                    l0 = dot2(v2{pf[cc][q], pf[cc][q + 1]}, one2, l0);
+                    l1 = dot2(v2{pf[cc][q + 2], pf[cc][q + 3]}, one2, l1);
+                }
+            lsum = l0 + l1;
+        }
         l_run += lsum;
         // (the two output blocks alternate, so consecutive MFMAs are independent)
 #pragma unroll
