@@ -358,11 +358,21 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk(GdnArgs a, GdnFusedArgs fa) 
             const float* bt = Bs + t4;
             float* am = Am + t4 * AS + s;
             T* aq = Aq + t4 * TS + s;
+            // G and beta of this lane's 16 rows (runs of 4 at t4 + 8 i), read before the masks
+            // so the selects below compile without branches
+            f32x4 gq[4], bq[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                gq[i] = *(const f32x4*)(gt + 8 * i);
+                bq[i] = *(const f32x4*)(bt + 8 * i);
+            }
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const int t = t4 + arow(j);
-                const float dec = s <= t ? __expf(gt[arow(j)] - gs) : 0.0f;
-                am[arow(j) * AS] = s < t ? bt[arow(j)] * dec * kk[j] : 0.0f;
+                // exp(G_t - G_s) may overflow above the diagonal; the selects drop it there
+                const float ex = __expf(gq[j >> 2][j & 3] - gs);
+                const float dec = s <= t ? ex : 0.0f;
+                am[arow(j) * AS] = s < t ? bq[j >> 2][j & 3] * dec * kk[j] : 0.0f;
                 aq[arow(j) * TS] = (T)(dec * qk[j]);
             }
         } else {
