@@ -430,7 +430,7 @@ def run_kev(args, dtype):
                      "frac": round(attn_achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": traffic_of("attention"),
                      "us_per_launch": round(a["seconds"] * 1e6, 2), "flops_per_launch": a["flops"],
                      "hbm_frac": round(a["bytes"] / a["seconds"] / HBM_PEAK, 4)},
-        "roofline_delta_rule": {"kernel": "gdn_chunk", "bound": "hbm", "achieved": round(gdn_achieved, 1),
+        "roofline_delta_rule": {"kernel": "gdn_chunk16", "bound": "hbm", "achieved": round(gdn_achieved, 1),
                                 "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                                 "frac": round(gd["bytes"] / gd["seconds"] / HBM_PEAK, 4),
                                 "traffic": traffic_of("delta_rule"),

@@ -557,7 +557,7 @@ int hk_gdn_fused_rows(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok,
                   final_state, out, out_tok, heads, n_tokens, ctx->fault_dev, init_rows, final_rows};
     hk::GdnFusedArgs fa{mixed, mixed_tok, conv_w, (int)conv_dim, conv_hist, conv_tail_out, ba, ba_tok, b_col, a_col,
                         base_g, dt_bias, 1.0f / sqrtf(128.0f), k_heads, z, z_tok, norm_w, eps, hist_rows, tail_rows};
-    int rc = hk_launch_gdn_v2(dtype, 1, &a, &fa, n_seqs, ctx->stream);
+    int rc = hk_launch_gdn16(dtype, 1, &a, &fa, n_seqs, ctx->stream);
     return rc ? hk_fail(ctx, rc, "fused Gated DeltaNet launch failed") : HK_OK;
 }
 

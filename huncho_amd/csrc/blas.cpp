@@ -5,8 +5,8 @@
 // activations. bf16 or fp16 operands with fp32 accumulation (HIPBLAS_COMPUTE_32F), or fp32.
 // Plans (descriptors + the fastest algorithm for the shape) are cached per shape. On first
 // use of a shape every solution hipBLASLt offers for the layout (the heuristic's list plus
-// the full solution list, filtered by matmulIsAlgoSupported) is timed once, and the best 8
-// again over 3 launches. The workspace is owned by the context and allocated on the first
+// the full solution list, filtered by matmulIsAlgoSupported) is timed, and the best 8 again
+// in interleaved rounds. The workspace is owned by the context and allocated on the first
 // GEMM.
 #include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
@@ -109,45 +109,50 @@ static std::vector<std::pair<hipblasLtMatmulAlgo_t, size_t>> candidates(hk_ctx* 
     return out;
 }
 
-// Times the candidates (beta = 0 into a scratch output, so the caller's buffers are
-// untouched): one launch each, then the best 8 over 3 launches. Returns the index of the
-// fastest; 0 if timing fails.
+// Times the candidates into a scratch output (the caller's buffers are untouched; with a C
+// operand the scratch serves as C too, so the timed kernel reads C as the real call does):
+// every candidate over 2 launches, then the best 8 in 3 interleaved rounds of 5 launches,
+// keeping each one's fastest round. Returns the index of the fastest; 0 if timing fails.
 static int pick_fastest(hk_ctx* ctx, Plan& p, std::vector<std::pair<hipblasLtMatmulAlgo_t, size_t>>& cands, int dtype,
-                        int n, const void* x, const void* w, long ldy) {
+                        int n, const void* x, const void* w, long ldy, long ldc, bool has_c) {
     if (cands.size() <= 1) return 0;
     hk_blas* B = ctx->blas;
     void* scratch = nullptr;
-    const size_t bytes = (size_t)ldy * n * (dtype == HK_F32 ? 4 : 2);
+    const size_t bytes = (size_t)std::max(ldy, ldc) * n * (dtype == HK_F32 ? 4 : 2);
     if (hipMalloc(&scratch, bytes) != hipSuccess) return 0;
     hipEvent_t e0, e1;
     hipEventCreate(&e0);
     hipEventCreate(&e1);
-    const float one = 1.0f, zero = 0.0f;
+    const float one = 1.0f, beta = has_c ? 1.0f : 0.0f;
+    auto launch = [&](int i) {
+        return hipblasLtMatmul(B->handle, p.desc, &one, w, p.a, x, p.b, &beta, scratch, p.c, scratch, p.d,
+                               &cands[i].first, B->workspace, cands[i].second, ctx->stream) == HIPBLAS_STATUS_SUCCESS;
+    };
     auto time_algo = [&](int i, int reps) -> float {
-        bool ok = hipblasLtMatmul(B->handle, p.desc, &one, w, p.a, x, p.b, &zero, scratch, p.d, scratch, p.d,
-                                  &cands[i].first, B->workspace, cands[i].second, ctx->stream) == HIPBLAS_STATUS_SUCCESS;
+        bool ok = launch(i);
         hipEventRecord(e0, ctx->stream);
-        for (int r = 0; ok && r < reps; ++r)
-            ok = hipblasLtMatmul(B->handle, p.desc, &one, w, p.a, x, p.b, &zero, scratch, p.d, scratch, p.d,
-                                 &cands[i].first, B->workspace, cands[i].second, ctx->stream) == HIPBLAS_STATUS_SUCCESS;
+        for (int r = 0; ok && r < reps; ++r) ok = launch(i);
         hipEventRecord(e1, ctx->stream);
         float ms = 0.0f;
         if (!ok || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1e30f;
         return ms / reps;
     };
+    time_algo(0, 2);  // clocks up before the first measurement
     std::vector<std::pair<float, int>> t1;
-    for (int i = 0; i < (int)cands.size(); ++i) t1.emplace_back(time_algo(i, 1), i);
+    for (int i = 0; i < (int)cands.size(); ++i) t1.emplace_back(time_algo(i, 2), i);
     std::sort(t1.begin(), t1.end());
+    int top = 0;
+    while (top < (int)t1.size() && top < 8 && t1[top].first < 1e29f) ++top;
+    std::vector<float> t2(top, 1e30f);
+    for (int round = 0; round < 3; ++round)
+        for (int k = 0; k < top; ++k) t2[k] = std::min(t2[k], time_algo(t1[k].second, 5));
     int best = t1[0].second;
     float best_ms = 1e30f;
-    for (int k = 0; k < (int)t1.size() && k < 8; ++k) {
-        if (t1[k].first >= 1e29f) break;
-        const float ms = time_algo(t1[k].second, 3);
-        if (ms < best_ms) {
-            best_ms = ms;
+    for (int k = 0; k < top; ++k)
+        if (t2[k] < best_ms) {
+            best_ms = t2[k];
             best = t1[k].second;
         }
-    }
     hipStreamSynchronize(ctx->stream);
     (void)hipGetLastError();
     hipEventDestroy(e0);
@@ -208,7 +213,7 @@ int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, l
             hipblasLtMatmulDescDestroy(p.desc);
             return hk_fail(ctx, HK_ERR_UNSUPPORTED, "no usable hipBLASLt algorithm for %dx%dx%d", out, n, in);
         }
-        const int best = pick_fastest(ctx, p, cands, dtype, n, x, w, ldy);
+        const int best = pick_fastest(ctx, p, cands, dtype, n, x, w, ldy, ldc, has_c);
         p.algo = cands[best].first;
         p.ws = cands[best].second;
         it = B->plans.emplace(key, p).first;

@@ -22,7 +22,7 @@
 // instead of transposing the data. Inputs stream from HBM once: q, k, v, g, beta in, o out.
 //
 // This file holds the fp32 variant (v_mfma_f32_32x32x2_f32, the fp32 model path); the 16-bit
-// variants and the fused Gated DeltaNet layer kernel live in gdn_v2.hip.
+// variants and the fused Gated DeltaNet layer kernel live in gdn16.hip.
 #include "common.hpp"
 #include "kernel_args.hpp"
 
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_f32(GdnArgs a) {
 }  // namespace hk
 
 extern "C" int hk_launch_gated_delta_chunked(int dtype, const hk::GdnArgs* args, int n_seqs, hipStream_t stream) {
-    if (dtype != hk::DT_F32) return hk_launch_gdn_v2(dtype, 0, args, nullptr, n_seqs, stream);
+    if (dtype != hk::DT_F32) return hk_launch_gdn16(dtype, 0, args, nullptr, n_seqs, stream);
     dim3 grid(args->H, n_seqs);
     static bool configured = false;
     if (!configured) {

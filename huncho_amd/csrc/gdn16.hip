@@ -1,0 +1,594 @@
+// gdn16.hip - chunked gated delta rule for 16-bit activations (bf16 / fp16) on gfx950, with
+// an optional fused Gated DeltaNet prologue and epilogue.
+//
+// Recurrence (crates/huncho-backend/src/delta_cpu.rs:95-131, qwen3_5.rs:950-987), per token t:
+//   S <- S exp(g_t); delta_t = beta_t (v_t - S^T k_t); S <- S + k_t delta_t^T; o_t = S^T q_t
+// evaluated in the equal chunked form (chunk 64, G = inclusive cumsum of g in the chunk):
+//   A = strict_lower(beta_t exp(G_t - G_s) k_t.k_s),  T = (I + A)^-1
+//   delta = T [beta (V - exp(G) K S0)],  O = exp(G) Q S0 + lower(exp(G_t - G_s) q_t.k_s) delta
+//   S1 = exp(G_last) S0 + K^T [exp(G_last - G) delta]
+// Only decay ratios exp(G_t - G_s) with t >= s (each <= 1) are used.
+//
+// Two modes (template FUSED):
+//   standalone  q, k [tokens][k_heads][128], v [tokens][heads][128], g, beta fp32 -> o
+//   fused       the Gated DeltaNet layer body of LinearAttn::forward (qwen3_5.rs:846-940)
+//               straight from the fused in_proj output rows [q | k | v | z | b | a]:
+//               causal depthwise conv (K = 4, ascending taps, conv_cpu.rs:34-48) + SiLU,
+//               l2norm of q and k, q * 128^-1/2, beta = sigmoid(b),
+//               g = -exp(A_log) softplus(a + dt_bias), the recurrence, then the gated
+//               RMSNorm rms(o) * w * silu(z) (193-201) -> out_proj input
+// so one kernel streams each layer's q|k|v|z|b|a once and writes one output row per token.
+//
+// Work split: one workgroup of 8 waves per (sequence, value head), two workgroups per CU
+// (79,360 B of LDS each, <= 128 registers per lane), so 4 waves share each SIMD. Wave w owns
+// value columns 16w..16w+15 of the fp32 state S [128 x 128], held for the whole sequence in
+// eight 16x16 MFMA accumulators (v_mfma_f32_16x16x32_{bf16,f16}; lane l: column l % 16,
+// rows 4 (l / 16) + r). Intermediates (K S, R, delta) stay in accumulator layout and feed the
+// next product as its B operand: each product's reduction index is permuted to the
+// accumulator's row order (element e of lane group q <-> index 32 s + 4 q + e, or
+// 32 s + 16 + 4 q + e - 4 for e >= 4), and the A operands are read from LDS in that order.
+//
+// Chunk pipeline:
+//   P0  global -> LDS: q, k, v rows (fused: waves 0-5 run the conv and l2norm); wave 7:
+//       g scan and beta
+//   P1  16x16 tiles of K K^T and Q K^T -> A (fp32, masked, decayed) and Aqk (16-bit);
+//       every wave: K S0, Q S0 for its columns -> R = beta (V - e^G K S0), e^G Q S0
+//   P2  the four 16x16 diagonal blocks of T = (I + A)^-1 in place (waves 0-3)
+//   P3  delta = T R by block forward substitution, O = e^G Q S0 + Aqk delta (staged in LDS
+//       over V), S update with the K^T operand read through transposing LDS reads
+//   P4  O (or the gated-normed O) -> HBM with 16-byte stores
+#include "common.hpp"
+#include "kernel_args.hpp"
+
+namespace hk {
+namespace gdn16 {
+
+template <typename T> struct M16;
+template <> struct M16<bf16> {
+    typedef bf16x8 v8;
+    typedef bf16x4 v4;
+    typedef bf16x2 v2;
+    static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 mma16(v4 a, v4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c,
+                                                         0, 0, 0);
+    }
+};
+template <> struct M16<f16> {
+    typedef f16x8 v8;
+    typedef f16x4 v4;
+    typedef f16x2 v2;
+    static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 mma16(v4 a, v4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <typename T> __device__ __forceinline__ float f(T x) { return (float)x; }
+template <typename T> __device__ __forceinline__ float rnd(float x) { return (float)(T)x; }
+
+constexpr int CH = 64, DK = 128, DV = 128, NTHREADS = 256;
+constexpr int RS = DK + 8;  // row stride (elements) of the Q / K / V tiles [64][136]
+constexpr int AS = CH + 4;  // fp32 row stride of A / T [64][68]
+constexpr int TS = CH + 8;  // row stride of Aqk [64][72]
+// Q, K, V [64][136] each, A, Aqk, g scan, beta: 79,360 B (two workgroups fit a CU's 160 KiB)
+constexpr size_t LDS_BYTES = 3 * CH * RS * 2 + CH * AS * 4 + CH * TS * 2 + 2 * CH * 4;
+
+// Element offset of column x of row r in a Q / K / V tile. The 16-byte row padding moves each
+// row 4 banks on, so 16-byte reads of 16 consecutive rows are conflict-free; and every
+// unrolled access is one per-lane base plus an instruction offset.
+__device__ __forceinline__ int el(int r, int x) { return r * RS + x; }
+
+__device__ __forceinline__ float silu(float x) { return fast_silu(x); }
+
+__device__ __forceinline__ float wave_incl_scan(float x, int lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        float y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
+// In place, the inverses T_bb = (I + A_bb)^-1 of the four 16x16 diagonal blocks of the
+// strictly lower A [64][AS], by forward substitution on waves 0-3 (wave w: block w, lane j:
+// column j). The strictly lower part of each solved block keeps its zeros above the diagonal.
+// Kept out of line: inlined, its unrolled row loads would be hoisted together and spill the
+// caller.
+__device__ __attribute__((noinline)) void solve_diagonal_blocks(float* Am, int wave, int lane) {
+    if (wave >= 4) return;
+    const int b = wave * 16, j = lane & 15;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float* row = Am + (b + i) * AS + b;
+        float a0 = (i == j) ? 1.0f : 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+        for (int k = 0; k + 3 < i; k += 4) {
+            f32x4 rv = *(const f32x4*)(row + k);
+            a0 -= rv[0] * x[k];
+            a1 -= rv[1] * x[k + 1];
+            a2 -= rv[2] * x[k + 2];
+            a3 -= rv[3] * x[k + 3];
+        }
+#pragma unroll
+        for (int k = i & ~3; k < i; ++k) a0 -= row[k] * x[k];
+        x[i] = (a0 + a1) + (a2 + a3);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) Am[(b + i) * AS + b + j] = x[i];
+    }
+}
+
+// Two runs of four 16-bit elements of a Q / K row: columns x0 .. x0 + 3 and x0 + 16 .. + 19
+// (the permuted reduction order of one 32-wide k-step).
+template <typename T>
+__device__ __forceinline__ typename M16<T>::v8 ld_pair(const T* tile, int r, int x0) {
+    typedef typename M16<T>::v4 v4;
+    const v4 lo = *(const v4*)(tile + el(r, x0));
+    const v4 hi = *(const v4*)(tile + el(r, x0 + 16));
+    return typename M16<T>::v8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+// The same two runs from a plain row-major row (Aqk)
+template <typename T>
+__device__ __forceinline__ typename M16<T>::v8 ld_pair_plain(const T* row, int x0) {
+    typedef typename M16<T>::v4 v4;
+    const v4 lo = *(const v4*)(row + x0);
+    const v4 hi = *(const v4*)(row + x0 + 16);
+    return typename M16<T>::v8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+// Accumulator tiles a (elements 0-3) and b (4-7) as one 16-bit B operand
+template <typename T>
+__device__ __forceinline__ typename M16<T>::v8 pack2(f32x4 a, f32x4 b) {
+    return typename M16<T>::v8{(T)a[0], (T)a[1], (T)a[2], (T)a[3], (T)b[0], (T)b[1], (T)b[2], (T)b[3]};
+}
+template <typename T>
+__device__ __forceinline__ typename M16<T>::v4 pack1(f32x4 a) {
+    return typename M16<T>::v4{(T)a[0], (T)a[1], (T)a[2], (T)a[3]};
+}
+// Four fp32 elements of A / T (row r, columns c .. c + 3) as a 16-bit operand, optionally negated
+template <typename T, bool NEG>
+__device__ __forceinline__ typename M16<T>::v4 ld_a4(const float* Am, int r, int c) {
+    const f32x4 x = *(const f32x4*)(Am + r * AS + c);
+    return NEG ? typename M16<T>::v4{(T)-x[0], (T)-x[1], (T)-x[2], (T)-x[3]}
+               : typename M16<T>::v4{(T)x[0], (T)x[1], (T)x[2], (T)x[3]};
+}
+
+template <typename T, bool FUSED>
+__global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa) {
+    typedef typename M16<T>::v8 v8;
+    typedef typename M16<T>::v4 v4;
+    typedef typename M16<T>::v2 v2;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    T* Qs = (T*)smem;                     // [64][RS]
+    T* Ks = Qs + CH * RS;                 // [64][RS]
+    T* Vs = Ks + CH * RS;                 // [64][RS]; O staging in P3
+    float* Am = (float*)(Vs + CH * RS);   // [64][AS]: A, then the diagonal blocks of T
+    T* Aq = (T*)(Am + CH * AS);           // [64][TS]
+    float* Gs = (float*)(Aq + CH * TS);
+    float* Bs = Gs + CH;
+
+    const int h = blockIdx.x, seq = blockIdx.y, H = a.H;
+    const int t0 = a.cu_seqlens[seq];
+    const int Tn = a.cu_seqlens[seq + 1] - t0;
+    if (t0 < 0 || Tn < 0 || t0 + Tn > a.n_tokens) {
+        if (threadIdx.x == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kh = h / a.qk_rep;
+    // this sequence's state rows and conv rows (per-row pointer tables or contiguous arrays)
+    const float* const s0 = a.init_rows ? a.init_rows[seq]
+                                        : (a.initial_state ? a.initial_state + (long)seq * H * DK * DV : nullptr);
+    float* const s1 = a.final_rows ? a.final_rows[seq]
+                                   : (a.final_state ? a.final_state + (long)seq * H * DK * DV : nullptr);
+    const T* const hist = !FUSED ? nullptr
+                          : fa.hist_rows ? (const T*)fa.hist_rows[seq]
+                                         : (fa.hist ? (const T*)fa.hist + (long)seq * fa.conv_dim * 3 : nullptr);
+    T* const tail = !FUSED ? nullptr
+                    : fa.tail_rows ? (T*)fa.tail_rows[seq]
+                                   : (fa.tail_out ? (T*)fa.tail_out + (long)seq * fa.conv_dim * 3 : nullptr);
+    const long sbase = (long)h * DK * DV;
+
+    // state: column tile cw (value columns 32 wave + 16 cw + l % 16), row tile rb (dk rows
+    // 16 rb + 4 (l / 16) + r)
+    f32x4 S[2][8];
+    if (s0) {
+        const float* sp = s0 + sbase + (long)(4 * (lane >> 4)) * DV + 32 * wave + (lane & 15);
+#pragma unroll
+        for (int cw = 0; cw < 2; ++cw)
+#pragma unroll
+            for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) S[cw][rb][r] = sp[(16 * rb + r) * DV + 16 * cw];
+    } else {
+#pragma unroll
+        for (int cw = 0; cw < 2; ++cw)
+#pragma unroll
+            for (int rb = 0; rb < 8; ++rb) S[cw][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // fused conv lanes (waves 0-2): tensor wave (q, k, v), chunk rows 16 q4 + 8 hf .. + 7,
+    // channels 8 j .. + 7 of the head; mixed column mcol + 8 j
+    const long mcol = (long)kh * 128 + wave * (long)fa.Hk * 128 + (wave == 2 ? (long)(h - kh) * 128 : 0);
+
+    for (int c0 = 0; c0 < Tn; c0 += CH) {
+        const int Lc = min(CH, Tn - c0);
+        // lane indices re-formed every chunk, so the compiler builds the per-lane LDS
+        // addresses here instead of holding dozens of them across the loop
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int q4 = ln >> 4, j = ln & 15;
+        const long mc = mcol + 8 * j;
+        __syncthreads();
+        // ---------------- P0: inputs -> LDS ----------------
+        if (FUSED) {
+            if (wave < 3) {
+                // 8 conv outputs per pass from an 11-row window of raw conv inputs (sequence
+                // positions c0 + r0 - 3 ..). Positions past the sequence end are loaded clamped:
+                // they only reach rows past the end, whose beta is 0 and whose outputs are not
+                // stored. Positions before the start are the conv history or 0.
+                T* dst = wave == 0 ? Qs : wave == 1 ? Ks : Vs;
+                // taps (0, 1) and (2, 3) of each channel as 16-bit pairs (the weights are the
+                // model dtype's values, exact in T)
+                v2 w01[8], w23[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const f32x4 w4 = *(const f32x4*)(fa.conv_w + (mc + e) * 4);
+                    w01[e] = v2{(T)w4[0], (T)w4[1]};
+                    w23[e] = v2{(T)w4[2], (T)w4[3]};
+                }
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const int r0 = 16 * q4 + 8 * hf;
+                    v8 raw[11];
+#pragma unroll
+                    for (int i = 0; i < 11; ++i) {
+                        const int p = c0 + r0 - 3 + i;
+                        const int pc = p < 0 ? 0 : (p >= Tn ? Tn - 1 : p);
+                        raw[i] = *(const v8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + mc);
+                    }
+                    if (c0 + r0 == 0) {  // window starts 3 positions before the sequence
+                        if (hist) {
+                            const T* hb = hist + mc * 3;
+#pragma unroll
+                            for (int i = 0; i < 3; ++i)
+#pragma unroll
+                                for (int e = 0; e < 8; ++e) raw[i][e] = hb[e * 3 + i];
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 3; ++i) raw[i] = v8{};
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        float y[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const float acc = dot2(w23[e], v2{raw[i + 2][e], raw[i + 3][e]},
+                                                   dot2(w01[e], v2{raw[i][e], raw[i + 1][e]}, 0.0f));
+                            y[e] = silu(acc);
+                        }
+                        if (wave < 2) {  // conv output stored in the activation dtype, then l2norm
+                                         // over the head's 128 channels (16 lanes)
+                            float ss = 0.0f;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {
+                                y[e] = rnd<T>(y[e]);
+                                ss += y[e] * y[e];
+                            }
+                            ss = sum16(ss);
+                            const float inv = fast_rsqrt(ss + 1e-6f);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) y[e] = wave == 0 ? (y[e] * inv) * fa.scale : y[e] * inv;
+                        }
+                        v8 o;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) o[e] = (T)y[e];
+                        *(v8*)(dst + el(r0 + i, 8 * j)) = o;
+                    }
+                }
+            }
+        } else {
+            // 3 tensors x 64 rows x 16 chunks = 12 chunks per lane; 16 lanes per row
+            v8 x[12];
+#pragma unroll
+            for (int i = 0; i < 12; ++i) {
+                const int tsr = i >> 2, r = 16 * (i & 3) + (tid >> 4);
+                const T* src = tsr == 0 ? (const T*)a.q + (long)kh * DK
+                             : tsr == 1 ? (const T*)a.k + (long)kh * DK : (const T*)a.v + (long)h * DV;
+                const long tok = tsr == 0 ? a.q_tok : tsr == 1 ? a.k_tok : a.v_tok;
+                x[i] = *(const v8*)(src + (long)(t0 + c0 + (r < Lc ? r : Lc - 1)) * tok + 8 * j);
+                if (r >= Lc) x[i] = v8{};
+            }
+#pragma unroll
+            for (int i = 0; i < 12; ++i) {
+                const int tsr = i >> 2, r = 16 * (i & 3) + (tid >> 4);
+                T* dst = tsr == 0 ? Qs : tsr == 1 ? Ks : Vs;
+                *(v8*)(dst + el(r, 8 * j)) = x[i];
+            }
+        }
+        if (wave == 3) {  // g (inclusive scan over the chunk) and beta
+            float gv = 0.0f, bv = 0.0f;
+            if (lane < Lc) {
+                const long tt = t0 + c0 + lane;
+                if (FUSED) {
+                    const T* row = (const T*)fa.ba + tt * fa.ba_tok;
+                    const float b = f(row[fa.b_col + h]);
+                    const float av = f(row[fa.a_col + h]);
+                    bv = rnd<T>(fast_sigmoid(b));
+                    gv = fa.base_g[h] * __logf(__expf(av + fa.dt_bias[h]) + 1.0f);
+                } else {
+                    gv = a.g[tt * a.gb_tok + h];
+                    bv = a.beta[tt * a.gb_tok + h];
+                }
+            }
+            Gs[lane] = wave_incl_scan(gv, lane);
+            Bs[lane] = bv;
+        }
+        __syncthreads();
+        // ---------------- P1: A, Aqk tiles; K S0, Q S0 ----------------
+        // lower tile pairs p = (ti, si), si <= ti: wave w takes pairs w, w + 4, w + 8; upper tiles
+        // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3) of A and Aqk are zeroed, wave w taking w and w + 4
+        for (int p = wave; p < 10; p += 4) {
+            const int ti = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
+            const int si = p - (ti * (ti + 1)) / 2;
+            f32x4 kk = f32x4{0.f, 0.f, 0.f, 0.f}, qk = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const v8 b = *(const v8*)(Ks + el(16 * si + j, 32 * ks + 8 * q4));
+                kk = M16<T>::mma(*(const v8*)(Ks + el(16 * ti + j, 32 * ks + 8 * q4)), b, kk);
+                qk = M16<T>::mma(*(const v8*)(Qs + el(16 * ti + j, 32 * ks + 8 * q4)), b, qk);
+            }
+            const int s = 16 * si + j, t4 = 16 * ti + 4 * q4;
+            const float gs = Gs[s];
+            const f32x4 gt = *(const f32x4*)(Gs + t4);
+            const f32x4 bt = *(const f32x4*)(Bs + t4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = t4 + r;
+                // exp(G_t - G_s) may overflow above the diagonal; the selects drop it there
+                const float ex = __expf(gt[r] - gs);
+                const float dec = s <= t ? ex : 0.0f;
+                Am[t * AS + s] = s < t ? bt[r] * dec * kk[r] : 0.0f;
+                Aq[t * TS + s] = (T)(dec * qk[r]);
+            }
+        }
+        for (int u = wave; u < 6; u += 4) {
+            const int ti = u < 3 ? 0 : u < 5 ? 1 : 2;
+            const int si = u < 3 ? u + 1 : u < 5 ? u - 1 : 3;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * ti + 4 * q4 + r, s = 16 * si + j;
+                Am[t * AS + s] = 0.0f;
+                Aq[t * TS + s] = (T)0.0f;
+            }
+        }
+        // per token tile tt and column tile cw: R = beta (V - e^G K S0), Og = e^G Q S0
+        f32x4 R[2][4], Og[2][4];
+        {
+            v8 Sb[2][4];  // S as the B operand of K S0 / Q S0 (k-step s: dk 32 s ..)
+#pragma unroll
+            for (int cw = 0; cw < 2; ++cw)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) Sb[cw][s] = pack2<T>(S[cw][2 * s], S[cw][2 * s + 1]);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                f32x4 ksa[2], qsa[2];
+#pragma unroll
+                for (int cw = 0; cw < 2; ++cw) ksa[cw] = qsa[cw] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const v8 kop = ld_pair<T>(Ks, 16 * tt + j, 32 * s + 4 * q4);
+                    const v8 qop = ld_pair<T>(Qs, 16 * tt + j, 32 * s + 4 * q4);
+#pragma unroll
+                    for (int cw = 0; cw < 2; ++cw) {
+                        ksa[cw] = M16<T>::mma(kop, Sb[cw][s], ksa[cw]);
+                        qsa[cw] = M16<T>::mma(qop, Sb[cw][s], qsa[cw]);
+                    }
+                }
+                const f32x4 gt = *(const f32x4*)(Gs + 16 * tt + 4 * q4);
+                const f32x4 bt = *(const f32x4*)(Bs + 16 * tt + 4 * q4);
+#pragma unroll
+                for (int cw = 0; cw < 2; ++cw) {
+                    // V[16 tt + 4 q4 + r][32 wave + 16 cw + j] through a transposing read: source
+                    // lane j addresses row 16 tt + 4 q4 + j / 4, columns 32 wave + 16 cw + 4 (j % 4) ..
+                    const i16x4 vr =
+                        lds_read_tr16(Vs + el(16 * tt + 4 * q4 + (j >> 2), 32 * wave + 16 * cw + 4 * (j & 3)));
+                    const v4 vv = __builtin_bit_cast(v4, vr);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float eg = __expf(gt[r]);
+                        // R rounded to the activation dtype: it is a 16-bit MFMA operand
+                        R[cw][tt][r] = rnd<T>(bt[r] * (f(vv[r]) - eg * ksa[cw][r]));
+                        Og[cw][tt][r] = eg * qsa[cw][r];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // ---------------- P2: diagonal blocks of T = (I + A)^-1 ----------------
+        solve_diagonal_blocks(Am, wave, lane);
+        __syncthreads();
+        // ---------------- P3: delta, O, state ----------------
+        // delta = T R by block forward substitution over 16-token blocks (T_ii solved above,
+        // A_ij the strictly lower blocks): delta_i = T_ii (R_i - sum_{j<i} A_ij delta_j); and
+        // O_i = e^G Q S0 + sum_{j<=i} Aqk_ij delta_j, on 16x16x16 products whose B operand is a
+        // delta tile in its accumulator layout
+        f32x4 dl[2][4];
+        v4 dbk[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f32x4 x[2] = {R[0][i], R[1][i]};
+#pragma unroll
+            for (int jj = 0; jj < i; ++jj) {
+                const v4 na = ld_a4<T, true>(Am, 16 * i + j, 16 * jj + 4 * q4);
+#pragma unroll
+                for (int cw = 0; cw < 2; ++cw) x[cw] = M16<T>::mma16(na, dbk[cw][jj], x[cw]);
+            }
+            const v4 ti_ = ld_a4<T, false>(Am, 16 * i + j, 16 * i + 4 * q4);
+#pragma unroll
+            for (int cw = 0; cw < 2; ++cw) {
+                dl[cw][i] = M16<T>::mma16(ti_, pack1<T>(x[cw]), f32x4{0.f, 0.f, 0.f, 0.f});
+                dbk[cw][i] = pack1<T>(dl[cw][i]);
+            }
+#pragma unroll
+            for (int jj = 0; jj <= i; ++jj) {
+                const v4 aq = *(const v4*)(Aq + (16 * i + j) * TS + 16 * jj + 4 * q4);
+#pragma unroll
+                for (int cw = 0; cw < 2; ++cw) Og[cw][i] = M16<T>::mma16(aq, dbk[cw][jj], Og[cw][i]);
+            }
+        }
+        // O staged over V (dead since P1)
+        T* Os = Vs;
+#pragma unroll
+        for (int cw = 0; cw < 2; ++cw)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) Os[el(16 * tt + 4 * q4 + r, 32 * wave + 16 * cw + j)] = (T)Og[cw][tt][r];
+        const float glast = Gs[CH - 1];
+        const float eglast = __expf(glast);
+        v8 Db[2][2];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const f32x4 gt = *(const f32x4*)(Gs + 16 * tt + 4 * q4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float d = __expf(glast - gt[r]);
+                dl[0][tt][r] *= d;
+                dl[1][tt][r] *= d;
+            }
+        }
+#pragma unroll
+        for (int cw = 0; cw < 2; ++cw) {
+            Db[cw][0] = pack2<T>(dl[cw][0], dl[cw][1]);
+            Db[cw][1] = pack2<T>(dl[cw][2], dl[cw][3]);
+        }
+        // S = e^{G_last} S + K^T (e^{G_last - G} delta). The A operand K^T[dk][token] comes
+        // from transposing reads: source lane j addresses K row 32 ks + 4 q4 + j / 4 (+ 16
+        // for elements 4-7), columns 16 rb + 4 (j % 4) .. + 3
+#pragma unroll
+        for (int cw = 0; cw < 2; ++cw)
+#pragma unroll
+            for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) S[cw][rb][r] *= eglast;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int rb = 0; rb < 8; ++rb) {
+                const int kr = 32 * ks + 4 * q4 + (j >> 2);
+                const i16x4 lo = lds_read_tr16(Ks + el(kr, 16 * rb + 4 * (j & 3)));
+                const i16x4 hi = lds_read_tr16(Ks + el(kr + 16, 16 * rb + 4 * (j & 3)));
+                const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+                for (int cw = 0; cw < 2; ++cw) S[cw][rb] = M16<T>::mma(af, Db[cw][ks], S[cw][rb]);
+            }
+        // P4 operands that do not depend on O: the gate norm_w * silu(z) of this thread's rows,
+        // computed before the barrier (rows past the end read a clamped row and are not stored)
+        const int rsub = tid & 15, rrow = tid >> 4;  // 16 lanes per row, 16 rows per pass
+        float gz[4][8];
+        if (FUSED) {
+            v8 zv[4];
+#pragma unroll
+            for (int pass = 0; pass < 4; ++pass) {
+                const long tt = t0 + c0 + min(pass * 16 + rrow, Lc - 1);
+                zv[pass] = *(const v8*)((const T*)fa.z + tt * fa.z_tok + (long)h * DV + 8 * rsub);
+            }
+#pragma unroll
+            for (int pass = 0; pass < 4; ++pass)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) gz[pass][e] = fa.norm_w[8 * rsub + e] * silu(f(zv[pass][e]));
+        }
+        __syncthreads();
+        // ---------------- P4: O -> HBM (gated RMSNorm when fused) ----------------
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int r = pass * 16 + rrow;
+            const v8 ov = *(const v8*)(Os + el(r, 8 * rsub));
+            const long tt = t0 + c0 + r;
+            if (FUSED) {
+                float x[8], ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    x[e] = f(ov[e]);
+                    ss += x[e] * x[e];
+                }
+                ss = sum16(ss);
+                const float inv = fast_rsqrt(ss * (1.0f / 128.0f) + fa.eps);
+                v8 y;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) y[e] = (T)((x[e] * inv) * gz[pass][e]);
+                if (r < Lc) *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
+            } else if (r < Lc) {
+                *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = ov;
+            }
+        }
+    }
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    if (s1) {
+        float* sp = s1 + sbase + (long)(4 * (ln >> 4)) * DV + 32 * wave + (ln & 15);
+#pragma unroll
+        for (int cw = 0; cw < 2; ++cw)
+#pragma unroll
+            for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sp[(16 * rb + r) * DV + 16 * cw] = S[cw][rb][r];
+    }
+    const long mc = mcol + 8 * (ln & 15);
+    if (FUSED && tail && wave < 3 && (ln >> 4) == 0) {
+        // cache tail: the last 3 raw conv inputs of [history, sequence]; wave ts writes the
+        // channels of q, k or v (16 lanes x 8 channels)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int p = Tn - 3 + i;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+            if (p >= 0) {
+                v8 x = *(const v8*)((const T*)fa.mixed + (long)(t0 + p) * fa.mixed_tok + mc);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = f(x[e]);
+            } else if (hist) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = f(hist[((long)mc + e) * 3 + (p + 3)]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) tail[((long)mc + e) * 3 + i] = (T)v[e];
+        }
+    }
+}
+
+}  // namespace gdn16
+}  // namespace hk
+
+template <typename T, bool FUSED>
+static int launch16(const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs, hipStream_t stream) {
+    static bool configured = false;
+    auto kern = hk::gdn16::gdn_chunk16<T, FUSED>;
+    if (!configured) {
+        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)hk::gdn16::LDS_BYTES) != hipSuccess)
+            return HK_ERR_DEVICE;
+        configured = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(a->H, n_seqs), dim3(hk::gdn16::NTHREADS), hk::gdn16::LDS_BYTES, stream, *a, *fa);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+// dtype16: 1 = bf16, 2 = fp16
+extern "C" int hk_launch_gdn16(int dtype16, int fused, const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs,
+                               hipStream_t stream) {
+    hk::GdnFusedArgs none{};
+    if (!fa) fa = &none;
+    if (dtype16 == 1)
+        return fused ? launch16<hk::bf16, true>(a, fa, n_seqs, stream) : launch16<hk::bf16, false>(a, fa, n_seqs, stream);
+    return fused ? launch16<hk::f16, true>(a, fa, n_seqs, stream) : launch16<hk::f16, false>(a, fa, n_seqs, stream);
+}

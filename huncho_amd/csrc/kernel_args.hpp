@@ -50,7 +50,7 @@ struct GdnArgs {
     float* const* final_rows;
 };
 
-// Gated DeltaNet layer body read straight from the fused in_proj output (gdn_v2 FUSED mode).
+// Gated DeltaNet layer body read straight from the fused in_proj output (gdn16 FUSED mode).
 struct GdnFusedArgs {
     const void* mixed;     // token rows [q(Hk*128) | k(Hk*128) | v(H*128) | ...]
     long mixed_tok;
@@ -218,8 +218,8 @@ extern "C" {
 int hk_launch_paged_prefill_attention(int dtype, const hk::AttnArgs* args, int n_seqs, int n_qblocks,
                                       hipStream_t stream);
 int hk_launch_gated_delta_chunked(int dtype, const hk::GdnArgs* args, int n_seqs, hipStream_t stream);
-int hk_launch_gdn_v2(int dtype16, int fused, const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs,
-                     hipStream_t stream);
+int hk_launch_gdn16(int dtype16, int fused, const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs,
+                    hipStream_t stream);
 int hk_launch_qk_norm_rope_kv_write(int dtype, const hk::KvArgs* args, hipStream_t stream);
 int hk_launch_gdn_prep(int dtype, const hk::PrepArgs* a, void* tail_out, hipStream_t st);
 int hk_launch_rms_norm(int dtype, const hk::NormArgs* a, hipStream_t st);
