@@ -127,21 +127,35 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_write(KvArgs a) {
     }
 }
 
-// 16-bit fast path: a workgroup of (Hq + Hkv) x 16 lanes takes TOK_PER_WG consecutive tokens,
-// one 16-lane group per head row (the Hq query heads, then the Hkv key heads with their value
-// rows), 8 consecutive elements per lane (16-byte accesses). The sequence of the workgroup's
-// first token is found once (uniform, scalar loads) and advanced token by token. RoPE partners
-// e +- rd/2 live in lane sub +- rd/16 of the same group, element i. Requires rd % 16 == 0.
-constexpr int TOK_PER_WG = 1;
+// 16-bit fast path: one workgroup of (Hq + Hkv) x 16 lanes per token, one 16-lane group per
+// head row (the Hq query heads, then the Hkv key heads with their value rows), 8 consecutive
+// elements per lane (16-byte accesses). RoPE partners e +- rd/2 live in lane sub +- rd/16 of
+// the same group, element i. Requires rd % 16 == 0.
+// Latency chain: the token's q / k / v rows are loaded first (their addresses depend only on
+// the token), while cu_seqlens and context_lens are staged in LDS to find the sequence and
+// position; then the cos / sin rows and the page (which need the position); then the stores.
 constexpr int CU_LDS = 1024;  // sequences whose lengths are staged in LDS
 
 template <typename T>
 __global__ __launch_bounds__(1024) void qk_norm_rope_kv_write_vec(KvArgs a) {
     typedef T v8 __attribute__((ext_vector_type(8)));
     const int r = threadIdx.x >> 4, sub = threadIdx.x & 15, lane = threadIdx.x & 63, gbase = lane & ~15;
-    const int t0 = blockIdx.x * TOK_PER_WG;
-    // cu_seqlens and context_lens staged in LDS by one coalesced load each, so the sequence
-    // search and the per-token lookups are LDS reads, not chains of dependent global loads
+    const int t = blockIdx.x;
+    const bool is_q = r < a.q_heads;
+    const int h = is_q ? r : r - a.q_heads;
+    // 1. the token's rows and the norm weights
+    const T* src = is_q ? (const T*)a.q_in + (long)t * a.q_in_tok + (long)h * a.q_in_head
+                        : (const T*)a.k_in + (long)t * a.k_in_tok + (long)h * HD;
+    const v8 xr = *(const v8*)(src + sub * 8);
+    const v8 vr = is_q ? v8{} : *(const v8*)((const T*)a.v_in + (long)t * a.v_in_tok + (long)h * HD + sub * 8);
+    const float* w = is_q ? a.q_norm : a.k_norm;
+    f32x4 w0 = f32x4{}, w1 = f32x4{};
+    if (w) {
+        w0 = *(const f32x4*)(w + sub * 8);
+        w1 = *(const f32x4*)(w + sub * 8 + 4);
+    }
+    // 2. sequence and position: cu_seqlens and context_lens staged in LDS by one coalesced
+    //    load each, so the search and the lookups are LDS reads
     __shared__ int cu_s[CU_LDS + 1], ctx_s[CU_LDS];
     const bool staged = a.n_seqs <= CU_LDS;
     if (staged) {
@@ -153,109 +167,80 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_kv_write_vec(KvArgs a) {
     }
     const int* cu = staged ? cu_s : a.cu_seqlens_q;
     const int* ctxl = staged ? ctx_s : a.context_lens;
-    int s = find_seq(cu, a.n_seqs, t0);
-    const bool is_q = r < a.q_heads;
-    const int h = is_q ? r : r - a.q_heads;
-    const float* w = is_q ? a.q_norm : a.k_norm;
+    const int s = find_seq(cu, a.n_seqs, t);
+    const int q0 = cu[s], q_len = cu[s + 1] - q0;
+    const int pos = ctxl[s] - q_len + (t - q0);
+    if (pos < 0 || t - q0 >= q_len) {  // uniform across the workgroup
+        if (threadIdx.x == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    if (a.rope_cos && pos >= a.rope_max_pos) {
+        if (threadIdx.x == 0) atomicOr(a.fault, 4);
+        return;
+    }
+    // 3. cos / sin rows and the page
     const int half = a.rd >> 1, hl = half >> 3;  // RoPE partner lane offset
     const bool rot = sub * 8 < a.rd, first = sub * 8 < half;
     const int psub = rot ? (first ? sub + hl : sub - hl) : sub;
     const int fi0 = first ? sub * 8 : sub * 8 - half;
-    // 1. every load of the workgroup's tokens first (q rows are rewritten in place, so loads
-    //    placed after an earlier token's stores would wait for them)
-    int pos_k[TOK_PER_WG], seq_k[TOK_PER_WG];
-    v8 xr[TOK_PER_WG], vr[TOK_PER_WG];
-    f32x4 cr[TOK_PER_WG][2], sr[TOK_PER_WG][2];
-#pragma unroll
-    for (int k = 0; k < TOK_PER_WG; ++k) {
-        const int t = t0 + k;
-        pos_k[k] = -1;
-        seq_k[k] = s;
-        xr[k] = v8{};
-        vr[k] = v8{};
-        if (t >= a.n_tokens) continue;
-        while (s + 1 < a.n_seqs && cu[s + 1] <= t) ++s;
-        seq_k[k] = s;
-        const int q0 = cu[s], q_len = cu[s + 1] - q0;
-        const int pos = ctxl[s] - q_len + (t - q0);
-        if (pos < 0 || t - q0 >= q_len) {
-            if (threadIdx.x == 0) atomicOr(a.fault, 1);
-            continue;
-        }
-        if (a.rope_cos && pos >= a.rope_max_pos) {
-            if (threadIdx.x == 0) atomicOr(a.fault, 4);
-            continue;
-        }
-        pos_k[k] = pos;
-        const T* src = is_q ? (const T*)a.q_in + (long)t * a.q_in_tok + (long)h * a.q_in_head
-                            : (const T*)a.k_in + (long)t * a.k_in_tok + (long)h * HD;
-        xr[k] = *(const v8*)(src + sub * 8);
-        if (!is_q) vr[k] = *(const v8*)((const T*)a.v_in + (long)t * a.v_in_tok + (long)h * HD + sub * 8);
-        if (a.rope_cos && rot) {
-            const float* cs = a.rope_cos + (long)pos * half + fi0;
-            const float* sn = a.rope_sin + (long)pos * half + fi0;
-            cr[k][0] = *(const f32x4*)cs;
-            cr[k][1] = *(const f32x4*)(cs + 4);
-            sr[k][0] = *(const f32x4*)sn;
-            sr[k][1] = *(const f32x4*)(sn + 4);
-        }
+    f32x4 cr[2], sr[2];
+    if (a.rope_cos && rot) {
+        const float* cs = a.rope_cos + (long)pos * half + fi0;
+        const float* sn = a.rope_sin + (long)pos * half + fi0;
+        cr[0] = *(const f32x4*)cs;
+        cr[1] = *(const f32x4*)(cs + 4);
+        sr[0] = *(const f32x4*)sn;
+        sr[1] = *(const f32x4*)(sn + 4);
     }
-    f32x4 w0 = f32x4{}, w1 = f32x4{};
-    if (w) {
-        w0 = *(const f32x4*)(w + sub * 8);
-        w1 = *(const f32x4*)(w + sub * 8 + 4);
-    }
-    // 2. norm, RoPE and stores
-#pragma unroll
-    for (int k = 0; k < TOK_PER_WG; ++k) {
-        const int t = t0 + k, pos = pos_k[k];
-        if (pos < 0) continue;  // uniform: past the batch or a faulted token
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = to_f(xr[k][e]);
-        if (w) {  // shuffles stay inside the 16-lane group
-            float ss = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-#pragma unroll
-            for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-            const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[e] = rnd<T>((x[e] * inv) * w0[e]);
-                x[e + 4] = rnd<T>((x[e + 4] * inv) * w1[e]);
-            }
-        }
-        if (a.rope_cos) {
-            float pv[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) pv[e] = __shfl(x[e], gbase + psub);
-            if (rot) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float cv = cr[k][e >> 2][e & 3], sv = sr[k][e >> 2][e & 3];
-                    const float rv = first ? -pv[e] : pv[e];
-                    x[e] = rnd<T>(rnd<T>(x[e] * cv) + rnd<T>(rv * sv));
-                }
-            }
-        }
-        v8 out;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] = from_f<T>(x[e]);
-        if (is_q) {
-            *(v8*)((T*)a.q_out + (long)t * a.q_out_tok + (long)h * a.q_out_head + sub * 8) = out;
-            continue;
-        }
+    int page = 0;
+    if (!is_q) {
         const int pidx = pos >> a.page_shift;
-        const int page = pidx < a.bt_stride ? a.block_tables[(long)seq_k[k] * a.bt_stride + pidx] : -1;
-        if (page < 0 || page >= a.num_pages) {
-            if (sub == 0) atomicOr(a.fault, 2);
-            continue;
-        }
-        const long row = (((long)page * a.kv_heads + h) << a.page_shift) + (pos & ((1 << a.page_shift) - 1));
-        *(v8*)((T*)a.k_pool + row * HD + sub * 8) = out;
-        *(v8*)((T*)a.v_pool + row * HD + sub * 8) = vr[k];
+        page = pidx < a.bt_stride ? a.block_tables[(long)s * a.bt_stride + pidx] : -1;
     }
+    // 4. norm, RoPE and stores
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = to_f(xr[e]);
+    if (w) {  // shuffles stay inside the 16-lane group
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[e] = rnd<T>((x[e] * inv) * w0[e]);
+            x[e + 4] = rnd<T>((x[e + 4] * inv) * w1[e]);
+        }
+    }
+    if (a.rope_cos) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = __shfl(x[e], gbase + psub);
+        if (rot) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float cv = cr[e >> 2][e & 3], sv = sr[e >> 2][e & 3];
+                const float rv = first ? -pv[e] : pv[e];
+                x[e] = rnd<T>(rnd<T>(x[e] * cv) + rnd<T>(rv * sv));
+            }
+        }
+    }
+    v8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = from_f<T>(x[e]);
+    if (is_q) {
+        *(v8*)((T*)a.q_out + (long)t * a.q_out_tok + (long)h * a.q_out_head + sub * 8) = out;
+        return;
+    }
+    if (page < 0 || page >= a.num_pages) {
+        if (sub == 0) atomicOr(a.fault, 2);
+        return;
+    }
+    const long row = (((long)page * a.kv_heads + h) << a.page_shift) + (pos & ((1 << a.page_shift) - 1));
+    *(v8*)((T*)a.k_pool + row * HD + sub * 8) = out;
+    *(v8*)((T*)a.v_pool + row * HD + sub * 8) = vr;
 }
 
 }  // namespace hk
@@ -271,7 +256,7 @@ extern "C" int hk_launch_qk_norm_rope_kv_write(int dtype, const hk::KvArgs* args
                                   (uintptr_t)args->k_norm) & 15) == 0;
     if (dtype != hk::DT_F32 && aligned && tables_aligned && rows * 16 <= 1024 &&
         (!args->rope_cos || args->rd % 16 == 0)) {
-        const dim3 grid((unsigned)((args->n_tokens + hk::TOK_PER_WG - 1) / hk::TOK_PER_WG));
+        const dim3 grid((unsigned)args->n_tokens);
         if (dtype == hk::DT_BF16)
             hipLaunchKernelGGL(hk::qk_norm_rope_kv_write_vec<hk::bf16>, grid, dim3(rows * 16), 0, stream, *args);
         else
