@@ -68,6 +68,18 @@ constexpr int VMCNT0 = 0x0F70;        // s_waitcnt vmcnt(0) (expcnt and lgkmcnt 
 __device__ __forceinline__ int swz(int r) { return 2 * (r & 3) + 8 * ((r >> 4) & 1); }
 __device__ __forceinline__ int lds_off(int r, int c) { return r * KV_ROW + 8 * (c ^ swz(r)); }
 
+// One global_load_lds_dwordx4: lane l copies the 16 bytes at g to LDS byte address lds + 16 l
+// (lds wave-uniform, in M0). Issued from inline assembly so that the compiler does not make
+// every later LDS access wait for the copy; each step waits for its copies explicitly before
+// the barrier that publishes them. Nothing else in these kernels uses M0.
+__device__ __forceinline__ void copy_x4(const void* g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+__device__ __forceinline__ unsigned lds_address(const void* p) {
+    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // Pipeline per 64-key tile (one barrier per tile):
 //   issue the global loads of tile t+1 (block-table entry read one tile earlier) and the
 //   block-table read of tile t+2; S^T = K Q^T, online softmax and O^T += V^T P^T on LDS
@@ -140,50 +152,35 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
         for (int db = 0; db < 4; ++db) vofs[db] = vrow * KV_ROW + 8 * ((4 * db + cl) ^ swz(vrow)) + 4 * (j & 1);
     }
 
-    const int kq = tid >> 4, ch = tid & 15;  // this thread moves keys 4 kq .. 4 kq + 3, chunk ch
-    int ent = 0;          // block-table entry of the next tile to load
-    bool tab_ok = false;  // that tile's key group lies inside the context and the table
+    // K / V tiles go straight from the pool to LDS (global_load_lds_dwordx4): wave w copies
+    // keys 16 w .. 16 w + 15 of a tile, which lie in one page (pages hold >= 16 keys), 4 rows
+    // per copy; lane i of copy c writes row 16 w + 4 c + i / 16 at physical chunk i % 16, so it
+    // reads logical chunk (i % 16) ^ swz(row). Keys at or past the context copy the context's
+    // last key: their scores are masked, so they add 0 x a finite value. A page outside the
+    // table or the pool sets fault bit 2 and copies pool row 0 instead.
+    int pg = 0;  // this wave's page for the next tile to copy (wave-uniform)
     auto lookup = [&](int tile) {
-        const int key = tile * BN + 4 * kq;
-        const int idx = key >> a.page_shift;
-        ent = table[min(idx, a.bt_stride - 1)];
-        tab_ok = key < ctx && idx < a.bt_stride;
-    };
-    uint4 kr[4], vr[4];
-    int nval = 0;  // keys of the loaded group inside the context (0..4)
-    auto load_tile = [&](int tile) {
-        const int key = tile * BN + 4 * kq;
-        const bool page_ok = (unsigned)ent < (unsigned)a.num_pages;
-        if (tab_ok && !page_ok) atomicOr(a.fault, 2);
-        const bool use = tab_ok && page_ok;
-        nval = use ? min(4, ctx - key) : 0;
-        const long base = (use ? ((((long)ent * a.kv_heads + kvh) << a.page_shift) + (key & pmask)) * D : 0) + ch * 8;
-        const T* kp = (const T*)a.k_pool + base;
-        const T* vp = (const T*)a.v_pool + base;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            kr[i] = *(const uint4*)(kp + i * D);
-            vr[i] = *(const uint4*)(vp + i * D);
+        const int kc = min(tile * BN + 16 * wave, ctx - 1);
+        const int idx = kc >> a.page_shift;
+        int e = idx < a.bt_stride ? table[idx] : -1;
+        if ((unsigned)e >= (unsigned)a.num_pages) {
+            if (lane == 0) atomicOr(a.fault, 2);
+            e = 0;
         }
+        pg = __builtin_amdgcn_readfirstlane(e);
     };
-    auto store_tile = [&](int buf) {
-        T* Kb = lds + buf * 2 * TILE_ELEMS;
-        T* Vb = Kb + TILE_ELEMS;
-        if (__all(nval == 4)) {  // every key of the wave's rows lies in the context: no masking
+    const int crow = lane >> 4, cch = lane & 15;  // copy lane: row within a copy, physical chunk
+    auto load_tile = [&](int tile, int buf) {
+        const unsigned kb = lds_address(lds + buf * 2 * TILE_ELEMS), vb = kb + TILE_ELEMS * 2;
+        const long page_row = ((long)pg * a.kv_heads + kvh) << a.page_shift;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int o = lds_off(4 * kq + i, ch);
-                *(uint4*)(Kb + o) = kr[i];
-                *(uint4*)(Vb + o) = vr[i];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t m = i < nval ? ~0u : 0u;
-                const int o = lds_off(4 * kq + i, ch);
-                *(uint4*)(Kb + o) = uint4{kr[i].x & m, kr[i].y & m, kr[i].z & m, kr[i].w & m};
-                *(uint4*)(Vb + o) = uint4{vr[i].x & m, vr[i].y & m, vr[i].z & m, vr[i].w & m};
-            }
+        for (int c = 0; c < 4; ++c) {
+            const int r = 16 * wave + 4 * c + crow;  // row of the tile = key offset
+            const int key = min(tile * BN + r, ctx - 1);
+            const long src = (page_row + (key & pmask)) * D + 8 * (cch ^ swz(r));
+            const unsigned dst = (unsigned)((16 * wave + 4 * c) * KV_ROW * 2);
+            copy_x4((const T*)a.k_pool + src, kb + dst);
+            copy_x4((const T*)a.v_pool + src, vb + dst);
         }
     };
 
@@ -267,8 +264,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     // S^T, online softmax, O^T += V^T P^T, stage the prefetched tile, barrier
     auto step = [&](int i) {
         const int buf = i & 1;
-        if (i + 1 < n_sched) {
-            load_tile(sched_tile(i + 1));
+        if (i + 1 < n_sched) {  // the other buffer was last read in step i - 1
+            load_tile(sched_tile(i + 1), buf ^ 1);
             if (i + 2 < n_sched) lookup(sched_tile(i + 2));
         }
         const T* Kb = lds + buf * 2 * TILE_ELEMS;
@@ -348,16 +345,16 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
                     acc_o[db] = Mma16<T>::mma(af, pf[h], acc_o[db]);
                 }
         }
-        if (i + 1 < n_sched) store_tile(buf ^ 1);
+        if (i + 1 < n_sched) __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of tile i + 1
         __syncthreads();
     };
 
     begin_block(qb_a);
     load_q(qb_a);
     lookup(0);
-    load_tile(0);
+    load_tile(0, 0);
     if (n_sched > 1) lookup(sched_tile(1));
-    store_tile(0);
+    __builtin_amdgcn_s_waitcnt(VMCNT0);  // Q and this wave's copies of tile 0
     __syncthreads();
     // The two blocks run as two loops whose bodies issue only the tile and table loads:
     // Q, gate and output traffic stays between them, so the compiler's wait counting never
