@@ -80,14 +80,10 @@ __device__ __forceinline__ unsigned lds_address(const void* p) {
     return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// Pipeline per 64-key tile (one barrier per tile):
-//   issue the global loads of tile t+1 (block-table entry read one tile earlier) and the
-//   block-table read of tile t+2; S^T = K Q^T, online softmax and O^T += V^T P^T on LDS
-//   buffer t % 2; write tile t+1 into buffer (t+1) % 2; barrier.
-// Each thread moves 4 consecutive keys (one page: pages hold >= 16 keys) x one 16-byte chunk
-// of K and of V, so one block-table entry addresses all 8 of its loads. Loads are
-// unconditional (addresses clamped to pool row 0) and masked when written to LDS (only
-// waves holding keys past the context pay for the masking).
+// Pipeline per 64-key tile (one barrier per tile): issue the direct-to-LDS copies of tile
+// t+1 into buffer (t+1) % 2 (page read one tile earlier) and the block-table read of tile
+// t+2; S^T = K Q^T, online softmax and O^T += V^T P^T on buffer t % 2; wait for this wave's
+// copies; barrier.
 // Softmax keeps the raw-score row max m and evaluates p = 2^(s c - m c) with one FMA
 // (c = scale log2 e); the O / l rescale happens only when the max grew by more than 2^8
 // (otherwise p <= 2^8 and the fp32 sums lose nothing), which is the same normalised result.
@@ -208,8 +204,6 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     float m_use = -INFINITY, l_run = 0.0f;
     const float c = a.scale_log2;
 
-    // epilogue of a block: o = O / l (both lane halves hold partial row sums), then the
-    // output gate o = round(o) * round(sigmoid(gate)) as the reference rounds both
     // Epilogue of block qb: o = O / l (both lane halves hold partial row sums), rounded to T,
     // then the output gate o = round(o) * round(sigmoid(gate)) as the reference rounds both.
     // O leaves its accumulator layout through LDS (the free K/V buffer `stg`, row-major with a
@@ -260,8 +254,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
         l_run = 0.0f;
     };
 
-    // one 64-key tile of the schedule: prefetch the next tile (and the table entry after it),
-    // S^T, online softmax, O^T += V^T P^T, stage the prefetched tile, barrier
+    // one 64-key tile of the schedule: start the copies of the next tile (and the table read
+    // after it), S^T, online softmax, O^T += V^T P^T, wait for the copies, barrier
     auto step = [&](int i) {
         const int buf = i & 1;
         if (i + 1 < n_sched) {  // the other buffer was last read in step i - 1

@@ -12,7 +12,7 @@ struct Layer {
     int type = 0;
     float *in_norm = nullptr, *post_norm = nullptr;
     void *w_gu = nullptr, *w_down = nullptr;
-    void *w_in = nullptr, *w_out = nullptr;
+    void *w_in = nullptr, *w_ba = nullptr, *w_out = nullptr;
     float *conv_w = nullptr, *norm_w = nullptr, *base_g = nullptr, *dt_bias = nullptr;
     void *w_qkv = nullptr, *w_o = nullptr;
     float *q_norm = nullptr, *k_norm = nullptr;
@@ -34,7 +34,7 @@ struct hk_kev_model {
     float* head_b = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
     // derived sizes
-    int key_dim = 0, value_dim = 0, conv_dim = 0, gdn_rows = 0, attn_rows = 0;
+    int key_dim = 0, value_dim = 0, conv_dim = 0, gdn_rows = 0, ba_rows = 0, attn_rows = 0;
 };
 
 // Per-call view of cached state for a continuation forward (all pointers owned by the cache).

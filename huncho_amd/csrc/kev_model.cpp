@@ -10,8 +10,9 @@
 //   final: rms of each sequence's last token, then the decision head (fp32).
 // Load-time layout work (done once, qwen3_5.rs:2185-2348 is the reference loader):
 //   * projections that read the same input are fused into one GEMM weight:
-//     GDN in_proj_qkv | in_proj_z | in_proj_b | in_proj_a, attention q_proj | k_proj |
-//     v_proj, MLP gate_proj | up_proj;
+//     GDN in_proj_qkv | in_proj_z (and in_proj_b | in_proj_a as a second, narrow GEMM, so
+//     the wide one keeps a multiple of 256 columns), attention q_proj | k_proj | v_proj,
+//     MLP gate_proj | up_proj;
 //   * zero-centred norm weights become (1 + w) in fp32 (effective_norm_weight, 180-182),
 //     conv weights, the gated-norm weight and dt_bias become fp32, A_log becomes
 //     base_g = -exp(A_log) in fp32 (788-790);
@@ -131,8 +132,11 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
     m->key_dim = c.lin_n_k_heads * c.lin_key_dim;
     m->value_dim = c.lin_n_v_heads * c.lin_v_dim;
     m->conv_dim = 2 * m->key_dim + m->value_dim;
-    // fused in_proj rows padded to a multiple of 8 (16-byte aligned rows for the fused layer)
-    m->gdn_rows = (m->conv_dim + m->value_dim + 2 * c.lin_n_v_heads + 7) / 8 * 8;
+    // GDN in_proj as two GEMMs: [qkv | z] (a multiple of the GEMM's 256-column tiles at the
+    // Kev shape, 8192) and [b | a] (2 Hv columns); both padded to a multiple of 8 rows
+    // (16-byte aligned rows for the fused layer)
+    m->gdn_rows = (m->conv_dim + m->value_dim + 7) / 8 * 8;
+    m->ba_rows = (2 * c.lin_n_v_heads + 7) / 8 * 8;
     m->attn_rows = 2 * c.n_heads * c.head_dim + 2 * c.n_kv_heads * c.head_dim;
     const int H = c.hidden, I = c.intermediate;
     int rc = HK_OK;
@@ -153,9 +157,9 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
         if ((rc = fuse_rows(m, {{w.down_proj, H}}, I, &L.w_down))) return fail(rc);
         if (L.type == 0) {
             const int Hv = c.lin_n_v_heads;
-            if ((rc = fuse_rows(m, {{w.in_qkv, m->conv_dim}, {w.in_z, m->value_dim}, {w.in_b, Hv}, {w.in_a, Hv}}, H,
-                                &L.w_in, m->gdn_rows)))
+            if ((rc = fuse_rows(m, {{w.in_qkv, m->conv_dim}, {w.in_z, m->value_dim}}, H, &L.w_in, m->gdn_rows)))
                 return fail(rc);
+            if ((rc = fuse_rows(m, {{w.in_b, Hv}, {w.in_a, Hv}}, H, &L.w_ba, m->ba_rows))) return fail(rc);
             if ((rc = fuse_rows(m, {{w.out_proj, H}}, m->value_dim, &L.w_out))) return fail(rc);
             if ((rc = small_f32(m, w.conv_w, (size_t)m->conv_dim * c.conv_k, &L.conv_w, same))) return fail(rc);
             if ((rc = small_f32(m, w.norm_w, c.lin_v_dim, &L.norm_w, same))) return fail(rc);
@@ -214,7 +218,7 @@ struct Workspace {
 };
 
 struct Buffers {
-    void *x, *h, *big, *q, *k, *v, *o, *act, *k_pool, *v_pool;
+    void *x, *h, *big, *ba, *q, *k, *v, *o, *act, *k_pool, *v_pool;
     float *g, *beta;
     int* ctx_lens;
     size_t pool_bytes;
@@ -230,6 +234,7 @@ Buffers carve(const hk_kev_model* m, Workspace& ws, int n, int n_seqs, int num_p
     b.x = ws.take_bytes((size_t)n * c.hidden * e);
     b.h = ws.take_bytes((size_t)n * c.hidden * e);
     b.big = ws.take_bytes((size_t)n * big_cols * e);
+    b.ba = ws.take_bytes((size_t)n * m->ba_rows * e);
     b.q = ws.take_bytes((size_t)n * m->key_dim * e);
     b.k = ws.take_bytes((size_t)n * m->key_dim * e);
     b.v = ws.take_bytes((size_t)n * m->value_dim * e);
@@ -330,16 +335,17 @@ int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
         if (L.type == 0) {
             const int rows = m->gdn_rows;
             RUN(hk_gemm_xwt(ctx, dt, n, rows, H, b.h, H, L.w_in, H, b.big, rows, nullptr, 0, 1.0f, 0.0f));
-            const int b_col = m->conv_dim + m->value_dim, a_col = b_col + Hv;
+            RUN(hk_gemm_xwt(ctx, dt, n, m->ba_rows, H, b.h, H, L.w_ba, H, b.ba, m->ba_rows, nullptr, 0, 1.0f, 0.0f));
+            const int b_col = 0, a_col = Hv;
             if (dt != HK_F32 && c.conv_k == 4 && rows % 8 == 0) {
                 // one kernel: conv + SiLU + l2norm + beta/g + chunked delta rule + gated RMSNorm
-                RUN(hk_gdn_fused_rows(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, nullptr, b.big, rows, b_col,
+                RUN(hk_gdn_fused_rows(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, nullptr, b.ba, m->ba_rows, b_col,
                                       a_col, L.base_g, L.dt_bias, (char*)b.big + (size_t)m->conv_dim * e, rows, L.norm_w,
                                       c.eps, cu_dev, n_seqs, n, Hv, Hk, nullptr, nullptr, b.o, (long)Hv * 128,
                                       view ? view->init_rows[gi] : nullptr, view ? view->final_rows[gi] : nullptr,
                                       view ? view->hist_rows[gi] : nullptr, view ? view->tail_rows[gi] : nullptr));
             } else {
-                RUN(hk_gdn_prep(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, b.big, rows, b_col, a_col, L.base_g,
+                RUN(hk_gdn_prep(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, b.ba, m->ba_rows, b_col, a_col, L.base_g,
                                 L.dt_bias, cu_dev, n_seqs, n, Hv, Hk, b.q, b.k, b.v, b.g, b.beta, nullptr));
                 RUN(hk_gated_delta_chunked(ctx, dt, b.q, (long)Hk * 128, b.k, (long)Hk * 128, b.v, (long)Hv * 128,
                                            b.g, b.beta, cu_dev, n_seqs, n, Hv, Hk, 128, 128, nullptr, nullptr, b.o,
