@@ -154,11 +154,19 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     // reads logical chunk (i % 16) ^ swz(row). Keys at or past the context copy the context's
     // last key: their scores are masked, so they add 0 x a finite value. A page outside the
     // table or the pool sets fault bit 2 and copies pool row 0 instead.
-    int pg = 0;  // this wave's page for the next tile to copy (wave-uniform)
+    // The table entry of a tile is read one step before its copies and used only then: using
+    // it in the step that reads it would wait for the copies issued just before (memory
+    // loads complete in issue order), which would serialise every tile's copies with the
+    // compute of the tile before.
+    int pg = 0;      // this wave's page for the next tile to copy (wave-uniform)
+    int e_next = 0;  // block-table entry of the tile after that (in flight)
     auto lookup = [&](int tile) {
         const int kc = min(tile * BN + 16 * wave, ctx - 1);
         const int idx = kc >> a.page_shift;
-        int e = idx < a.bt_stride ? table[idx] : -1;
+        e_next = idx < a.bt_stride ? table[idx] : -1;
+    };
+    auto resolve = [&]() {
+        int e = e_next;
         if ((unsigned)e >= (unsigned)a.num_pages) {
             if (lane == 0) atomicOr(a.fault, 2);
             e = 0;
@@ -259,6 +267,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     auto step = [&](int i) {
         const int buf = i & 1;
         if (i + 1 < n_sched) {  // the other buffer was last read in step i - 1
+            resolve();
             load_tile(sched_tile(i + 1), buf ^ 1);
             if (i + 2 < n_sched) lookup(sched_tile(i + 2));
         }
@@ -346,6 +355,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     begin_block(qb_a);
     load_q(qb_a);
     lookup(0);
+    resolve();
     load_tile(0, 0);
     if (n_sched > 1) lookup(sched_tile(1));
     __builtin_amdgcn_s_waitcnt(VMCNT0);  // Q and this wave's copies of tile 0
