@@ -160,13 +160,15 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     // compute of the tile before.
     int pg = 0;      // this wave's page for the next tile to copy (wave-uniform)
     int e_next = 0;  // block-table entry of the tile after that (in flight)
+    bool in_table = true;
     auto lookup = [&](int tile) {
         const int kc = min(tile * BN + 16 * wave, ctx - 1);
         const int idx = kc >> a.page_shift;
-        e_next = idx < a.bt_stride ? table[idx] : -1;
+        in_table = idx < a.bt_stride;
+        e_next = table[min(idx, a.bt_stride - 1)];
     };
     auto resolve = [&]() {
-        int e = e_next;
+        int e = in_table ? e_next : -1;
         if ((unsigned)e >= (unsigned)a.num_pages) {
             if (lane == 0) atomicOr(a.fault, 2);
             e = 0;
@@ -192,12 +194,15 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     int qi = 0, qpos = 0, first_pos = 0;
     bool q_valid = false;
     v8 qf[8];  // Q[q][ks*16 + g*8 .. +8] for ks = 0..7
-    auto load_q = [&](int qb) {  // issued once the previous block's last S^T no longer needs qf
-        const int qi_ = qb * P + p;
-        const bool ok = qi_ < q_len;
-        const T* qp = (const T*)a.q + (long)(q0 + (ok ? qi_ : 0)) * a.q_tok + (long)head * a.q_head;
+    // Issued once the previous block's last S^T no longer needs qf. Rows past the sequence load
+    // its last row (their columns of S^T, P and O^T are computed and never stored; each query
+    // column is independent), so the loads need no select, which would make the compiler wait
+    // for them on the spot.
+    auto load_q = [&](int qb) {
+        const int qi_ = min(qb * P + p, q_len - 1);
+        const T* qp = (const T*)a.q + (long)(q0 + qi_) * a.q_tok + (long)head * a.q_head;
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) qf[ks] = ok ? *(const v8*)(qp + ks * 16 + g * 8) : v8{};
+        for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const v8*)(qp + ks * 16 + g * 8);
     };
     auto begin_block = [&](int qb) {
         qi = qb * P + p;  // index among the sequence's new queries
@@ -205,6 +210,12 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
         qpos = off + (q_valid ? qi : q_len - 1);
         first_pos = off + qb * P;
     };
+
+    // The epilogue's gate reads are unconditional (Q rows stand in when there is no gate), so
+    // the compiler issues all of them before it waits for the first.
+    const bool gated_out = a.gate != nullptr;
+    const void* const tb = gated_out ? a.gate : a.q;
+    const long tb_tok = gated_out ? a.g_tok : a.q_tok, tb_head = gated_out ? a.g_head : a.q_head;
 
     f32x16 acc_o[4];
 #pragma unroll
@@ -219,7 +230,6 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     // (16 lanes x 16 bytes) instead of 32 rows x 16 bytes per instruction; the gate loads are
     // issued first and land while O is staged.
     auto finish_block = [&](int qb, int stg) {
-        const bool gated = a.gate != nullptr;
         T* const sb = lds + stg * 2 * TILE_ELEMS;  // [128 rows][128] T, 32 KB
         v8 gch[8];
         int orow[8];  // token index of each chunk's row (-1: past the sequence)
@@ -229,8 +239,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
             const int qi_ = qb * P + (R & (P - 1));
             const int hd = kvh * a.group + (R >> p_shift);
             orow[k] = qi_ < q_len ? q0 + qi_ : -1;
-            const T* gp = (const T*)a.gate + (long)(q0 + min(qi_, q_len - 1)) * a.g_tok + (long)hd * a.g_head + ch * 8;
-            gch[k] = gated ? *(const v8*)gp : v8{};
+            const T* gp = (const T*)tb + (long)(q0 + min(qi_, q_len - 1)) * tb_tok + (long)hd * tb_head + ch * 8;
+            gch[k] = *(const v8*)gp;  // unconditional (a Q row when ungated): no select, no early wait
         }
         const float l_tot = l_run + __shfl_xor(l_run, 32);
         const float inv_l = 1.0f / l_tot;
@@ -248,7 +258,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
         for (int k = 0; k < 8; ++k) {
             const int id = tid + 256 * k, R = id >> 4, ch = id & 15;
             v8 ov = *(const v8*)(sb + R * KV_ROW + 8 * (ch ^ (R & 15)));
-            if (gated) {
+            if (gated_out) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) ov[e] = (T)((float)ov[e] * (float)(T)fast_sigmoid((float)gch[k][e]));
             }
@@ -348,13 +358,15 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
                     acc_o[db] = Mma16<T>::mma(af, pf[h], acc_o[db]);
                 }
         }
-        if (i + 1 < n_sched) __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of tile i + 1
+        // this wave's copies of tile i + 1; unconditional, so that no load is pending on the
+        // loop's back edge and the compiler adds no wait of its own inside the next step
+        __builtin_amdgcn_s_waitcnt(VMCNT0);
         __syncthreads();
     };
 
     begin_block(qb_a);
+    lookup(0);  // issued before Q, so that resolving it waits for the table read alone
     load_q(qb_a);
-    lookup(0);
     resolve();
     load_tile(0, 0);
     if (n_sched > 1) lookup(sched_tile(1));
