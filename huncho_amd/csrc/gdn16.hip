@@ -29,8 +29,8 @@
 // 32 s + 16 + 4 q + e - 4 for e >= 4), and the A operands are read from LDS in that order.
 //
 // Chunk pipeline:
-//   P0  global -> LDS: q, k, v rows (fused: waves 0-5 run the conv and l2norm); wave 7:
-//       g scan and beta
+//   P0  global -> LDS: q, k, v rows (fused: all four waves run the conv, SiLU and l2norm,
+//       4 rows of each tensor per 16-lane group); wave 3: g scan and beta
 //   P1  16x16 tiles of K K^T and Q K^T -> A (fp32, masked, decayed) and Aqk (16-bit);
 //       every wave: K S0, Q S0 for its columns -> R = beta (V - e^G K S0), e^G Q S0
 //   P2  the four 16x16 diagonal blocks of T = (I + A)^-1 in place (waves 0-3)
@@ -213,8 +213,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
             for (int rb = 0; rb < 8; ++rb) S[cw][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // fused conv lanes (waves 0-2): tensor wave (q, k, v), chunk rows 16 q4 + 8 hf .. + 7,
-    // channels 8 j .. + 7 of the head; mixed column mcol + 8 j
+    // conv-tail lanes (waves 0-2): tensor wave (q, k, v), channels 8 j .. + 7 of the head;
+    // mixed column mcol + 8 j
     const long mcol = (long)kh * 128 + wave * (long)fa.Hk * 128 + (wave == 2 ? (long)(h - kh) * 128 : 0);
 
     for (int c0 = 0; c0 < Tn; c0 += CH) {
@@ -224,74 +224,85 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const int q4 = ln >> 4, j = ln & 15;
-        const long mc = mcol + 8 * j;
         __syncthreads();
         // ---------------- P0: inputs -> LDS ----------------
         if (FUSED) {
-            if (wave < 3) {
-                // 8 conv outputs per pass from an 11-row window of raw conv inputs (sequence
-                // positions c0 + r0 - 3 ..). Positions past the sequence end are loaded clamped:
-                // they only reach rows past the end, whose beta is 0 and whose outputs are not
-                // stored. Positions before the start are the conv history or 0.
-                T* dst = wave == 0 ? Qs : wave == 1 ? Ks : Vs;
+            // 16 lane groups (4 per wave) x 4 rows of each of q, k and v: group G = 4 wave + q4
+            // takes chunk rows 4 G .. 4 G + 3 of every tensor, so all four waves share the conv,
+            // SiLU and l2norm evenly. Each tensor's 4 conv outputs come from a 7-row window of raw
+            // conv inputs (sequence positions c0 + 4 G - 3 ..). Positions past the sequence end
+            // are loaded clamped: they only reach rows past the end, whose beta is 0 and whose
+            // outputs are not stored. Positions before the start are the conv history or 0.
+            const int r0 = 4 * (4 * wave + q4);
+            auto tcol = [&](int tsr) {  // mixed column of this lane's channels in tensor tsr
+                return (tsr == 2 ? 2 * (long)fa.Hk * 128 + (long)h * 128 : (long)tsr * fa.Hk * 128 + (long)kh * 128) +
+                       8 * j;
+            };
+            // all three windows are loaded before the first conv, so the chunk waits for one
+            // memory round trip
+            v8 raw[3][7];
+#pragma unroll
+            for (int tsr = 0; tsr < 3; ++tsr)
+#pragma unroll
+                for (int i = 0; i < 7; ++i) {
+                    const int p = c0 + r0 - 3 + i;
+                    const int pc = p < 0 ? 0 : (p >= Tn ? Tn - 1 : p);
+                    raw[tsr][i] = *(const v8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + tcol(tsr));
+                }
+            if (c0 + r0 == 0) {  // windows start 3 positions before the sequence
+#pragma unroll
+                for (int tsr = 0; tsr < 3; ++tsr) {
+                    if (hist) {
+                        const T* hb = hist + tcol(tsr) * 3;
+#pragma unroll
+                        for (int i = 0; i < 3; ++i)
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) raw[tsr][i][e] = hb[e * 3 + i];
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 3; ++i) raw[tsr][i] = v8{};
+                    }
+                }
+            }
+#pragma unroll
+            for (int tsr = 0; tsr < 3; ++tsr) {
+                const long mct = tcol(tsr);
+                T* dst = tsr == 0 ? Qs : tsr == 1 ? Ks : Vs;
                 // taps (0, 1) and (2, 3) of each channel as 16-bit pairs (the weights are the
                 // model dtype's values, exact in T)
                 v2 w01[8], w23[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const f32x4 w4 = *(const f32x4*)(fa.conv_w + (mc + e) * 4);
+                    const f32x4 w4 = *(const f32x4*)(fa.conv_w + (mct + e) * 4);
                     w01[e] = v2{(T)w4[0], (T)w4[1]};
                     w23[e] = v2{(T)w4[2], (T)w4[3]};
                 }
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const int r0 = 16 * q4 + 8 * hf;
-                    v8 raw[11];
+                for (int i = 0; i < 4; ++i) {
+                    float y[8];
 #pragma unroll
-                    for (int i = 0; i < 11; ++i) {
-                        const int p = c0 + r0 - 3 + i;
-                        const int pc = p < 0 ? 0 : (p >= Tn ? Tn - 1 : p);
-                        raw[i] = *(const v8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + mc);
+                    for (int e = 0; e < 8; ++e) {
+                        const float acc = dot2(w23[e], v2{raw[tsr][i + 2][e], raw[tsr][i + 3][e]},
+                                               dot2(w01[e], v2{raw[tsr][i][e], raw[tsr][i + 1][e]}, 0.0f));
+                        y[e] = silu(acc);
                     }
-                    if (c0 + r0 == 0) {  // window starts 3 positions before the sequence
-                        if (hist) {
-                            const T* hb = hist + mc * 3;
-#pragma unroll
-                            for (int i = 0; i < 3; ++i)
-#pragma unroll
-                                for (int e = 0; e < 8; ++e) raw[i][e] = hb[e * 3 + i];
-                        } else {
-#pragma unroll
-                            for (int i = 0; i < 3; ++i) raw[i] = v8{};
-                        }
-                    }
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        float y[8];
+                    if (tsr < 2) {  // conv output stored in the activation dtype, then l2norm over
+                                    // the head's 128 channels (16 lanes); q also takes the scale
+                        float ss = 0.0f;
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
-                            const float acc = dot2(w23[e], v2{raw[i + 2][e], raw[i + 3][e]},
-                                                   dot2(w01[e], v2{raw[i][e], raw[i + 1][e]}, 0.0f));
-                            y[e] = silu(acc);
+                            y[e] = rnd<T>(y[e]);
+                            ss += y[e] * y[e];
                         }
-                        if (wave < 2) {  // conv output stored in the activation dtype, then l2norm
-                                         // over the head's 128 channels (16 lanes)
-                            float ss = 0.0f;
+                        ss = sum16(ss);
+                        const float inv = fast_rsqrt(ss + 1e-6f);
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) {
-                                y[e] = rnd<T>(y[e]);
-                                ss += y[e] * y[e];
-                            }
-                            ss = sum16(ss);
-                            const float inv = fast_rsqrt(ss + 1e-6f);
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) y[e] = wave == 0 ? (y[e] * inv) * fa.scale : y[e] * inv;
-                        }
-                        v8 o;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) o[e] = (T)y[e];
-                        *(v8*)(dst + el(r0 + i, 8 * j)) = o;
+                        for (int e = 0; e < 8; ++e) y[e] = tsr == 0 ? (y[e] * inv) * fa.scale : y[e] * inv;
                     }
+                    v8 o;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[e] = (T)y[e];
+                    *(v8*)(dst + el(r0 + i, 8 * j)) = o;
                 }
             }
         } else {

@@ -545,12 +545,14 @@ def test_gdn_prep_bf16(ctx):
 def test_norms_and_swiglu_bf16(ctx):
     from huncho_amd.ops import gated_rms_norm, rms_norm, swiglu
 
-    n, H = 50, 1024
-    x = abi.synth_normal_bf16(SEED, 90, n * H).reshape(n, H)
-    w = O.round_bf16(abi.synth_normal(SEED, 91, H, 0.0, 0.02)) + np.float32(1)
-    y = rms_norm(ctx, bf16_dev(x), cuda(w), 1e-6)
-    ref = O.round_bf16(O.rms_norm_effective(O.bf16_to_f32(x), w, 1e-6))
-    assert rel_err(O.bf16_to_f32(bits_of(y)), ref) < 1e-2
+    # widths 512 / 1024 (two rows per wave) and 2048 (one); odd row counts end on a clamped row
+    for n, H in ((50, 1024), (51, 1024), (7, 512), (9, 2048)):
+        x = abi.synth_normal_bf16(SEED, 90, n * H).reshape(n, H)
+        w = O.round_bf16(abi.synth_normal(SEED, 91, H, 0.0, 0.02)) + np.float32(1)
+        y = rms_norm(ctx, bf16_dev(x), cuda(w), 1e-6)
+        ref = O.round_bf16(O.rms_norm_effective(O.bf16_to_f32(x), w, 1e-6))
+        assert rel_err(O.bf16_to_f32(bits_of(y)), ref) < 1e-2, (n, H)
+    n = 50
     heads = 8
     o = abi.synth_normal_bf16(SEED, 92, n * heads * 128).reshape(n, heads, 128)
     z = abi.synth_normal_bf16(SEED, 93, n * heads * 128 * 2).reshape(n, heads * 128 * 2)
@@ -559,9 +561,10 @@ def test_norms_and_swiglu_bf16(ctx):
     ref = O.round_bf16(O.rms_norm_gated(O.bf16_to_f32(o), O.bf16_to_f32(z)[:, heads * 128:].reshape(n, heads, 128),
                                         nw, 1e-6))
     assert rel_err(O.bf16_to_f32(bits_of(gn)), ref) < 1e-2
-    I = 3584
-    gu = abi.synth_normal_bf16(SEED, 95, n * 2 * I).reshape(n, 2 * I)
-    s = swiglu(ctx, bf16_dev(gu), I)
-    gf = O.bf16_to_f32(gu)
-    ref = O.round_bf16(O.round_bf16(gf[:, :I] / (1 + np.exp(-gf[:, :I]))) * gf[:, I:])
-    assert rel_err(O.bf16_to_f32(bits_of(s)), ref) < 1e-2
+    # a 448-thread row block (3584) and 256-thread column blocks (5120); odd row counts
+    for n, I in ((50, 3584), (51, 3584), (3, 5120)):
+        gu = abi.synth_normal_bf16(SEED, 95, n * 2 * I).reshape(n, 2 * I)
+        s = swiglu(ctx, bf16_dev(gu), I)
+        gf = O.bf16_to_f32(gu)
+        ref = O.round_bf16(O.round_bf16(gf[:, :I] / (1 + np.exp(-gf[:, :I]))) * gf[:, I:])
+        assert rel_err(O.bf16_to_f32(bits_of(s)), ref) < 1e-2, (n, I)
