@@ -60,25 +60,12 @@ constexpr int KV_ROW = 128;                        // LDS row: one key's 128 dim
 constexpr int TILE_ELEMS = BN * KV_ROW;            // one K or V tile: 16 KB
 constexpr size_t ATTN16_LDS = 4 * TILE_ELEMS * 2;  // K and V, double-buffered: 65,536 B
 constexpr float RESCALE_LOG2 = 8.0f;  // exponents may run up to 2^8 above the row max in use
-constexpr int VMCNT0 = 0x0F70;        // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 
 // The 16-byte chunk c of key row r sits at chunk c ^ swz(r). With this swizzle the row
 // writes, the permuted-row K reads of S^T = K Q^T and the transposing V reads of P.V each
 // spread over all LDS banks (no bank holds more words than the access's minimum).
 __device__ __forceinline__ int swz(int r) { return 2 * (r & 3) + 8 * ((r >> 4) & 1); }
 __device__ __forceinline__ int lds_off(int r, int c) { return r * KV_ROW + 8 * (c ^ swz(r)); }
-
-// One global_load_lds_dwordx4: lane l copies the 16 bytes at g to LDS byte address lds + 16 l
-// (lds wave-uniform, in M0). Issued from inline assembly so that the compiler does not make
-// every later LDS access wait for the copy; each step waits for its copies explicitly before
-// the barrier that publishes them. Nothing else in these kernels uses M0.
-__device__ __forceinline__ void copy_x4(const void* g, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
-                 : "memory");
-}
-__device__ __forceinline__ unsigned lds_address(const void* p) {
-    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
-}
 
 // Pipeline per 64-key tile (one barrier per tile): issue the direct-to-LDS copies of tile
 // t+1 into buffer (t+1) % 2 (page read one tile earlier) and the block-table read of tile

@@ -15,7 +15,8 @@
 // bidir_attn_16 design: one workgroup = one (sequence, head, 128 query positions); 4 waves x
 // 32 queries; S^T = K Q^T on v_mfma_f32_32x32x16 (each lane owns a query column, K rows
 // permuted so a lane's accumulator holds 16 consecutive keys that feed P.V directly); K and
-// V tiles of 64 keys in double-buffered LDS with XOR chunk swizzles (K: row & 7; V:
+// V tiles of 64 keys, copied straight from the q/k/v rows (global_load_lds_dwordx4, no staging
+// registers), in double-buffered LDS with XOR chunk swizzles (K: row & 7; V:
 // (row & 3) << 1 | (row >> 4) & 1, chosen so the permuted K reads, the transposing V reads
 // (ds_read_b64_tr_b16) and the row writes all reach the LDS banks evenly); online softmax
 // in base 2 with lazy rescaling; only tiles that intersect the block's key range are read.
@@ -87,26 +88,20 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
         for (int db = 0; db < 2; ++db) vro[db] = vrow * D + 8 * ((4 * db + cl) ^ vswz(vrow)) + 4 * (j & 1);
     }
 
-    // thread t moves key rows t / 8 and t / 8 + 32 of a tile, 16-byte chunk t % 8, of K and V;
-    // keys past the sequence end read its last row (finite; their scores are masked)
-    const int lr = tid >> 3, lc = tid & 7;
-    // (native vector registers: a copied uint4 struct array stays in scratch memory)
-    v8 kr[2], vr[2];
-    auto load_tile = [&](int tile) {
+    // K / V tiles go straight from the q/k/v rows to LDS (global_load_lds_dwordx4): wave w
+    // copies key rows 16 w .. 16 w + 15 of K and of V, 8 rows per copy; lane i of a copy writes
+    // row r = base + i / 8 at physical chunk i % 8, so it reads logical chunk (i % 8) ^ swizzle(r).
+    // Keys past the sequence end read its last row (finite; their scores are masked).
+    const int crow = lane >> 3, cch = lane & 7;
+    auto load_tile = [&](int tile, int buf) {
+        const unsigned kb_ = lds_address(lds + buf * 2 * TILE), vb_ = kb_ + TILE * 2;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int key = min(tile * BN + lr + 32 * i, L - 1);
-            kr[i] = *(const v8*)((const T*)a.k + (long)(t0 + key) * a.k_tok + (long)h * D + lc * 8);
-            vr[i] = *(const v8*)((const T*)a.v + (long)(t0 + key) * a.v_tok + (long)h * D + lc * 8);
-        }
-    };
-    auto store_tile = [&](int buf) {
-        T* Kb = lds + buf * 2 * TILE;
-        T* Vb = Kb + TILE;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            *(v8*)(Kb + k_off(lr + 32 * i, lc)) = kr[i];
-            *(v8*)(Vb + v_off(lr + 32 * i, lc)) = vr[i];
+        for (int cp = 0; cp < 2; ++cp) {
+            const int r0 = 16 * wave + 8 * cp, r = r0 + crow;
+            const long key = t0 + min(tile * BN + r, L - 1);
+            const unsigned dst = (unsigned)(r0 * D * 2);
+            copy_x4((const T*)a.k + key * a.k_tok + (long)h * D + 8 * (cch ^ kswz(r)), kb_ + dst);
+            copy_x4((const T*)a.v + key * a.v_tok + (long)h * D + 8 * (cch ^ vswz(r)), vb_ + dst);
         }
     };
 
@@ -116,12 +111,12 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
     float m_use = -INFINITY, l_run = 0.0f;
     const float c = a.scale_log2;
 
-    load_tile(tile_lo);
-    store_tile(0);
+    load_tile(tile_lo, 0);
+    __builtin_amdgcn_s_waitcnt(VMCNT0);  // Q and this wave's copies of the first tile
     __syncthreads();
     for (int it = 0; it < n_tiles; ++it) {
         const int buf = it & 1, tile = tile_lo + it;
-        if (it + 1 < n_tiles) load_tile(tile + 1);
+        if (it + 1 < n_tiles) load_tile(tile + 1, buf ^ 1);  // that buffer was last read in step it - 1
         const T* Kb = lds + buf * 2 * TILE;
         const T* Vb = Kb + TILE;
         // (the two accumulation chains alternate, so consecutive MFMAs are independent)
@@ -209,7 +204,9 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
                 const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 acc_o[db] = Mma16<T>::mma(af, pf[cc], acc_o[db]);
             }
-        if (it + 1 < n_tiles) store_tile(buf ^ 1);
+        // this wave's copies of the next tile; unconditional, so that no load is pending on the
+        // loop's back edge
+        __builtin_amdgcn_s_waitcnt(VMCNT0);
         __syncthreads();
     }
     const float l_tot = l_run + __shfl_xor(l_run, 32);

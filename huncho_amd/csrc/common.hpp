@@ -105,6 +105,22 @@ __device__ __forceinline__ float wave_max32(float v) {
     return fmaxf(v, __shfl_xor(v, 32));
 }
 
+constexpr int VMCNT0 = 0x0F70;  // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
+
+// One global_load_lds_dwordx4: lane l copies the 16 bytes at g to LDS byte address lds + 16 l
+// (lds wave-uniform, in M0). Issued from inline assembly so that the compiler does not make
+// every later LDS access wait for the copy; a kernel that uses it waits for its copies
+// explicitly (s_waitcnt vmcnt) before the barrier that publishes them. Nothing else in these
+// kernels uses M0.
+__device__ __forceinline__ void copy_x4(const void* g, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+// LDS byte address of a pointer into shared memory
+__device__ __forceinline__ unsigned lds_address(const void* p) {
+    return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 }  // namespace hk
 
 // Status codes shared with include/huncho_rocm.h.
