@@ -61,11 +61,15 @@ constexpr int TILE_ELEMS = BN * KV_ROW;            // one K or V tile: 16 KB
 constexpr size_t ATTN16_LDS = 4 * TILE_ELEMS * 2;  // K and V, double-buffered: 65,536 B
 constexpr float RESCALE_LOG2 = 8.0f;  // exponents may run up to 2^8 above the row max in use
 
-// The 16-byte chunk c of key row r sits at chunk c ^ swz(r). With this swizzle the row
-// writes, the permuted-row K reads of S^T = K Q^T and the transposing V reads of P.V each
-// spread over all LDS banks (no bank holds more words than the access's minimum).
+// The 16-byte chunk c of key row r sits at chunk c ^ swz(r) in a V tile and c ^ swzk(r) in a
+// K tile. The V swizzle depends only on row bits 0, 1 and 4, so the transposing V reads of P.V
+// can add key offsets of 4, 8 and 32 rows to one per-lane address. The K swizzle serves the
+// permuted-row reads of S^T = K Q^T: a 16-lane group reads rows {0-7, 16-23} (or {8-15, 24-31})
+// at one logical chunk, and swzk maps those rows to 16 distinct chunks, one 16-byte slot each
+// of the 256-byte bank row (the V swizzle gives only 8 distinct, even, chunks there).
 __device__ __forceinline__ int swz(int r) { return 2 * (r & 3) + 8 * ((r >> 4) & 1); }
-__device__ __forceinline__ int lds_off(int r, int c) { return r * KV_ROW + 8 * (c ^ swz(r)); }
+__device__ __forceinline__ int swzk(int r) { return (r & 7) | (((r >> 4) & 1) << 3); }
+__device__ __forceinline__ int lds_off_k(int r, int c) { return r * KV_ROW + 8 * (c ^ swzk(r)); }
 
 // Pipeline per 64-key tile (one barrier per tile): issue the direct-to-LDS copies of tile
 // t+1 into buffer (t+1) % 2 (page read one tile earlier) and the block-table read of tile
@@ -127,7 +131,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     {
         const int kr_ = perm_key(col);
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) koff[ks] = lds_off(kr_, 2 * ks + g);
+        for (int ks = 0; ks < 8; ++ks) koff[ks] = lds_off_k(kr_, 2 * ks + g);
         const int G = lane >> 4, j = lane & 15;
         const int vrow = (G >> 1) * 16 + (j >> 2);
         const int cl = 2 * (G & 1) + ((j & 3) >> 1);
@@ -138,9 +142,10 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
     // K / V tiles go straight from the pool to LDS (global_load_lds_dwordx4): wave w copies
     // keys 16 w .. 16 w + 15 of a tile, which lie in one page (pages hold >= 16 keys), 4 rows
     // per copy; lane i of copy c writes row 16 w + 4 c + i / 16 at physical chunk i % 16, so it
-    // reads logical chunk (i % 16) ^ swz(row). Keys at or past the context copy the context's
-    // last key: their scores are masked, so they add 0 x a finite value. A page outside the
-    // table or the pool sets fault bit 2 and copies pool row 0 instead.
+    // reads logical chunk (i % 16) ^ swzk(row) of K and (i % 16) ^ swz(row) of V. Keys at or
+    // past the context copy the context's last key: their scores are masked, so they add
+    // 0 x a finite value. A page outside the table or the pool sets fault bit 2 and copies pool
+    // row 0 instead.
     // The table entry of a tile is read one step before its copies and used only then: using
     // it in the step that reads it would wait for the copies issued just before (memory
     // loads complete in issue order), which would serialise every tile's copies with the
@@ -170,10 +175,10 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
         for (int c = 0; c < 4; ++c) {
             const int r = 16 * wave + 4 * c + crow;  // row of the tile = key offset
             const int key = min(tile * BN + r, ctx - 1);
-            const long src = (page_row + (key & pmask)) * D + 8 * (cch ^ swz(r));
+            const long row_el = (page_row + (key & pmask)) * D;
             const unsigned dst = (unsigned)((16 * wave + 4 * c) * KV_ROW * 2);
-            copy_x4((const T*)a.k_pool + src, kb + dst);
-            copy_x4((const T*)a.v_pool + src, vb + dst);
+            copy_x4((const T*)a.k_pool + row_el + 8 * (cch ^ swzk(r)), kb + dst);
+            copy_x4((const T*)a.v_pool + row_el + 8 * (cch ^ swz(r)), vb + dst);
         }
     };
 
