@@ -28,6 +28,11 @@ import time
 SEED = 20261201
 MFMA_PEAK_BF16 = 2.5e15   # dense bf16 / fp16 MFMA, FLOP/s
 HBM_PEAK = 8.0e12         # bytes/s
+# FLOPs of one 64-token chunk of the chunked delta rule for one head (dk = dv = 128): K K^T and
+# Q K^T (2 x 64 x 64 x 128 x 2), K S0 and Q S0 (2 x 64 x 128 x 128 x 2), T R
+# (64 x 64 x 128 x 2), the triangular inverse (64^3 / 3 x 2), Aqk delta (64 x 64 x 128 x 2) and
+# the state update K^T delta (128 x 64 x 128 x 2): 10.66 MFLOP
+GDN_CHUNK_FLOPS = 4 * 64 * 64 * 128 * 2 + 3 * 64 * 128 * 128 * 2 + 64 ** 3 / 3 * 2
 
 
 def parse():
@@ -76,7 +81,7 @@ def kernel_rooflines(ctx, shape, n_seqs, seq_len, dtype, iters):
     import torch
 
     from huncho_amd import abi
-    from huncho_amd.ops import gated_delta_chunked, paged_prefill_attention, qk_norm_rope_kv_write
+    from huncho_amd.ops import gated_delta_chunked, gdn_fused, paged_prefill_attention, qk_norm_rope_kv_write
 
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(dev)
@@ -106,11 +111,25 @@ def kernel_rooflines(ctx, shape, n_seqs, seq_len, dtype, iters):
     attn_flops = 4.0 * hq * d * seq_len * (seq_len + 1) / 2 * n_seqs
     attn_bytes = n * (2 * hq + 2 * hkv) * d * 2
 
-    H = shape.lin_n_v_heads
-    qg = torch.nn.functional.normalize(torch.randn((n, shape.lin_n_k_heads, 128), generator=g, device=dev),
-                                       dim=-1)
-    kg = torch.nn.functional.normalize(torch.randn((n, shape.lin_n_k_heads, 128), generator=g, device=dev),
-                                       dim=-1).to(dtype)
+    # the fused Gated DeltaNet layer kernel the forward runs: in_proj rows [q | k | v | z]
+    # (8192 columns) and [b | a] rows as the GEMMs write them, conv weights, A_log, dt_bias
+    H, Hk = shape.lin_n_v_heads, shape.lin_n_k_heads
+    conv_dim = shape.conv_dim
+    mixed = (torch.randn((n, conv_dim + H * 128), generator=g, device=dev) * 0.5).to(dtype)
+    ba = torch.randn((n, 2 * H), generator=g, device=dev).to(dtype)
+    conv_w = (torch.randn((conv_dim, 4), generator=g, device=dev) * 0.3).to(dtype).float()
+    base_g = -torch.exp(torch.randn(H, generator=g, device=dev) * 0.1)
+    dt_bias = torch.randn(H, generator=g, device=dev) * 0.1
+    norm_w = 1.0 + torch.randn(128, generator=g, device=dev) * 0.02
+    z = mixed[:, conv_dim:]
+    fo = torch.empty((n, H, 128), dtype=dtype, device=dev)
+    t_fused = time_launches(lambda: gdn_fused(ctx, mixed, conv_w, ba, 0, H, base_g, dt_bias, z, norm_w, shape.eps,
+                                              cu, H, Hk, out=fo), iters, stream)
+    # per (token, head): q, k, v raw rows 3 x 256 B + z 256 B + b, a 4 B + output 256 B
+    fused_bytes = n * H * (3 * 256 + 256 + 4 + 256)
+
+    qg = torch.nn.functional.normalize(torch.randn((n, Hk, 128), generator=g, device=dev), dim=-1)
+    kg = torch.nn.functional.normalize(torch.randn((n, Hk, 128), generator=g, device=dev), dim=-1).to(dtype)
     qg = (qg * 128 ** -0.5).to(dtype)
     vg = torch.randn((n, H, 128), generator=g, device=dev).to(dtype)
     gg = -torch.nn.functional.softplus(torch.randn((n, H), generator=g, device=dev)) * 0.5
@@ -119,22 +138,72 @@ def kernel_rooflines(ctx, shape, n_seqs, seq_len, dtype, iters):
     t_gdn = time_launches(lambda: gated_delta_chunked(ctx, qg, kg, vg, gg, bb, cu, out=og), iters, stream)
     gdn_bytes = n * H * (4 * 128 * 2 + 8)
     chunks = math.ceil(seq_len / 64) * n_seqs * H
-    gdn_flops = chunks * 11.71e6
+    gdn_flops = chunks * GDN_CHUNK_FLOPS
     torch.cuda.synchronize()
     return {
         "attention": {"seconds": t_attn, "flops": attn_flops, "bytes": attn_bytes},
+        "delta_rule_fused": {"seconds": t_fused, "flops": gdn_flops, "bytes": fused_bytes},
         "delta_rule": {"seconds": t_gdn, "flops": gdn_flops, "bytes": gdn_bytes},
     }
 
 
+def kev_forward_flops(shape, lengths):
+    """Algorithmic FLOPs of one Kev forward: the projections (2 per weight per token, unpadded
+    widths), causal attention (4 Hq d per visible (query, key) pair) and the chunked delta rule
+    (GDN_CHUNK_FLOPS per 64-token chunk and head)."""
+    H, I, d = shape.hidden, shape.intermediate, shape.head_dim
+    Hv = shape.lin_n_v_heads
+    vd = Hv * shape.lin_v_dim
+    n = sum(lengths)
+    gemm = attn = gdn = 0.0
+    for t in shape.layer_types:
+        gemm += 2.0 * n * (H * 2 * I + I * H)  # MLP gate|up, down
+        if t == 0:
+            gemm += 2.0 * n * (H * (shape.conv_dim + vd + 2 * Hv) + vd * H)
+            gdn += sum(math.ceil(L / 64) for L in lengths) * Hv * GDN_CHUNK_FLOPS
+        else:
+            gemm += 2.0 * n * (H * (2 * shape.n_heads * d + 2 * shape.n_kv_heads * d) + shape.n_heads * d * H)
+            attn += sum(4.0 * shape.n_heads * d * L * (L + 1) / 2 for L in lengths)
+    return {"gemm": gemm, "attention": attn, "delta_rule": gdn, "total": gemm + attn + gdn}
+
+
+def host_info():
+    """This host's CPU as the baseline legs see it: logical CPUs (nproc), the CPUs this process
+    may run on (its affinity mask) and the model name from /proc/cpuinfo."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    return {"nproc": os.cpu_count() or 1, "affinity": affinity, "model": model}
+
+
+def default_threads(args):
+    """All-core leg threads: the affinity mask, capped at 16 (the host CPU share of one GPU)."""
+    return args.cpu_threads or max(1, min(16, host_info()["affinity"]))
+
+
+def timed(fn):
+    t0 = time.perf_counter()
+    fn()
+    return time.perf_counter() - t0
+
+
 def cpu_baseline(shape, weights, seq_len, threads, n_seqs=12):
-    """The CPU oracle's fp32 forward of a few sequences of the same model on this host."""
+    """The CPU oracle's fp32 forward of the same model on this host: an all-core leg over
+    n_seqs sequences (OpenMP over rows, heads and (sequence, head) chains) and a single-thread
+    leg over one sequence in the reference's scalar order."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    import numpy as np
-
     from oracle import oracle as O
+    from huncho_amd import abi
 
-    O.set_threads(threads)
     cfg = O.QwenConfig(hidden_size=shape.hidden, num_hidden_layers=shape.n_layers,
                        num_attention_heads=shape.n_heads, num_key_value_heads=shape.n_kv_heads,
                        head_dim=shape.head_dim, intermediate_size=shape.intermediate, vocab_size=shape.vocab,
@@ -144,17 +213,93 @@ def cpu_baseline(shape, weights, seq_len, threads, n_seqs=12):
                        rope_theta=shape.rope_theta, partial_rotary_factor=shape.rotary_dim / shape.head_dim)
     f = {k: O.bf16_to_f32(v).reshape(v.shape) for k, v in weights.items()}
     model = O.QwenModel(cfg, f, bf16=False)
-    from huncho_amd import abi
-
     seqs = [abi.synth_uniform_int(SEED, 900 + i, seq_len, 0, shape.vocab - 1) for i in range(n_seqs)]
-    t0 = time.perf_counter()
-    for ids in seqs:
-        h = model.forward(ids)
-        _ = h[-1] @ f["decision_head.weight"].T
-    dt = time.perf_counter() - t0
+    head_w = f["decision_head.weight"]
+
+    def run(rows):
+        for ids in rows:
+            _ = model.forward(ids)[-1] @ head_w.T
+
+    O.set_threads(threads)
+    dt = timed(lambda: run(seqs))
+    O.set_threads(1)
+    dt1 = timed(lambda: run(seqs[:1]))
+    O.set_threads(threads)
+    hi = host_info()
     return {"value": round(n_seqs * seq_len / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{n_seqs} sequences x {seq_len} tokens of the same Kev-shaped model (all 24 layers + head), "
-                      f"fp32 CPU oracle forward, {threads} OpenMP threads, {dt:.2f} s"}
+                      f"fp32 CPU oracle forward, {threads} OpenMP threads, {dt:.2f} s",
+            "host": hi,
+            "single_thread": {"value": round(seq_len / dt1, 2), "unit": "tokens/s", "cores": 1,
+                              "sample": f"1 sequence x {seq_len} tokens, 1 thread, {dt1:.2f} s"}}
+
+
+def cpu_kernel_baselines(threads):
+    """The oracle's attention and delta-rule kernels on this host, per kernel config: GQA causal
+    attention fp32 (T 256, 16/8 heads x 128, pages of 16, identity table), the gated delta rule
+    fp32 (T 512, 16 heads, 128 x 128 state) and, as a bounded sample of the varlen bf16 batch,
+    its first 4 sequences. Each at `threads` threads and at 1 thread."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import numpy as np
+
+    from oracle import oracle as O
+
+    out = {}
+    rng = np.random.default_rng(SEED)
+    # attention, fp32, T = 256
+    T, hq, hkv, d, P = 256, 16, 8, 128, 16
+    q = rng.standard_normal((T, hq, d), dtype=np.float32)
+    kp = rng.standard_normal((T // P, hkv, P, d), dtype=np.float32)
+    vp = rng.standard_normal((T // P, hkv, P, d), dtype=np.float32)
+    bt = np.arange(T // P, dtype=np.int32)[None]
+    cu, lens = np.array([0, T], np.int32), np.array([T], np.int32)
+    fl = 4.0 * hq * d * T * (T + 1) / 2
+    for nt in (threads, 1):
+        O.set_threads(nt)
+        reps = 5
+        dt = timed(lambda: [O.paged_attention(q, kp, vp, bt, cu, lens, P, d ** -0.5) for _ in range(reps)]) / reps
+        out.setdefault("attention_fp32_T256", {})[f"threads_{nt}"] = {"seconds": round(dt, 5),
+                                                                       "gflops": round(fl / dt / 1e9, 2)}
+    # delta rule, fp32, T = 512
+    T, H = 512, 16
+    qd = rng.standard_normal((T, H, 128), dtype=np.float32)
+    kd = rng.standard_normal((T, H, 128), dtype=np.float32)
+    qd /= np.linalg.norm(qd, axis=-1, keepdims=True)
+    kd /= np.linalg.norm(kd, axis=-1, keepdims=True)
+    vd = rng.standard_normal((T, H, 128), dtype=np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((T, H))))).astype(np.float32)
+    gd = (-np.log1p(np.exp(rng.standard_normal((T, H)))) * 0.5).astype(np.float32)
+    cu = np.array([0, T], np.int32)
+    fl = T * H * (7 * 128 * 128 + 2 * 128)
+    for nt in (threads, 1):
+        O.set_threads(nt)
+        reps = 3
+        dt = timed(lambda: [O.gated_delta_rule(qd, kd, vd, gd, beta, cu) for _ in range(reps)]) / reps
+        out.setdefault("delta_rule_fp32_T512", {})[f"threads_{nt}"] = {"seconds": round(dt, 5),
+                                                                        "gflops": round(fl / dt / 1e9, 2)}
+    # varlen paged bf16 attention: the first 4 of 32 sequences (lengths uniform in [64, 2048])
+    from huncho_amd import abi
+
+    lengths = [int(x) for x in abi.synth_uniform_int(SEED, 960, 32, 64, 2048)][:4]
+    n = sum(lengths)
+    pages = [(L + P - 1) // P for L in lengths]
+    n_pages = sum(pages)  # a pool of just these sequences' pages, in a seeded permutation
+    perm = abi.synth_permutation(SEED, 961, n_pages)
+    btv = np.full((4, max(pages)), -1, np.int32)
+    k0 = 0
+    for s_, np_ in enumerate(pages):
+        btv[s_, :np_] = perm[k0:k0 + np_]
+        k0 += np_
+    qb = O.bf16_bits(rng.standard_normal((n, hq, d), dtype=np.float32))
+    kpb = O.bf16_bits(rng.standard_normal((n_pages, hkv, P, d), dtype=np.float32))
+    vpb = O.bf16_bits(rng.standard_normal((n_pages, hkv, P, d), dtype=np.float32))
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    fl = sum(4.0 * hq * d * L * (L + 1) / 2 for L in lengths)
+    O.set_threads(threads)
+    dt = timed(lambda: O.paged_attention(qb, kpb, vpb, btv, cu, np.array(lengths, np.int32), P, d ** -0.5))
+    out["varlen_attention_bf16_4seqs"] = {"lengths": lengths, f"threads_{threads}": {
+        "seconds": round(dt, 5), "gflops": round(fl / dt / 1e9, 2)}}
+    return out
 
 
 def laya_lengths(n_seqs):
@@ -220,14 +365,23 @@ def laya_cpu_baseline(shape, weights, threads, n_rows=3, n_tokens=2048):
     f = {k: O.bf16_to_f32(v).reshape(v.shape) for k, v in weights.items()}
     model = O.BertModel(cfg, f)
     rows = [abi.synth_uniform_int(SEED, 902 + i, n_tokens, 0, shape.vocab - 1).tolist() for i in range(n_rows)]
-    t0 = time.perf_counter()
-    for ids in rows:
-        h = model.forward([ids])[0]
-        _ = f["head.weight"] @ h.mean(0)
-    dt = time.perf_counter() - t0
+
+    def run(rs):
+        for ids in rs:
+            h = model.forward([ids])[0]
+            _ = f["head.weight"] @ h.mean(0)
+
+    dt = timed(lambda: run(rows))
+    O.set_threads(1)
+    short = [rows[0][:256]]
+    dt1 = timed(lambda: run(short))
+    O.set_threads(threads)
     return {"value": round(n_rows * n_tokens / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{n_rows} sequences x {n_tokens} tokens of the same ModernBERT-base-shaped encoder (all 22 "
-                      f"layers + mean-pooled head), fp32 CPU oracle forward, {threads} OpenMP threads, {dt:.2f} s"}
+                      f"layers + mean-pooled head), fp32 CPU oracle forward, {threads} OpenMP threads, {dt:.2f} s",
+            "host": host_info(),
+            "single_thread": {"value": round(256 / dt1, 2), "unit": "tokens/s", "cores": 1,
+                              "sample": f"1 sequence x 256 tokens, 1 thread, {dt1:.2f} s"}}
 
 
 def run_laya(args, dtype):
@@ -300,8 +454,8 @@ def run_laya(args, dtype):
         "device": {"name": info.name.decode(), "cus": info.compute_units, "clock_mhz": info.clock_khz // 1000},
     }
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        log(f"CPU baseline with {threads} threads")
+        threads = default_threads(args)
+        log(f"CPU baseline with {threads} threads and 1 thread")
         line["cpu_baseline"] = laya_cpu_baseline(shape, weights, threads)
     print(json.dumps(line), flush=True)
 
@@ -401,15 +555,24 @@ def run_kev(args, dtype):
     log(f"{ms:.2f} ms/step; first row calibrated probabilities {np.round(probs, 4).tolist()}")
 
     kr = kernel_rooflines(ctx, shape, args.batch, args.seq_len, dtype, args.kernel_iters)
-    a, gd = kr["attention"], kr["delta_rule"]
+    a, gf, gd = kr["attention"], kr["delta_rule_fused"], kr["delta_rule"]
     attn_achieved = a["flops"] / a["seconds"] / 1e12
-    gdn_achieved = gd["bytes"] / gd["seconds"] / 1e9
-    log(f"attention {a['seconds'] * 1e6:.1f} us/launch, delta rule {gd['seconds'] * 1e6:.1f} us/launch")
+    log(f"attention {a['seconds'] * 1e6:.1f} us/launch, fused delta rule {gf['seconds'] * 1e6:.1f} us/launch, "
+        f"standalone delta rule {gd['seconds'] * 1e6:.1f} us/launch")
     measured = load_traffic("kev") if (args.batch, args.seq_len, args.dtype) == (64, 512, "bf16") else {}
     traffic_of = lambda k: sum(measured[k]) if k in measured else None
+    fw = kev_forward_flops(shape, lengths)
+    step_s = elapsed / args.steps
+
+    def hbm_line(kernel, r, key):
+        return {"kernel": kernel, "bound": "hbm", "achieved": round(r["bytes"] / r["seconds"] / 1e9, 1),
+                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(r["bytes"] / r["seconds"] / HBM_PEAK, 4),
+                "traffic": traffic_of(key), "us_per_launch": round(r["seconds"] * 1e6, 2),
+                "bytes_per_launch": r["bytes"], "tflops": round(r["flops"] / r["seconds"] / 1e12, 2)}
+
     line = {
         "metric": "prefill tokens/s (Kev-shaped 64x512 bf16); attn TFLOP/s as % of MFMA peak",
-        "value": round(n_tokens / (elapsed / args.steps), 1),
+        "value": round(n_tokens / step_s, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -425,23 +588,24 @@ def run_kev(args, dtype):
                    "layer_pattern": "3 gated-delta-rule : 1 gated GQA attention", "attn_heads": "16q/8kv x 128",
                    "gdn_heads": "16 x 128", "mlp": "SwiGLU 3584", "vocab": shape.vocab, "page_size": shape.page_size,
                    "decision_head": shape.n_out},
+        "forward": {"tflops": round(fw["total"] / step_s / 1e12, 2),
+                    "frac_of_mfma_peak": round(fw["total"] / step_s / MFMA_PEAK_BF16, 4),
+                    "tflop_per_step": {k: round(v / 1e12, 4) for k, v in fw.items()}},
         "roofline": {"kernel": "paged_prefill_attn", "bound": "mfma", "achieved": round(attn_achieved, 2),
                      "peak": MFMA_PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                      "frac": round(attn_achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": traffic_of("attention"),
                      "us_per_launch": round(a["seconds"] * 1e6, 2), "flops_per_launch": a["flops"],
                      "hbm_frac": round(a["bytes"] / a["seconds"] / HBM_PEAK, 4)},
-        "roofline_delta_rule": {"kernel": "gdn_chunk16", "bound": "hbm", "achieved": round(gdn_achieved, 1),
-                                "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                                "frac": round(gd["bytes"] / gd["seconds"] / HBM_PEAK, 4),
-                                "traffic": traffic_of("delta_rule"),
-                                "us_per_launch": round(gd["seconds"] * 1e6, 2), "bytes_per_launch": gd["bytes"],
-                                "tflops": round(gd["flops"] / gd["seconds"] / 1e12, 2)},
+        "roofline_delta_rule": hbm_line("gdn_chunk16<fused> (the forward's Gated DeltaNet layer kernel)", gf,
+                                        "delta_rule_fused"),
+        "roofline_delta_rule_standalone": hbm_line("gdn_chunk16 (standalone recurrence)", gd, "delta_rule"),
         "device": {"name": info.name.decode(), "cus": info.compute_units, "clock_mhz": info.clock_khz // 1000},
     }
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        log(f"CPU baseline with {threads} threads")
+        threads = default_threads(args)
+        log(f"CPU baseline with {threads} threads and 1 thread")
         line["cpu_baseline"] = cpu_baseline(shape, weights, args.seq_len, threads)
+        line["cpu_kernel_baselines"] = cpu_kernel_baselines(threads)
     print(json.dumps(line), flush=True)
 
 

@@ -19,7 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_build" / "libhuncho_rocm.so"
 
 HK_OK, HK_ERR_INVALID, HK_ERR_UNSUPPORTED, HK_ERR_DEVICE, HK_ERR_NOMEM = 0, 1, 2, 3, 4
 HK_F32, HK_BF16, HK_F16 = 0, 1, 2
-HK_FAULT_SEQLENS, HK_FAULT_PAGE, HK_FAULT_ROPE, HK_FAULT_TOKEN = 1, 2, 4, 8
+HK_FAULT_SEQLENS, HK_FAULT_PAGE, HK_FAULT_ROPE, HK_FAULT_TOKEN, HK_FAULT_RANGE = 1, 2, 4, 8, 16
 
 vp = C.c_void_p
 i32p = C.POINTER(C.c_int32)
@@ -63,6 +63,11 @@ class BertConfig(C.Structure):
 BERT_LAYER_FIELDS = ["attn_norm", "wqkv", "wo", "mlp_norm", "wi", "wo2"]
 
 
+class KevReadout(C.Structure):
+    _fields_ = [("cu_positions_host", i32p), ("positions_host", i32p), ("cu_positions_dev", vp),
+                ("positions_dev", vp), ("hidden_dev", vp), ("pointer_scores_dev", vp)]
+
+
 class BertLayerWeights(C.Structure):
     _fields_ = [(n, vp) for n in BERT_LAYER_FIELDS]
 
@@ -80,6 +85,8 @@ SIGNATURES = {
     "hk_ctx_last_error": (C.c_char_p, [vp]),
     "hk_ctx_device_info": (I, [vp, C.POINTER(DeviceInfo)]),
     "hk_ctx_take_faults": (I, [vp, C.POINTER(I)]),
+    "hk_ctx_set_gemm_autotune": (I, [vp, I]),
+    "hk_ctx_gemm_plans": (I, [vp, C.c_char_p, SZ, C.POINTER(SZ)]),
     "hk_buffer_alloc": (I, [vp, C.c_size_t, C.POINTER(vp)]),
     "hk_buffer_free": (I, [vp, vp]),
     "hk_memcpy_h2d": (I, [vp, vp, vp, C.c_size_t]),
@@ -102,6 +109,10 @@ SIGNATURES = {
     "hk_kev_model_destroy": (I, [vp]),
     "hk_kev_workspace_size": (I, [vp, I, I, C.POINTER(SZ)]),
     "hk_kev_forward": (I, [vp, vp, vp, i32p, I, vp, I, I, vp, SZ, vp, vp]),
+    "hk_kev_model_set_pointer_head": (I, [vp, I, vp, vp, vp, vp]),
+    "hk_kev_forward_readout": (I, [vp, vp, vp, i32p, I, vp, I, I, vp, SZ, C.POINTER(KevReadout), vp]),
+    "hk_kev_forward_cached_readout": (I, [vp, C.POINTER(C.c_uint64), I, vp, vp, i32p, vp, SZ,
+                                          C.POINTER(KevReadout), vp]),
     "hk_kev_cache_create": (I, [vp, I, I, C.POINTER(vp)]),
     "hk_kev_cache_destroy": (I, [vp]),
     "hk_kev_cache_open": (I, [vp, C.POINTER(C.c_uint64)]),
@@ -176,6 +187,18 @@ class Context:
         f = C.c_int(0)
         self.check(lib().hk_ctx_take_faults(self.h, C.byref(f)))
         return f.value
+
+    def set_gemm_autotune(self, enable: bool) -> None:
+        """Opt in (or out) of timing every GEMM solution for shapes first seen afterwards."""
+        self.check(lib().hk_ctx_set_gemm_autotune(self.h, 1 if enable else 0))
+
+    def gemm_plans(self) -> str:
+        """One line per cached GEMM plan: shape, hipBLASLt solution index and how it was chosen."""
+        need = SZ(0)
+        self.check(lib().hk_ctx_gemm_plans(self.h, None, 0, C.byref(need)))
+        buf = C.create_string_buffer(need.value)
+        self.check(lib().hk_ctx_gemm_plans(self.h, buf, need.value, C.byref(need)))
+        return buf.value.decode()
 
     def device_info(self) -> DeviceInfo:
         info = DeviceInfo()

@@ -429,12 +429,14 @@ extern "C" int hk_paged_prefill_attention(hk_ctx* ctx, int dtype, const void* q,
     REQUIRE(!gate || gate_head >= head_dim, "gate stride too small");
     REQUIRE(scale > 0 && isfinite(scale), "scale must be positive and finite");
     {  // vector widths of the kernels' loads and stores (elements): q rows, o / gate rows
-        const long qv = dtype == HK_F32 ? 2 : 8, ov = 4, esz = dtype == HK_F32 ? 4 : 2;
+        // 16-bit: 16-byte q loads, gate loads and O stores (8 elements); fp32: 8-byte q loads
+        // and 16-byte O stores (4 elements; the gate is read per element)
+        const long qv = dtype == HK_F32 ? 2 : 8, ov = dtype == HK_F32 ? 4 : 8, esz = dtype == HK_F32 ? 4 : 2;
         const uintptr_t qa = (uintptr_t)q, oa = (uintptr_t)o, ga = (uintptr_t)gate;
         REQUIRE(q_tok % qv == 0 && q_head % qv == 0 && qa % (qv * esz) == 0, "q rows must be %ld-element aligned", qv);
-        REQUIRE(o_tok % ov == 0 && o_head % ov == 0 && oa % (ov * esz) == 0, "o rows must be 4-element aligned");
+        REQUIRE(o_tok % ov == 0 && o_head % ov == 0 && oa % (ov * esz) == 0, "o rows must be %ld-element aligned", ov);
         REQUIRE(!gate || (gate_tok % ov == 0 && gate_head % ov == 0 && ga % (ov * esz) == 0),
-                "gate rows must be 4-element aligned");
+                "gate rows must be %ld-element aligned", ov);
         REQUIRE((((uintptr_t)k_pool | (uintptr_t)v_pool) & 15) == 0, "K/V pools must be 16-byte aligned");
     }
     if (max_q_len == 0 || n_tokens == 0) return HK_OK;

@@ -23,6 +23,9 @@ struct hk_ctx {
 int hk_fail(hk_ctx* ctx, int code, const char* fmt, ...);
 int hk_check_hip(hk_ctx* ctx, hipError_t e, const char* what);
 void hk_blas_release(hk_ctx* ctx);
+// Creates the context's hipBLASLt handle and GEMM workspace (once; called at model creation so
+// that no forward allocates).
+int hk_blas_prepare(hk_ctx* ctx);
 float hk_host_f16_to_f32(uint16_t b);
 uint16_t hk_host_f32_to_f16(float x);
 

@@ -115,6 +115,7 @@ extern "C" int hk_bert_model_create(hk_ctx* ctx, int dtype, const hk_bert_config
         return hk_fail(ctx, HK_ERR_INVALID, "invalid ModernBERT configuration");
     if (c.n_out > 0 && !head_w) return hk_fail(ctx, HK_ERR_INVALID, "missing head weight");
     hipSetDevice(ctx->device);
+    if (int rc = hk_blas_prepare(ctx)) return rc;  // GEMM handle + workspace, before any forward
     hk_bert_model* m = new hk_bert_model();
     m->ctx = ctx;
     m->dtype = dtype;

@@ -3,16 +3,24 @@
 // Row-major Y[n][out] = alpha * X[n][in] . W[out][in]^T + beta * C is the column-major
 // product Y^T = W . X^T: m = out, n = n, k = in, op(A) = T on the weight, op(B) = N on the
 // activations. bf16 or fp16 operands with fp32 accumulation (HIPBLAS_COMPUTE_32F), or fp32.
-// Plans (descriptors + the fastest algorithm for the shape) are cached per shape. On first
-// use of a shape every solution hipBLASLt offers for the layout (the heuristic's list plus
-// the full solution list, filtered by matmulIsAlgoSupported) is timed, and the best 8 again
-// in interleaved rounds. The workspace is owned by the context and allocated on the first
-// GEMM.
+//
+// Plans (descriptors + one algorithm per shape) are cached per shape. The algorithm is a
+// deterministic function of the shape: the solution index pinned for it in kPinned (measured
+// on MI355X with this hipBLASLt) when it supports the problem, else the heuristic's first
+// choice. Building a plan allocates no device memory, times nothing and does not synchronise,
+// so a forward stays stream-ordered on its first call for a batch shape. Timing every
+// candidate is opt-in (hk_ctx_set_gemm_autotune): it allocates scratch, synchronises, and its
+// choice then depends on the device's timing. The handle and the workspace belong to the
+// context and are created by hk_blas_prepare (model creation), never inside a forward.
 #include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
+#include <stdio.h>
+#include <string.h>
+
 #include <algorithm>
 #include <map>
+#include <string>
 #include <tuple>
 #include <utility>
 #include <vector>
@@ -26,6 +34,18 @@ struct Plan {
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr, d = nullptr;
     hipblasLtMatmulAlgo_t algo{};
     size_t ws = 0;
+    int index = -1;      // hipBLASLt solution index
+    const char* source = "";  // "pinned", "heuristic" or "timed"
+};
+
+// Solution indices pinned per (dtype, out, n, in, C operand) at the Kev-shaped 64 x 512 token
+// batch, measured on MI355X (gfx950) with ROCm 7.2's hipBLASLt by timing every supported
+// solution (hk_ctx_set_gemm_autotune) and keeping the fastest.
+struct Pinned {
+    int dtype, out, n, in, has_c, index;
+};
+const Pinned kPinned[] = {
+    {0, 0, 0, 0, 0, -1},  // (sentinel)
 };
 
 typedef std::tuple<int, int, int, int, long, long, long, long, int> Key;
@@ -36,6 +56,7 @@ struct hk_blas {
     hipblasLtHandle_t handle = nullptr;
     void* workspace = nullptr;
     size_t ws_bytes = 0;
+    bool autotune = false;
     std::map<Key, Plan> plans;
 };
 
@@ -58,7 +79,7 @@ void hk_blas_release(hk_ctx* ctx) {
     ctx->blas = nullptr;
 }
 
-static int blas_init(hk_ctx* ctx) {
+int hk_blas_prepare(hk_ctx* ctx) {
     if (ctx->blas) return HK_OK;
     hk_blas* b = new hk_blas();
     if (hipblasLtCreate(&b->handle) != HIPBLAS_STATUS_SUCCESS) {
@@ -164,7 +185,7 @@ static int pick_fastest(hk_ctx* ctx, Plan& p, std::vector<std::pair<hipblasLtMat
 int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, long ldx, const void* w, long ldw,
                 void* y, long ldy, const void* c, long ldc, float alpha, float beta) {
     if (n == 0 || out == 0) return HK_OK;
-    if (int rc = blas_init(ctx)) return rc;
+    if (!ctx->blas) return hk_fail(ctx, HK_ERR_INVALID, "GEMM state not prepared (hk_blas_prepare at model creation)");
     hk_blas* B = ctx->blas;
     const bool has_c = c != nullptr && beta != 0.0f;
     if (!has_c) {
@@ -204,23 +225,94 @@ int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, l
             if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
             return hk_fail(ctx, HK_ERR_UNSUPPORTED, "no hipBLASLt algorithm for %dx%dx%d", out, n, in);
         }
-        auto cands = candidates(ctx, p, t, res, returned);
-        if (cands.empty()) {
+        auto destroy = [&]() {
             hipblasLtMatrixLayoutDestroy(p.a);
             hipblasLtMatrixLayoutDestroy(p.b);
             hipblasLtMatrixLayoutDestroy(p.c);
             hipblasLtMatrixLayoutDestroy(p.d);
             hipblasLtMatmulDescDestroy(p.desc);
-            return hk_fail(ctx, HK_ERR_UNSUPPORTED, "no usable hipBLASLt algorithm for %dx%dx%d", out, n, in);
+        };
+        if (B->autotune) {
+            auto cands = candidates(ctx, p, t, res, returned);
+            if (cands.empty()) {
+                destroy();
+                return hk_fail(ctx, HK_ERR_UNSUPPORTED, "no usable hipBLASLt algorithm for %dx%dx%d", out, n, in);
+            }
+            const int best = pick_fastest(ctx, p, cands, dtype, n, x, w, ldy, ldc, has_c);
+            p.algo = cands[best].first;
+            p.ws = cands[best].second;
+            p.source = "timed";
+        } else {
+            // the pinned solution when it supports this problem, else the heuristic's first
+            // usable choice
+            bool chosen = false;
+            for (const Pinned& e : kPinned) {
+                if (e.index < 0 || e.dtype != dtype || e.out != out || e.n != n || e.in != in ||
+                    e.has_c != (has_c ? 1 : 0) || ldw != in || ldx != in || ldy != out || ldc != out)
+                    continue;
+                std::vector<int> idx{e.index};
+                std::vector<hipblasLtMatmulHeuristicResult_t> got;
+                if (hipblaslt_ext::getAlgosFromIndex(B->handle, idx, got) != HIPBLAS_STATUS_SUCCESS || got.empty())
+                    break;
+                const float one = 1.0f, zero = 0.0f;
+                size_t ws = 0;
+                if (hipblaslt_ext::matmulIsAlgoSupported(B->handle, p.desc, &one, p.a, p.b, &zero, p.c, p.d,
+                                                         got[0].algo, ws) == HIPBLAS_STATUS_SUCCESS &&
+                    ws <= B->ws_bytes) {
+                    p.algo = got[0].algo;
+                    p.ws = ws;
+                    p.source = "pinned";
+                    chosen = true;
+                }
+                break;
+            }
+            for (int i = 0; !chosen && i < returned; ++i) {
+                if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > B->ws_bytes) continue;
+                p.algo = res[i].algo;
+                p.ws = res[i].workspaceSize;
+                p.source = "heuristic";
+                chosen = true;
+            }
+            if (!chosen) {
+                destroy();
+                return hk_fail(ctx, HK_ERR_UNSUPPORTED, "no usable hipBLASLt algorithm for %dx%dx%d", out, n, in);
+            }
         }
-        const int best = pick_fastest(ctx, p, cands, dtype, n, x, w, ldy, ldc, has_c);
-        p.algo = cands[best].first;
-        p.ws = cands[best].second;
+        p.index = hipblaslt_ext::getIndexFromAlgo(p.algo);
         it = B->plans.emplace(key, p).first;
     }
     Plan& p = it->second;
     hipblasStatus_t st = hipblasLtMatmul(B->handle, p.desc, &alpha, w, p.a, x, p.b, &beta, c, p.c, y, p.d, &p.algo,
                                          B->workspace, p.ws, ctx->stream);
     if (st != HIPBLAS_STATUS_SUCCESS) return hk_fail(ctx, HK_ERR_DEVICE, "hipblasLtMatmul failed (%d)", (int)st);
+    return HK_OK;
+}
+
+extern "C" int hk_ctx_set_gemm_autotune(hk_ctx* ctx, int enable) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = hk_blas_prepare(ctx)) return rc;
+    ctx->blas->autotune = enable != 0;
+    return HK_OK;
+}
+
+extern "C" int hk_ctx_gemm_plans(hk_ctx* ctx, char* buf, size_t len, size_t* needed) {
+    if (!ctx) return HK_ERR_INVALID;
+    std::string out;
+    if (ctx->blas) {
+        char line[160];
+        for (auto& kv : ctx->blas->plans) {
+            const Key& k = kv.first;
+            snprintf(line, sizeof line, "dtype=%d out=%d n=%d in=%d ldw=%ld ldx=%ld ldy=%ld ldc=%ld c=%d index=%d %s\n",
+                     std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k), std::get<5>(k),
+                     std::get<6>(k), std::get<7>(k), std::get<8>(k), kv.second.index, kv.second.source);
+            out += line;
+        }
+    }
+    if (needed) *needed = out.size() + 1;
+    if (buf && len) {
+        const size_t n = out.size() < len - 1 ? out.size() : len - 1;
+        memcpy(buf, out.data(), n);
+        buf[n] = 0;
+    }
     return HK_OK;
 }

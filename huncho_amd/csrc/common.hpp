@@ -75,6 +75,9 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const void* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p);
 }
 
+// Device fault bits shared with the C ABI (HK_FAULT_*).
+constexpr int FAULT_SEQLENS = 1, FAULT_PAGE = 2, FAULT_ROPE = 4, FAULT_TOKEN = 8, FAULT_RANGE = 16;
+
 // Kernel dtype codes shared with the C ABI.
 enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
@@ -110,11 +113,10 @@ constexpr int VMCNT0 = 0x0F70;  // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left a
 // One global_load_lds_dwordx4: lane l copies the 16 bytes at g to LDS byte address lds + 16 l
 // (lds wave-uniform, in M0). Issued from inline assembly so that the compiler does not make
 // every later LDS access wait for the copy; a kernel that uses it waits for its copies
-// explicitly (s_waitcnt vmcnt) before the barrier that publishes them. Nothing else in these
-// kernels uses M0.
+// explicitly (s_waitcnt vmcnt) before the barrier that publishes them. The LDS address is an
+// M0 operand ("{m0}"), so the compiler sets M0 itself and knows the asm reads it.
 __device__ __forceinline__ void copy_x4(const void* g, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
-                 : "memory");
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 // LDS byte address of a pointer into shared memory
 __device__ __forceinline__ unsigned lds_address(const void* p) {

@@ -19,11 +19,11 @@
 //               RMSNorm rms(o) * w * silu(z) (193-201) -> out_proj input
 // so one kernel streams each layer's q|k|v|z|b|a once and writes one output row per token.
 //
-// Work split: one workgroup of 8 waves per (sequence, value head), two workgroups per CU
-// (79,360 B of LDS each, <= 128 registers per lane), so 4 waves share each SIMD. Wave w owns
-// value columns 16w..16w+15 of the fp32 state S [128 x 128], held for the whole sequence in
-// eight 16x16 MFMA accumulators (v_mfma_f32_16x16x32_{bf16,f16}; lane l: column l % 16,
-// rows 4 (l / 16) + r). Intermediates (K S, R, delta) stay in accumulator layout and feed the
+// Work split: one workgroup of 4 waves (256 threads) per (sequence, value head), two
+// workgroups per CU (79,360 B of LDS each, <= 256 registers per lane), so 2 waves share each
+// SIMD. Wave w owns value columns 32w..32w+31 of the fp32 state S [128 x 128] as two 16-column
+// tiles, held for the whole sequence in sixteen 16x16 MFMA accumulators
+// (v_mfma_f32_16x16x32_{bf16,f16}; lane l: column l % 16, rows 4 (l / 16) + r). Intermediates (K S, R, delta) stay in accumulator layout and feed the
 // next product as its B operand: each product's reduction index is permuted to the
 // accumulator's row order (element e of lane group q <-> index 32 s + 4 q + e, or
 // 32 s + 16 + 4 q + e - 4 for e >= 4), and the A operands are read from LDS in that order.
@@ -161,15 +161,22 @@ __device__ __forceinline__ typename M16<T>::v4 ld_a4(const float* Am, int r, int
 
 template <typename T, bool FUSED>
 __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa) {
-    typedef typename M16<T>::v8 v8;
-    typedef typename M16<T>::v4 v4;
-    typedef typename M16<T>::v2 v2;
+    // MFMA operands and LDS tiles are fp16 (CT) for both activation dtypes: bf16 activations
+    // are exact in fp16 (inside its range), and every intermediate rounded to an operand (R, A,
+    // T, delta, the state S, Aqk) keeps 11 significant bits instead of bf16's 8. The reference
+    // runs this recurrence in fp32 (delta_cpu.rs:95-131); its bf16 storage points (conv output,
+    // normalised q and k, beta, the recurrence output) are rounded to T as before.
+    typedef f16 CT;
+    typedef typename M16<CT>::v8 v8;
+    typedef typename M16<CT>::v4 v4;
+    typedef typename M16<T>::v8 tv8;
+    typedef typename M16<T>::v2 tv2;
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    T* Qs = (T*)smem;                     // [64][RS]
-    T* Ks = Qs + CH * RS;                 // [64][RS]
-    T* Vs = Ks + CH * RS;                 // [64][RS]; O staging in P3
+    CT* Qs = (CT*)smem;                   // [64][RS]
+    CT* Ks = Qs + CH * RS;                // [64][RS]
+    CT* Vs = Ks + CH * RS;                // [64][RS]; O staging in P3
     float* Am = (float*)(Vs + CH * RS);   // [64][AS]: A, then the diagonal blocks of T
-    T* Aq = (T*)(Am + CH * AS);           // [64][TS]
+    CT* Aq = (CT*)(Am + CH * AS);         // [64][TS]
     float* Gs = (float*)(Aq + CH * TS);
     float* Bs = Gs + CH;
 
@@ -217,6 +224,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
     // mixed column mcol + 8 j
     const long mcol = (long)kh * 128 + wave * (long)fa.Hk * 128 + (wave == 2 ? (long)(h - kh) * 128 : 0);
 
+    bool range_bad = false;  // a non-finite output row (fp16 operand range exceeded)
     for (int c0 = 0; c0 < Tn; c0 += CH) {
         const int Lc = min(CH, Tn - c0);
         // lane indices re-formed every chunk, so the compiler builds the per-lane LDS
@@ -240,14 +248,14 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
             };
             // all three windows are loaded before the first conv, so the chunk waits for one
             // memory round trip
-            v8 raw[3][7];
+            tv8 raw[3][7];
 #pragma unroll
             for (int tsr = 0; tsr < 3; ++tsr)
 #pragma unroll
                 for (int i = 0; i < 7; ++i) {
                     const int p = c0 + r0 - 3 + i;
                     const int pc = p < 0 ? 0 : (p >= Tn ? Tn - 1 : p);
-                    raw[tsr][i] = *(const v8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + tcol(tsr));
+                    raw[tsr][i] = *(const tv8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + tcol(tsr));
                 }
             if (c0 + r0 == 0) {  // windows start 3 positions before the sequence
 #pragma unroll
@@ -260,30 +268,30 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
                             for (int e = 0; e < 8; ++e) raw[tsr][i][e] = hb[e * 3 + i];
                     } else {
 #pragma unroll
-                        for (int i = 0; i < 3; ++i) raw[tsr][i] = v8{};
+                        for (int i = 0; i < 3; ++i) raw[tsr][i] = tv8{};
                     }
                 }
             }
 #pragma unroll
             for (int tsr = 0; tsr < 3; ++tsr) {
                 const long mct = tcol(tsr);
-                T* dst = tsr == 0 ? Qs : tsr == 1 ? Ks : Vs;
+                CT* dst = tsr == 0 ? Qs : tsr == 1 ? Ks : Vs;
                 // taps (0, 1) and (2, 3) of each channel as 16-bit pairs (the weights are the
                 // model dtype's values, exact in T)
-                v2 w01[8], w23[8];
+                tv2 w01[8], w23[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const f32x4 w4 = *(const f32x4*)(fa.conv_w + (mct + e) * 4);
-                    w01[e] = v2{(T)w4[0], (T)w4[1]};
-                    w23[e] = v2{(T)w4[2], (T)w4[3]};
+                    w01[e] = tv2{(T)w4[0], (T)w4[1]};
+                    w23[e] = tv2{(T)w4[2], (T)w4[3]};
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float y[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const float acc = dot2(w23[e], v2{raw[tsr][i + 2][e], raw[tsr][i + 3][e]},
-                                               dot2(w01[e], v2{raw[tsr][i][e], raw[tsr][i + 1][e]}, 0.0f));
+                        const float acc = dot2(w23[e], tv2{raw[tsr][i + 2][e], raw[tsr][i + 3][e]},
+                                               dot2(w01[e], tv2{raw[tsr][i][e], raw[tsr][i + 1][e]}, 0.0f));
                         y[e] = silu(acc);
                     }
                     if (tsr < 2) {  // conv output stored in the activation dtype, then l2norm over
@@ -299,29 +307,33 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
 #pragma unroll
                         for (int e = 0; e < 8; ++e) y[e] = tsr == 0 ? (y[e] * inv) * fa.scale : y[e] * inv;
                     }
+                    // stored at the reference's rounding point (T), held exactly in CT
                     v8 o;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) o[e] = (T)y[e];
+                    for (int e = 0; e < 8; ++e) o[e] = (CT)rnd<T>(y[e]);
                     *(v8*)(dst + el(r0 + i, 8 * j)) = o;
                 }
             }
         } else {
             // 3 tensors x 64 rows x 16 chunks = 12 chunks per lane; 16 lanes per row
-            v8 x[12];
+            tv8 x[12];
 #pragma unroll
             for (int i = 0; i < 12; ++i) {
                 const int tsr = i >> 2, r = 16 * (i & 3) + (tid >> 4);
                 const T* src = tsr == 0 ? (const T*)a.q + (long)kh * DK
                              : tsr == 1 ? (const T*)a.k + (long)kh * DK : (const T*)a.v + (long)h * DV;
                 const long tok = tsr == 0 ? a.q_tok : tsr == 1 ? a.k_tok : a.v_tok;
-                x[i] = *(const v8*)(src + (long)(t0 + c0 + (r < Lc ? r : Lc - 1)) * tok + 8 * j);
-                if (r >= Lc) x[i] = v8{};
+                x[i] = *(const tv8*)(src + (long)(t0 + c0 + (r < Lc ? r : Lc - 1)) * tok + 8 * j);
+                if (r >= Lc) x[i] = tv8{};
             }
 #pragma unroll
             for (int i = 0; i < 12; ++i) {
                 const int tsr = i >> 2, r = 16 * (i & 3) + (tid >> 4);
-                T* dst = tsr == 0 ? Qs : tsr == 1 ? Ks : Vs;
-                *(v8*)(dst + el(r, 8 * j)) = x[i];
+                CT* dst = tsr == 0 ? Qs : tsr == 1 ? Ks : Vs;
+                v8 c;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) c[e] = (CT)f(x[i][e]);
+                *(v8*)(dst + el(r, 8 * j)) = c;
             }
         }
         if (wave == 3) {  // g (inclusive scan over the chunk) and beta
@@ -353,8 +365,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const v8 b = *(const v8*)(Ks + el(16 * si + j, 32 * ks + 8 * q4));
-                kk = M16<T>::mma(*(const v8*)(Ks + el(16 * ti + j, 32 * ks + 8 * q4)), b, kk);
-                qk = M16<T>::mma(*(const v8*)(Qs + el(16 * ti + j, 32 * ks + 8 * q4)), b, qk);
+                kk = M16<CT>::mma(*(const v8*)(Ks + el(16 * ti + j, 32 * ks + 8 * q4)), b, kk);
+                qk = M16<CT>::mma(*(const v8*)(Qs + el(16 * ti + j, 32 * ks + 8 * q4)), b, qk);
             }
             const int s = 16 * si + j, t4 = 16 * ti + 4 * q4;
             const float gs = Gs[s];
@@ -367,7 +379,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
                 const float ex = __expf(gt[r] - gs);
                 const float dec = s <= t ? ex : 0.0f;
                 Am[t * AS + s] = s < t ? bt[r] * dec * kk[r] : 0.0f;
-                Aq[t * TS + s] = (T)(dec * qk[r]);
+                Aq[t * TS + s] = (CT)(dec * qk[r]);
             }
         }
         for (int u = wave; u < 6; u += 4) {
@@ -377,7 +389,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * ti + 4 * q4 + r, s = 16 * si + j;
                 Am[t * AS + s] = 0.0f;
-                Aq[t * TS + s] = (T)0.0f;
+                Aq[t * TS + s] = (CT)0.0f;
             }
         }
         // per token tile tt and column tile cw: R = beta (V - e^G K S0), Og = e^G Q S0
@@ -387,7 +399,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
 #pragma unroll
             for (int cw = 0; cw < 2; ++cw)
 #pragma unroll
-                for (int s = 0; s < 4; ++s) Sb[cw][s] = pack2<T>(S[cw][2 * s], S[cw][2 * s + 1]);
+                for (int s = 0; s < 4; ++s) Sb[cw][s] = pack2<CT>(S[cw][2 * s], S[cw][2 * s + 1]);
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
                 f32x4 ksa[2], qsa[2];
@@ -395,12 +407,12 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
                 for (int cw = 0; cw < 2; ++cw) ksa[cw] = qsa[cw] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    const v8 kop = ld_pair<T>(Ks, 16 * tt + j, 32 * s + 4 * q4);
-                    const v8 qop = ld_pair<T>(Qs, 16 * tt + j, 32 * s + 4 * q4);
+                    const v8 kop = ld_pair<CT>(Ks, 16 * tt + j, 32 * s + 4 * q4);
+                    const v8 qop = ld_pair<CT>(Qs, 16 * tt + j, 32 * s + 4 * q4);
 #pragma unroll
                     for (int cw = 0; cw < 2; ++cw) {
-                        ksa[cw] = M16<T>::mma(kop, Sb[cw][s], ksa[cw]);
-                        qsa[cw] = M16<T>::mma(qop, Sb[cw][s], qsa[cw]);
+                        ksa[cw] = M16<CT>::mma(kop, Sb[cw][s], ksa[cw]);
+                        qsa[cw] = M16<CT>::mma(qop, Sb[cw][s], qsa[cw]);
                     }
                 }
                 const f32x4 gt = *(const f32x4*)(Gs + 16 * tt + 4 * q4);
@@ -415,8 +427,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float eg = __expf(gt[r]);
-                        // R rounded to the activation dtype: it is a 16-bit MFMA operand
-                        R[cw][tt][r] = rnd<T>(bt[r] * (f(vv[r]) - eg * ksa[cw][r]));
+                        // R rounded to CT: it is a 16-bit MFMA operand
+                        R[cw][tt][r] = rnd<CT>(bt[r] * (f(vv[r]) - eg * ksa[cw][r]));
                         Og[cw][tt][r] = eg * qsa[cw][r];
                     }
                 }
@@ -438,31 +450,32 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
             f32x4 x[2] = {R[0][i], R[1][i]};
 #pragma unroll
             for (int jj = 0; jj < i; ++jj) {
-                const v4 na = ld_a4<T, true>(Am, 16 * i + j, 16 * jj + 4 * q4);
+                const v4 na = ld_a4<CT, true>(Am, 16 * i + j, 16 * jj + 4 * q4);
 #pragma unroll
-                for (int cw = 0; cw < 2; ++cw) x[cw] = M16<T>::mma16(na, dbk[cw][jj], x[cw]);
+                for (int cw = 0; cw < 2; ++cw) x[cw] = M16<CT>::mma16(na, dbk[cw][jj], x[cw]);
             }
-            const v4 ti_ = ld_a4<T, false>(Am, 16 * i + j, 16 * i + 4 * q4);
+            const v4 ti_ = ld_a4<CT, false>(Am, 16 * i + j, 16 * i + 4 * q4);
 #pragma unroll
             for (int cw = 0; cw < 2; ++cw) {
-                dl[cw][i] = M16<T>::mma16(ti_, pack1<T>(x[cw]), f32x4{0.f, 0.f, 0.f, 0.f});
-                dbk[cw][i] = pack1<T>(dl[cw][i]);
+                dl[cw][i] = M16<CT>::mma16(ti_, pack1<CT>(x[cw]), f32x4{0.f, 0.f, 0.f, 0.f});
+                dbk[cw][i] = pack1<CT>(dl[cw][i]);
             }
 #pragma unroll
             for (int jj = 0; jj <= i; ++jj) {
                 const v4 aq = *(const v4*)(Aq + (16 * i + j) * TS + 16 * jj + 4 * q4);
 #pragma unroll
-                for (int cw = 0; cw < 2; ++cw) Og[cw][i] = M16<T>::mma16(aq, dbk[cw][jj], Og[cw][i]);
+                for (int cw = 0; cw < 2; ++cw) Og[cw][i] = M16<CT>::mma16(aq, dbk[cw][jj], Og[cw][i]);
             }
         }
         // O staged over V (dead since P1)
-        T* Os = Vs;
+        CT* Os = Vs;
 #pragma unroll
         for (int cw = 0; cw < 2; ++cw)
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) Os[el(16 * tt + 4 * q4 + r, 32 * wave + 16 * cw + j)] = (T)Og[cw][tt][r];
+                for (int r = 0; r < 4; ++r)  // the reference's output rounding (T), held exactly in CT
+                    Os[el(16 * tt + 4 * q4 + r, 32 * wave + 16 * cw + j)] = (CT)rnd<T>(Og[cw][tt][r]);
         const float glast = Gs[CH - 1];
         const float eglast = __expf(glast);
         v8 Db[2][2];
@@ -478,8 +491,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
         }
 #pragma unroll
         for (int cw = 0; cw < 2; ++cw) {
-            Db[cw][0] = pack2<T>(dl[cw][0], dl[cw][1]);
-            Db[cw][1] = pack2<T>(dl[cw][2], dl[cw][3]);
+            Db[cw][0] = pack2<CT>(dl[cw][0], dl[cw][1]);
+            Db[cw][1] = pack2<CT>(dl[cw][2], dl[cw][3]);
         }
         // S = e^{G_last} S + K^T (e^{G_last - G} delta). The A operand K^T[dk][token] comes
         // from transposing reads: source lane j addresses K row 32 ks + 4 q4 + j / 4 (+ 16
@@ -499,18 +512,18 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
                 const i16x4 hi = lds_read_tr16(Ks + el(kr + 16, 16 * rb + 4 * (j & 3)));
                 const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-                for (int cw = 0; cw < 2; ++cw) S[cw][rb] = M16<T>::mma(af, Db[cw][ks], S[cw][rb]);
+                for (int cw = 0; cw < 2; ++cw) S[cw][rb] = M16<CT>::mma(af, Db[cw][ks], S[cw][rb]);
             }
         // P4 operands that do not depend on O: the gate norm_w * silu(z) of this thread's rows,
         // computed before the barrier (rows past the end read a clamped row and are not stored)
         const int rsub = tid & 15, rrow = tid >> 4;  // 16 lanes per row, 16 rows per pass
         float gz[4][8];
         if (FUSED) {
-            v8 zv[4];
+            tv8 zv[4];
 #pragma unroll
             for (int pass = 0; pass < 4; ++pass) {
                 const long tt = t0 + c0 + min(pass * 16 + rrow, Lc - 1);
-                zv[pass] = *(const v8*)((const T*)fa.z + tt * fa.z_tok + (long)h * DV + 8 * rsub);
+                zv[pass] = *(const tv8*)((const T*)fa.z + tt * fa.z_tok + (long)h * DV + 8 * rsub);
             }
 #pragma unroll
             for (int pass = 0; pass < 4; ++pass)
@@ -532,16 +545,27 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
                     ss += x[e] * x[e];
                 }
                 ss = sum16(ss);
+                // a 16-bit operand out of fp16 range makes the row non-finite
+                if (r < Lc && !(ss < __builtin_inff())) range_bad = true;
                 const float inv = fast_rsqrt(ss * (1.0f / 128.0f) + fa.eps);
-                v8 y;
+                tv8 y;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) y[e] = (T)((x[e] * inv) * gz[pass][e]);
-                if (r < Lc) *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
+                if (r < Lc) *(tv8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
             } else if (r < Lc) {
-                *(v8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = ov;
+                tv8 y;
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    y[e] = (T)f(ov[e]);  // exact: ov holds T values
+                    ss += f(ov[e]) * f(ov[e]);
+                }
+                if (!(ss < __builtin_inff())) range_bad = true;
+                *(tv8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
             }
         }
     }
+    if (range_bad) atomicOr(a.fault, FAULT_RANGE);
     int ln = lane;
     asm volatile("" : "+v"(ln));
     if (s1) {
@@ -564,7 +588,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = 0.0f;
             if (p >= 0) {
-                v8 x = *(const v8*)((const T*)fa.mixed + (long)(t0 + p) * fa.mixed_tok + mc);
+                tv8 x = *(const tv8*)((const T*)fa.mixed + (long)(t0 + p) * fa.mixed_tok + mc);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = f(x[e]);
             } else if (hist) {

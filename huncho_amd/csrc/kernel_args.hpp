@@ -212,6 +212,25 @@ struct MeanPoolArgs {
     float* pool;  // [n_tokens][width] fp32 partial sums (slot rows t0 .. t0 + min(32, L) - 1)
 };
 
+// Readout at request positions (Qwen3_5Backend::readout, qwen3_5.rs:3196-3255): the
+// final-normed hidden row at each position and, with a pointer head, its fp32 score.
+struct ReadoutArgs {
+    const void* x;              // residual stream before the final norm [tokens][width]
+    long x_tok;
+    const int* cu;              // token cu_seqlens [n_seqs + 1]
+    const int* cu_pos;          // [n_seqs + 1] offsets into positions
+    const int* positions;       // [n_positions], relative to each row's tokens
+    int n_seqs, n_positions, width;
+    const float* w_eff;         // final norm (1 + w) [width]
+    float eps;
+    void* hidden_out;           // [n_positions][width] model dtype, or null
+    const float *q_w, *q_b, *k_w, *k_b;  // pointer head [head_dim][width] / [head_dim], fp32
+    int head_dim;
+    float scale;                // 1 / sqrt(head_dim)
+    float* scores;              // [n_positions] fp32, or null
+    int* fault;
+};
+
 }  // namespace hk
 
 extern "C" {
@@ -231,6 +250,7 @@ int hk_launch_final_norm_head(int dtype, const void* x, long x_tok, const int* c
                               float eps, int width, const void* head_w, const float* head_b, int n_out, float* logits,
                               void* h_out, hipStream_t st);
 int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st);
+int hk_launch_readout(int dtype, const hk::ReadoutArgs* a, hipStream_t st);
 int hk_launch_bidir_attention(int dtype, const hk::BertAttnArgs* a, int n_seqs, int max_len, hipStream_t stream);
 int hk_launch_layer_norm(int dtype, const hk::LayerNormArgs* a, hipStream_t stream);
 int hk_launch_geglu(int dtype, const hk::GegluArgs* a, hipStream_t stream);

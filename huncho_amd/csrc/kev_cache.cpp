@@ -202,9 +202,30 @@ extern "C" int hk_kev_cache_workspace_size(hk_kev_cache* c, int n_tokens, int n_
     return HK_OK;
 }
 
+static int forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids,
+                          const int32_t* cu_dev, const int32_t* cu_host, void* workspace, size_t workspace_bytes,
+                          float* logits, void* hidden_last, const hk_kev_readout* readout);
+
 extern "C" int hk_kev_forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids,
                                      const int32_t* cu_dev, const int32_t* cu_host, void* workspace,
                                      size_t workspace_bytes, float* logits, void* hidden_last) {
+    return forward_cached(c, handles_host, n_seqs, ids, cu_dev, cu_host, workspace, workspace_bytes, logits,
+                          hidden_last, nullptr);
+}
+
+extern "C" int hk_kev_forward_cached_readout(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs,
+                                             const int32_t* ids, const int32_t* cu_dev, const int32_t* cu_host,
+                                             void* workspace, size_t workspace_bytes, const hk_kev_readout* readout,
+                                             float* logits) {
+    if (!c) return HK_ERR_INVALID;
+    if (!readout) return hk_fail(c->m->ctx, HK_ERR_INVALID, "readout required");
+    return forward_cached(c, handles_host, n_seqs, ids, cu_dev, cu_host, workspace, workspace_bytes, logits, nullptr,
+                          readout);
+}
+
+static int forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids,
+                          const int32_t* cu_dev, const int32_t* cu_host, void* workspace, size_t workspace_bytes,
+                          float* logits, void* hidden_last, const hk_kev_readout* readout) {
     if (!c) return HK_ERR_INVALID;
     hk_kev_model* m = c->m;
     hk_ctx* ctx = m->ctx;
@@ -227,6 +248,8 @@ extern "C" int hk_kev_forward_cached(hk_kev_cache* c, const uint64_t* handles_ho
             return hk_fail(ctx, HK_ERR_INVALID, "sequence length %d exceeds max_context %d", hs[s]->tokens + len,
                            cfg.max_context);
     }
+    if (readout)
+        if (int rc = kev_validate_readout(m, cu_host, n_seqs, readout)) return rc;
     const int n = cu_host[n_seqs];
     const size_t model_ws = (kev_workspace_bytes(m, n, n_seqs, 0) + 255) & ~(size_t)255;
     if (model_ws + table_bytes(c, n_seqs) > workspace_bytes)
@@ -316,7 +339,7 @@ extern "C" int hk_kev_forward_cached(hk_kev_cache* c, const uint64_t* handles_ho
         view.tail_rows.push_back((void* const*)(r + 3 * n_seqs));
     }
     int rc = kev_forward_impl(m, ids, cu_dev, cu_host, n_seqs, bt_dev, c->bt_stride, c->max_pages, workspace, model_ws,
-                              logits, hidden_last, &view);
+                              logits, hidden_last, &view, readout);
     if (rc) return rollback(rc);
     // commit only after the forward finished without device faults
     if (hipStreamSynchronize(ctx->stream) != hipSuccess)
@@ -332,7 +355,9 @@ extern "C" int hk_kev_forward_cached(hk_kev_cache* c, const uint64_t* handles_ho
     }
     for (int s = 0; s < n_seqs; ++s) {
         KevHandle& h = *hs[s];
-        if (cow_src[s] >= 0) --c->refs[cow_src[s]];  // still held by the other sharers
+        // the replaced tail page loses this holder; when every holder continued in this call
+        // (a parent and its fork together), each took a private copy and the page is free
+        if (cow_src[s] >= 0 && --c->refs[cow_src[s]] == 0) c->free_list.push_back(cow_src[s]);
         for (size_t i = h.pages.size() - (cow_src[s] >= 0 ? 1 : 0); i < plan[s].size(); ++i) ++c->refs[plan[s][i]];
         h.pages = std::move(plan[s]);
         h.tokens = lens[s];

@@ -33,6 +33,9 @@ struct hk_kev_model {
     void* head_w = nullptr;
     float* head_b = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
+    // Kev PointerHead (kev.rs:112-165), fp32: q/k weights [ptr_hd][hidden], biases [ptr_hd]
+    float *ptr_qw = nullptr, *ptr_qb = nullptr, *ptr_kw = nullptr, *ptr_kb = nullptr;
+    int ptr_hd = 0;
     // derived sizes
     int key_dim = 0, value_dim = 0, conv_dim = 0, gdn_rows = 0, ba_rows = 0, attn_rows = 0;
 };
@@ -49,9 +52,13 @@ struct KevCacheView {
 };
 
 // The scoring forward (fresh batch when view == nullptr). Returns an HK_* status.
+// readout (optional): rows and pointer scores at request positions, validated before any work.
 int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev, const int32_t* cu_host, int n_seqs,
                      const int32_t* bt, int bt_stride, int num_pages, void* workspace, size_t workspace_bytes,
-                     float* logits, void* hidden_last, const KevCacheView* view);
+                     float* logits, void* hidden_last, const KevCacheView* view, const hk_kev_readout* readout);
+// Host-side validation of a readout against the rows' new-token counts (HK_OK or an error set on
+// the context).
+int kev_validate_readout(hk_kev_model* m, const int32_t* cu_host, int n_seqs, const hk_kev_readout* r);
 // Workspace bytes of a forward over n tokens in n_seqs sequences with num_pages workspace pages
 // (0 when the pools belong to a cache).
 size_t kev_workspace_bytes(const hk_kev_model* m, int n, int n_seqs, int num_pages);

@@ -101,6 +101,8 @@ extern "C" int hk_kev_model_destroy(hk_kev_model* m) {
     hipSetDevice(m->ctx->device);
     hipStreamSynchronize(m->ctx->stream);
     for (void* p : m->owned) hipFree(p);
+    for (float* p : {m->ptr_qw, m->ptr_qb, m->ptr_kw, m->ptr_kb})
+        if (p) hipFree(p);
     delete m;
     return HK_OK;
 }
@@ -122,6 +124,7 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
         return hk_fail(ctx, HK_ERR_INVALID, "invalid model configuration");
     if (c.n_out > 0 && !head_w) return hk_fail(ctx, HK_ERR_INVALID, "missing decision head");
     hipSetDevice(ctx->device);
+    if (int rc = hk_blas_prepare(ctx)) return rc;  // GEMM handle + workspace, before any forward
     hk_kev_model* m = new hk_kev_model();
     m->ctx = ctx;
     m->dtype = dtype;
@@ -279,18 +282,83 @@ extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t
                               int n_seqs, const int32_t* bt, int bt_stride, int num_pages, void* workspace,
                               size_t workspace_bytes, float* logits, void* hidden_last) {
     return kev_forward_impl(m, ids, cu_dev, cu_host, n_seqs, bt, bt_stride, num_pages, workspace, workspace_bytes,
-                            logits, hidden_last, nullptr);
+                            logits, hidden_last, nullptr, nullptr);
+}
+
+extern "C" int hk_kev_forward_readout(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
+                                      const int32_t* cu_host, int n_seqs, const int32_t* bt, int bt_stride,
+                                      int num_pages, void* workspace, size_t workspace_bytes,
+                                      const hk_kev_readout* readout, float* logits) {
+    if (!m) return HK_ERR_INVALID;
+    if (!readout) return hk_fail(m->ctx, HK_ERR_INVALID, "readout required");
+    return kev_forward_impl(m, ids, cu_dev, cu_host, n_seqs, bt, bt_stride, num_pages, workspace, workspace_bytes,
+                            logits, nullptr, nullptr, readout);
+}
+
+extern "C" int hk_kev_model_set_pointer_head(hk_kev_model* m, int head_dim, const float* q_w, const float* q_b,
+                                             const float* k_w, const float* k_b) {
+    if (!m) return HK_ERR_INVALID;
+    hk_ctx* ctx = m->ctx;
+    if (head_dim <= 0 || head_dim > 1024 || !q_w || !q_b || !k_w || !k_b)
+        return hk_fail(ctx, HK_ERR_INVALID, "pointer head: head_dim in 1..1024 and all four tensors required");
+    if (m->cfg.hidden + head_dim > 8190)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "pointer head: hidden + head_dim must be <= 8190");
+    hipSetDevice(ctx->device);
+    const size_t wb = (size_t)head_dim * m->cfg.hidden * 4, bb = (size_t)head_dim * 4;
+    float *qw = nullptr, *qb = nullptr, *kw = nullptr, *kb = nullptr;
+    bool ok = hipMalloc((void**)&qw, wb) == hipSuccess && hipMalloc((void**)&qb, bb) == hipSuccess &&
+              hipMalloc((void**)&kw, wb) == hipSuccess && hipMalloc((void**)&kb, bb) == hipSuccess;
+    ok = ok && hipMemcpy(qw, q_w, wb, hipMemcpyDeviceToDevice) == hipSuccess &&
+         hipMemcpy(qb, q_b, bb, hipMemcpyDeviceToDevice) == hipSuccess &&
+         hipMemcpy(kw, k_w, wb, hipMemcpyDeviceToDevice) == hipSuccess &&
+         hipMemcpy(kb, k_b, bb, hipMemcpyDeviceToDevice) == hipSuccess;
+    if (!ok) {
+        for (float* p : {qw, qb, kw, kb})
+            if (p) hipFree(p);
+        return hk_fail(ctx, HK_ERR_NOMEM, "pointer head allocation or copy failed");
+    }
+    hipStreamSynchronize(ctx->stream);  // a previous head may still be in use by queued work
+    for (float* p : {m->ptr_qw, m->ptr_qb, m->ptr_kw, m->ptr_kb})
+        if (p) hipFree(p);
+    m->ptr_qw = qw;
+    m->ptr_qb = qb;
+    m->ptr_kw = kw;
+    m->ptr_kb = kb;
+    m->ptr_hd = head_dim;
+    return HK_OK;
+}
+
+int kev_validate_readout(hk_kev_model* m, const int32_t* cu_host, int n_seqs, const hk_kev_readout* r) {
+    hk_ctx* ctx = m->ctx;
+    if (!r->cu_positions_host || !r->cu_positions_dev || (!r->positions_host && r->cu_positions_host[n_seqs] > 0))
+        return hk_fail(ctx, HK_ERR_INVALID, "readout: host and device position arrays are required");
+    if (r->cu_positions_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "readout: cu_positions[0] must be 0");
+    for (int s = 0; s < n_seqs; ++s) {
+        const int a = r->cu_positions_host[s], b = r->cu_positions_host[s + 1];
+        const int len = cu_host[s + 1] - cu_host[s];
+        if (b < a) return hk_fail(ctx, HK_ERR_INVALID, "readout: cu_positions decreases at row %d", s);
+        for (int i = a; i < b; ++i)
+            if (r->positions_host[i] < 0 || r->positions_host[i] >= len)
+                return hk_fail(ctx, HK_ERR_INVALID, "readout position %d is outside row %d's %d tokens",
+                               r->positions_host[i], s, len);
+    }
+    const int np = r->cu_positions_host[n_seqs];
+    if (np > 0 && !r->positions_dev) return hk_fail(ctx, HK_ERR_INVALID, "readout: positions_dev required");
+    if (r->pointer_scores_dev && !m->ptr_qw)
+        return hk_fail(ctx, HK_ERR_INVALID, "readout: pointer scores need a pointer head (hk_kev_model_set_pointer_head)");
+    if (m->cfg.hidden + 4 > 8190) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "readout: hidden too large");
+    return HK_OK;
 }
 
 int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev, const int32_t* cu_host, int n_seqs,
                      const int32_t* bt, int bt_stride, int num_pages, void* workspace, size_t workspace_bytes,
-                     float* logits, void* hidden_last, const KevCacheView* view) {
+                     float* logits, void* hidden_last, const KevCacheView* view, const hk_kev_readout* readout) {
     if (!m) return HK_ERR_INVALID;
     hk_ctx* ctx = m->ctx;
     const hk_kev_config& c = m->cfg;
     if (!ids || !cu_dev || !cu_host || !bt || !workspace || n_seqs <= 0 || bt_stride <= 0 || num_pages <= 0)
         return hk_fail(ctx, HK_ERR_INVALID, "invalid forward arguments");
-    if (c.n_out > 0 && !logits) return hk_fail(ctx, HK_ERR_INVALID, "logits output required");
+    if (c.n_out > 0 && !logits && !readout) return hk_fail(ctx, HK_ERR_INVALID, "logits output required");
     if (cu_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "cu_seqlens[0] must be 0");
     int max_len = 0;
     for (int s = 0; s < n_seqs; ++s) {
@@ -301,6 +369,8 @@ int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
             return hk_fail(ctx, HK_ERR_INVALID, "sequence %d needs more pages than bt_stride", s);
         if (len > max_len) max_len = len;
     }
+    if (readout)
+        if (int rc = kev_validate_readout(m, cu_host, n_seqs, readout)) return rc;
     const int n = cu_host[n_seqs];
     Workspace ws;
     ws.base = (char*)workspace;
@@ -380,11 +450,34 @@ int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
         RUN(hk_swiglu(ctx, dt, b.big, 2 * I, I, n, I, b.act));
         RUN(hk_gemm_xwt(ctx, dt, n, H, I, b.act, I, L.w_down, I, b.x, H, b.x, H, 1.0f, 1.0f));
     }
-    if (c.n_out > 0 || hidden_last) {
+    if ((c.n_out > 0 && logits) || hidden_last) {
         RUN(hk_launch_final_norm_head(dt, b.x, H, cu_dev, n_seqs, m->final_norm, c.eps, H, m->head_w, m->head_b,
-                                      c.n_out, logits, hidden_last, ctx->stream)
+                                      logits ? c.n_out : 0, logits, hidden_last, ctx->stream)
                 ? hk_fail(ctx, HK_ERR_DEVICE, "final head launch")
                 : 0);
+    }
+    if (readout && (readout->hidden_dev || readout->pointer_scores_dev)) {
+        hk::ReadoutArgs ra{};
+        ra.x = b.x;
+        ra.x_tok = H;
+        ra.cu = cu_dev;
+        ra.cu_pos = readout->cu_positions_dev;
+        ra.positions = readout->positions_dev;
+        ra.n_seqs = n_seqs;
+        ra.n_positions = readout->cu_positions_host[n_seqs];
+        ra.width = H;
+        ra.w_eff = m->final_norm;
+        ra.eps = c.eps;
+        ra.hidden_out = readout->hidden_dev;
+        ra.q_w = m->ptr_qw;
+        ra.q_b = m->ptr_qb;
+        ra.k_w = m->ptr_kw;
+        ra.k_b = m->ptr_kb;
+        ra.head_dim = m->ptr_hd;
+        ra.scale = m->ptr_hd > 0 ? (float)(1.0 / sqrt((double)m->ptr_hd)) : 0.0f;
+        ra.scores = readout->pointer_scores_dev;
+        ra.fault = ctx->fault_dev;
+        RUN(hk_launch_readout(dt, &ra, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "readout launch") : 0);
     }
     return HK_OK;
 }

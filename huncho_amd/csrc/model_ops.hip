@@ -13,6 +13,10 @@
 //   final_norm_head     final RMSNorm of each sequence's last token (1548) and a linear
 //                       decision head in fp32 (the Kev readout runs its projections in
 //                       fp32, kev.rs:161-165)
+//   readout             final-normed rows at request positions and the Kev PointerHead
+//                       scores k(h_pos) . q(h_last) / sqrt(head_dim) in fp32
+//                       (Qwen3_5Backend::readout 3196-3255, PointerHead::forward
+//                       kev.rs:161-165)
 // All math is fp32 with rounding to the storage type T where the reference stores a
 // tensor of the activation dtype. One wave per 128-wide head row or per hidden row.
 #include "common.hpp"
@@ -502,6 +506,75 @@ extern "C" int hk_launch_final_norm_head(int dtype, const void* x, long x_tok, c
 }
 
 namespace hk {
+
+// Final RMSNorm of row r (rounded to T, as the reference's hidden tensor is stored) into
+// dst[width] fp32, by a 256-thread workgroup; red[4] is LDS scratch.
+template <typename T>
+__device__ void norm_row_to(const T* xr, const float* w_eff, float eps, int width, float* dst, float* red) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    float ss = 0.0f;
+    for (int i = tid; i < width; i += 256) {
+        const float v = to_f(xr[i]);
+        ss += v * v;
+    }
+    ss = wsum(ss);
+    __syncthreads();  // red is free (an earlier call's readers are done)
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float denom = sqrtf(tot / (float)width + eps);
+    for (int i = tid; i < width; i += 256) dst[i] = rndt<T>((to_f(xr[i]) / denom) * w_eff[i]);
+}
+
+// out[j] = sum_i W[j][i] h[i] + b[j] (fp32) for j < head_dim: wave w takes rows w, w + 4, ...
+__device__ void linear_f32(const float* W, const float* b, const float* h, int width, int head_dim, float* out) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int j = wave; j < head_dim; j += 4) {
+        const float* wr = W + (long)j * width;
+        float acc = 0.0f;
+        for (int i = lane; i < width; i += 64) acc += wr[i] * h[i];
+        acc = wsum(acc);
+        if (lane == 0) out[j] = b ? acc + b[j] : acc;
+    }
+}
+
+// One workgroup per requested position. LDS: hp[width], hd[width], q[head_dim], k[head_dim],
+// red[4] (fp32).
+template <typename T>
+__global__ __launch_bounds__(256) void readout(ReadoutArgs a) {
+    extern __shared__ float rsm[];
+    float* hp = rsm;
+    float* hd = hp + a.width;
+    float* qv = hd + a.width;
+    float* kv = qv + a.head_dim;
+    float* red = kv + a.head_dim;
+    const int p = blockIdx.x, tid = threadIdx.x;
+    const int s = seq_of(a.cu_pos, a.n_seqs, p);
+    const int t0 = a.cu[s], len = a.cu[s + 1] - t0;
+    const int pos = a.positions[p];
+    if (a.cu_pos[s] > p || p >= a.cu_pos[s + 1] || pos < 0 || pos >= len) {
+        if (tid == 0) atomicOr(a.fault, 1);
+        return;
+    }
+    norm_row_to<T>((const T*)a.x + (long)(t0 + pos) * a.x_tok, a.w_eff, a.eps, a.width, hp, red);
+    __syncthreads();
+    if (a.hidden_out)
+        for (int i = tid; i < a.width; i += 256) ((T*)a.hidden_out)[(long)p * a.width + i] = from_f<T>(hp[i]);
+    if (!a.scores) return;
+    // the decision row: the final-normed last token of the row
+    norm_row_to<T>((const T*)a.x + (long)(t0 + len - 1) * a.x_tok, a.w_eff, a.eps, a.width, hd, red);
+    __syncthreads();
+    linear_f32(a.q_w, a.q_b, hd, a.width, a.head_dim, qv);
+    linear_f32(a.k_w, a.k_b, hp, a.width, a.head_dim, kv);
+    __syncthreads();
+    if (tid < 64) {
+        float acc = 0.0f;
+        for (int j = tid; j < a.head_dim; j += 64) acc += kv[j] * qv[j];
+        acc = wsum(acc);
+        if (tid == 0) a.scores[p] = acc * a.scale;
+    }
+}
+
 __global__ void seq_lens_kernel(const int* cu, int n, int* out) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s < n) out[s] = cu[s + 1] - cu[s];
@@ -511,5 +584,19 @@ __global__ void seq_lens_kernel(const int* cu, int n, int* out) {
 extern "C" int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st) {
     if (n == 0) return HK_OK;
     hipLaunchKernelGGL(hk::seq_lens_kernel, dim3((n + 255) / 256), dim3(256), 0, st, cu, n, out);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+extern "C" int hk_launch_readout(int dtype, const hk::ReadoutArgs* a, hipStream_t st) {
+    if (a->n_positions == 0) return HK_OK;
+    // LDS: two fp32 rows, q and k, 4 partial sums (<= 64 KiB: width + head_dim <= 8190)
+    const size_t lds = (size_t)(2 * a->width + 2 * a->head_dim + 4) * sizeof(float);
+    if (lds > 65536) return HK_ERR_UNSUPPORTED;
+    if (dtype == DT_BF16)
+        hipLaunchKernelGGL(hk::readout<bf16>, dim3(a->n_positions), dim3(256), lds, st, *a);
+    else if (dtype == DT_F16)
+        hipLaunchKernelGGL(hk::readout<f16>, dim3(a->n_positions), dim3(256), lds, st, *a);
+    else
+        hipLaunchKernelGGL(hk::readout<float>, dim3(a->n_positions), dim3(256), lds, st, *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }

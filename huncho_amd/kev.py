@@ -224,6 +224,39 @@ class KevModel:
             batch["hidden"].data_ptr() if want_hidden else None))
         return batch["logits"]
 
+    def set_pointer_head(self, q_weight, q_bias, k_weight, k_bias) -> None:
+        """The Kev PointerHead (kev.rs:112-165): q/k projections [head_dim, hidden] and biases
+        [head_dim], kept in fp32 on the device."""
+        qw, qb, kw, kb = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(self.device)
+                          for a in (q_weight, q_bias, k_weight, k_bias))
+        hd = qw.shape[0]
+        assert qw.shape == kw.shape == (hd, self.shape.hidden) and qb.shape == kb.shape == (hd,)
+        torch.cuda.synchronize(self.device)
+        self.ctx.check(abi.lib().hk_kev_model_set_pointer_head(self.h, hd, qw.data_ptr(), qb.data_ptr(),
+                                                               kw.data_ptr(), kb.data_ptr()))
+        self.pointer_head_dim = hd
+
+    def forward_readout(self, rows, positions, want_hidden: bool = True, want_scores: bool = False):
+        """Backend::forward readout for independent rows (Qwen3_5Backend::readout,
+        qwen3_5.rs:3196-3255): `positions[i]` indexes rows[i]. Returns (hidden rows at the
+        positions [n_positions, hidden] fp32 numpy or None, pointer scores [n_positions] or
+        None, decision logits [rows, n_out] or None)."""
+        flat = np.concatenate([np.asarray(r, np.int64) for r in rows])
+        if flat.size and (flat.min() < 0 or flat.max() >= self.shape.vocab):
+            raise ValueError("token id outside the vocabulary")
+        batch = self.prepare([len(r) for r in rows])
+        ids = torch.from_numpy(flat.astype(np.int32)).to(self.device)
+        ro, keep = readout_struct(positions, self.shape.hidden, self.dtype, self.device, want_hidden, want_scores)
+        logits = batch["logits"] if self.shape.n_out else None
+        self.ctx.check(abi.lib().hk_kev_forward_readout(
+            self.h, ids.data_ptr(), batch["cu"].data_ptr(), batch["cu_host"].ctypes.data_as(C.POINTER(C.c_int32)),
+            len(rows), batch["bt"].data_ptr(), batch["bt"].shape[1], batch["num_pages"], self._ws.data_ptr(),
+            self._ws.numel(), C.byref(ro), logits.data_ptr() if logits is not None else None))
+        faults = self.ctx.take_faults()
+        if faults:
+            raise abi.HkError(abi.HK_ERR_INVALID, f"device fault flags {faults:#x}")
+        return readout_results(keep, logits)
+
     def forward_batch(self, rows, temperature: float = 1.0):
         """Independent token rows -> (raw decision logits [rows, n_out], calibrated
         probabilities). Rejects out-of-vocabulary ids before any work (qwen3_5.rs:2669-2678)."""
@@ -238,6 +271,29 @@ class KevModel:
             raise abi.HkError(abi.HK_ERR_INVALID, f"device fault flags {faults:#x}")
         probs = np.stack([abi.calibrate(row, temperature) for row in logits])
         return logits, probs
+
+
+def readout_struct(positions, hidden: int, dtype, device, want_hidden: bool, want_scores: bool):
+    """hk_kev_readout for per-row position lists, with the buffers it points to (kept alive in
+    the returned dict)."""
+    cu = np.concatenate([[0], np.cumsum([len(p) for p in positions])]).astype(np.int32)
+    n = int(cu[-1])
+    # at least one element, so the pointers are valid for an empty readout too
+    pos = np.concatenate([np.asarray(p, np.int32) for p in positions] + [np.zeros(1, np.int32)]).astype(np.int32)
+    keep = {"cu": cu, "pos": pos, "cu_dev": torch.from_numpy(cu).to(device), "pos_dev": torch.from_numpy(pos).to(device),
+            "hidden": torch.empty((max(n, 1), hidden), dtype=dtype, device=device) if want_hidden else None,
+            "scores": torch.empty(max(n, 1), dtype=torch.float32, device=device) if want_scores else None, "n": n}
+    ro = abi.KevReadout(cu.ctypes.data_as(abi.i32p), pos.ctypes.data_as(abi.i32p), keep["cu_dev"].data_ptr(),
+                        keep["pos_dev"].data_ptr(), keep["hidden"].data_ptr() if want_hidden else None,
+                        keep["scores"].data_ptr() if want_scores else None)
+    return ro, keep
+
+
+def readout_results(keep, logits):
+    n = keep["n"]
+    hidden = keep["hidden"][:n].float().cpu().numpy() if keep["hidden"] is not None else None
+    scores = keep["scores"][:n].cpu().numpy() if keep["scores"] is not None else None
+    return hidden, scores, (logits.cpu().numpy() if logits is not None else None)
 
 
 class KevCache:
@@ -323,6 +379,26 @@ class KevCache:
         out = logits.cpu().numpy()[:, : self.model.shape.n_out]
         probs = np.stack([abi.calibrate(r, temperature) for r in out]) if self.model.shape.n_out else None
         return out, probs, (hidden.float().cpu().numpy() if hidden is not None else None)
+
+    def continue_rows_readout(self, handles, rows, positions, want_hidden: bool = True, want_scores: bool = False):
+        """continue_rows with the readout at `positions` (relative to each row's new tokens)."""
+        if not 1 <= len(rows) <= MAX_ROWS or len(handles) != len(rows):
+            raise ValueError(f"1..{MAX_ROWS} rows, one handle each")
+        flat = np.concatenate([np.asarray(r, np.int64) for r in rows])
+        if flat.size and (flat.min() < 0 or flat.max() >= self.model.shape.vocab):
+            raise ValueError("token id outside the vocabulary")
+        cu = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int32)
+        n, dev = int(cu[-1]), self.model.device
+        ids = torch.from_numpy(flat.astype(np.int32)).to(dev)
+        cu_dev = torch.from_numpy(cu).to(dev)
+        ws = self._workspace(n, len(rows))
+        ro, keep = readout_struct(positions, self.model.shape.hidden, self.model.dtype, dev, want_hidden, want_scores)
+        logits = torch.empty((len(rows), max(self.model.shape.n_out, 1)), dtype=torch.float32, device=dev)
+        hs = (C.c_uint64 * len(handles))(*handles)
+        self.ctx.check(abi.lib().hk_kev_forward_cached_readout(
+            self.h, hs, len(rows), ids.data_ptr(), cu_dev.data_ptr(), cu.ctypes.data_as(C.POINTER(C.c_int32)),
+            ws.data_ptr(), ws.numel(), C.byref(ro), logits.data_ptr() if self.model.shape.n_out else None))
+        return readout_results(keep, logits if self.model.shape.n_out else None)
 
     def prefill(self, tokens) -> int:
         """A new handle holding `tokens` (Backend::prefill)."""

@@ -54,6 +54,8 @@ extern "C" {
 #define HK_FAULT_PAGE 2      /* block-table entry outside [0, num_pages) or past bt_stride */
 #define HK_FAULT_ROPE 4      /* position beyond the RoPE table */
 #define HK_FAULT_TOKEN 8     /* token id outside the vocabulary */
+#define HK_FAULT_RANGE 16    /* a non-finite Gated DeltaNet output row: an fp16 MFMA operand of the
+                                16-bit recurrence (|x| > 65504) overflowed */
 
 typedef struct hk_ctx hk_ctx;
 
@@ -84,6 +86,19 @@ int hk_ctx_device_info(hk_ctx* ctx, hk_device_info_t* out);
 int hk_ctx_take_faults(hk_ctx* ctx, int* faults_out);
 int hk_device_count(int* out);
 const char* hk_version(void);
+
+/* ---- dense projections (hipBLASLt) ------------------------------------------------------------
+ * The context's GEMM algorithm per shape is a deterministic function of the shape by default:
+ * a solution pinned for the shape at build time, else hipBLASLt's heuristic first choice. The
+ * GEMM handle and workspace are created with the first model on the context, so a forward
+ * never allocates, times or synchronises. hk_ctx_set_gemm_autotune(ctx, 1) makes shapes first
+ * seen afterwards time every supported solution instead (allocates scratch and synchronises
+ * on that first use; the choice then follows the device's timing). No reference counterpart:
+ * candle's Linear (qwen3_5.rs:306-515) calls its BLAS with the library's own choice.
+ * hk_ctx_gemm_plans writes one line per cached plan ("dtype= out= n= in= ... index= source")
+ * into buf (NUL-terminated, truncated to len) and the full length + 1 into *needed. */
+int hk_ctx_set_gemm_autotune(hk_ctx* ctx, int enable);
+int hk_ctx_gemm_plans(hk_ctx* ctx, char* buf, size_t len, size_t* needed);
 
 /* ---- device memory for callers without a HIP binding (the Rust FFI crate): plain
  * hipMalloc / hipFree on the context's device, stream-ordered copies on the context's
@@ -235,6 +250,37 @@ int hk_kev_forward(hk_kev_model* m, const int32_t* ids_dev, const int32_t* cu_se
                    int num_pages, void* workspace_dev, size_t workspace_bytes, float* logits_dev,
                    void* hidden_last_dev);
 
+/* ---- readout at the request's positions (Qwen3_5Backend::readout, qwen3_5.rs:3196-3255;
+ * ForwardInput.positions, crates/huncho-core/src/backend.rs:52-58) -----------------------------
+ * Row s reads positions[cu_positions[s] .. cu_positions[s + 1]), each relative to that row's new
+ * tokens (the reference's `position < input.tokens.len()` check, qwen3_5.rs:2688-2696; rows may
+ * read no position). hidden_dev receives the final-normed hidden row at each position in the
+ * model dtype (the reference's `selected`); pointer_scores_dev the Kev PointerHead score
+ * (W_k h_pos + b_k) . (W_q h_last + b_q) / sqrt(head_dim) in fp32, h_last the row's final-normed
+ * last token (kev.rs:161-165; the model needs hk_kev_model_set_pointer_head). Either output may
+ * be NULL. Host and device copies of both index arrays are required; the host copies are
+ * validated before any work. */
+typedef struct {
+    const int32_t* cu_positions_host;  /* [n_seqs + 1], cu_positions_host[0] = 0, non-decreasing */
+    const int32_t* positions_host;     /* [n_positions] */
+    const int32_t* cu_positions_dev;   /* the same arrays on the device */
+    const int32_t* positions_dev;
+    void* hidden_dev;                  /* [n_positions][hidden] or NULL */
+    float* pointer_scores_dev;         /* [n_positions] or NULL */
+} hk_kev_readout;
+
+/* Copies a Kev PointerHead (kev.rs:112-165): q and k projections [head_dim][hidden] with biases
+ * [head_dim], fp32 device buffers (head_dim <= 1024; the caller's buffers may be freed after).
+ * Replaces a previously set head. */
+int hk_kev_model_set_pointer_head(hk_kev_model* m, int head_dim, const float* q_w_dev, const float* q_b_dev,
+                                  const float* k_w_dev, const float* k_b_dev);
+/* hk_kev_forward with the readout at positions; logits_dev (the decision head of the last token
+ * per row) may be NULL. */
+int hk_kev_forward_readout(hk_kev_model* m, const int32_t* ids_dev, const int32_t* cu_seqlens_dev,
+                           const int32_t* cu_seqlens_host, int n_seqs, const int32_t* block_tables_dev, int bt_stride,
+                           int num_pages, void* workspace_dev, size_t workspace_bytes, const hk_kev_readout* readout,
+                           float* logits_dev);
+
 /* ---- prefix cache: cached sequences that continue, fork and are released (the Backend trait's
  * cache surface, crates/huncho-core/src/backend.rs:333-437: prefill / fork / release_cache;
  * crates/huncho-backend/src/qwen3_5.rs:2655-2757 forward with fork_from, 2818-2847; pages and
@@ -267,6 +313,12 @@ int hk_kev_cache_workspace_size(hk_kev_cache* c, int n_tokens, int n_seqs, size_
 int hk_kev_forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids_dev,
                           const int32_t* cu_seqlens_dev, const int32_t* cu_seqlens_host, void* workspace_dev,
                           size_t workspace_bytes, float* logits_dev, void* hidden_last_dev);
+
+/* hk_kev_forward_cached with the readout at positions (relative to each row's new tokens, as
+ * ForwardInput.positions are for a fork_from continuation, backend.rs:66-69). */
+int hk_kev_forward_cached_readout(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids_dev,
+                                  const int32_t* cu_seqlens_dev, const int32_t* cu_seqlens_host, void* workspace_dev,
+                                  size_t workspace_bytes, const hk_kev_readout* readout, float* logits_dev);
 
 /* ---- ModernBERT encoder (the Laya backend: candle ModernBert, crates/huncho-backend/src/
  * candle.rs:65-117 load, 319-416 forward; config normalisation 157-203) ----------------------

@@ -42,6 +42,7 @@ float ho_bf16_to_f32(uint16_t x) {
 static inline float rb(float x) { return ho_bf16_to_f32(ho_f32_to_bf16(x)); }
 
 void ho_round_bf16(float* x, size_t n) {
+#pragma omp parallel for schedule(static) if (n > (1u << 20))
     for (size_t i = 0; i < n; ++i) x[i] = rb(x[i]);
 }
 void ho_to_bf16(const float* x, uint16_t* out, size_t n) {

@@ -115,7 +115,10 @@ def bf16_to_f32(bits) -> np.ndarray:
 
 
 def round_bf16(x) -> np.ndarray:
-    return bf16_to_f32(bf16_bits(x))
+    """fp32 values rounded to bf16 and back (ho_round_bf16 on a copy)."""
+    y = np.array(x, dtype=np.float32, order="C", copy=True)
+    lib().ho_round_bf16(y.reshape(-1), y.size)
+    return y
 
 
 def normal(seed: int, stream: int, shape, mean=0.0, std=1.0) -> np.ndarray:

@@ -131,6 +131,27 @@ def test_forks_are_private_and_parent_unchanged(setup):
     cache.close()
 
 
+def test_parent_and_fork_continue_together(setup):
+    """A parent and its fork share a partial tail page (21-token prefix) and continue in one
+    call: each gets a private copy of the tail, the shared page is returned to the pool (no
+    page is lost), and both equal their fresh forwards."""
+    model, cache = setup["model"], KevCache(setup["model"], max_pages=64)
+    prefix = toks(55, 21)
+    s1, s2 = toks(56, 9), toks(57, 30)
+    parent = cache.prefill(prefix)
+    child = cache.fork(parent)
+    _, p, _ = cache.continue_rows([parent, child], [s1, s2], TEMP)
+    p_fresh = fresh_probs(model, [prefix + s1, prefix + s2])
+    assert float(np.abs(p - p_fresh).max()) < 2e-3
+    # pages held now: the shared full first page, a private copy of the tail for each, and the
+    # child's 2 new pages (parent 30 tokens, child 51)
+    assert cache.stats() == (2, 64 - 5)
+    cache.release(parent)
+    cache.release(child)
+    assert cache.stats() == (0, 64)
+    cache.close()
+
+
 def test_fork_batch_leaves_parent_and_pool(setup):
     model, cache = setup["model"], KevCache(setup["model"], max_pages=64)
     prefix = toks(60, 48)  # three full pages: branches append to fresh pages only

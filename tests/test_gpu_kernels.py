@@ -103,8 +103,10 @@ def test_paged_kv_write_rejects_bad_page_without_writing(ctx):
     assert ctx.take_faults() == 0
 
 
-def test_qk_norm_rope_bf16_bit_exact(ctx):
-    """q_norm/k_norm + partial RoPE (rd = 64 of 128) + page write against the oracle's bf16 op sequence."""
+def test_qk_norm_rope_bf16_pages_bit_exact(ctx):
+    """q_norm/k_norm + partial RoPE (rd = 64 of 128) + page write against the oracle's bf16 op
+    sequence: V pages and the untouched gate halves bit-exact; rotated q and K pages equal except
+    for under 1 % of elements, by at most 4 bf16 ulp (the rms reduction order differs)."""
     from huncho_amd.ops import qk_norm_rope_kv_write
 
     lengths = [37, 100]
@@ -284,6 +286,36 @@ def test_attention_bf16_gqa_groups_and_pages(ctx, group, P):
     ref = O.round_bf16(O.round_bf16(ref) * sg)
     e = rel_err(O.bf16_to_f32(bits_of(o)), ref)
     assert e < 2e-2, e
+
+
+def test_attention_bf16_gate_and_output_strides(ctx):
+    """16-bit gate loads and O stores move 8 elements: a gate head stride of 136 (8-aligned)
+    gives the contiguous-gate result bit for bit, a stride of 132 is rejected before launch."""
+    from huncho_amd.ops import paged_kv_write, paged_prefill_attention
+
+    hkv, hq, d, P, L = 2, 4, 128, 16, 70
+    bt = block_tables_for([L], P, 8, SEED + 7)
+    kk = abi.synth_normal_bf16(SEED, 80, L * hkv * d).reshape(L, hkv, d)
+    vv = abi.synth_normal_bf16(SEED, 81, L * hkv * d).reshape(L, hkv, d)
+    kp = torch.zeros((8, hkv, P, d), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    cu, cl, btd = cuda(np.array([0, L], np.int32)), cuda(np.array([L], np.int32)), cuda(bt)
+    paged_kv_write(ctx, bf16_dev(kk), bf16_dev(vv), cu, cl, btd, kp, vp)
+    q = bf16_dev(abi.synth_normal_bf16(SEED, 82, L * hq * d).reshape(L, hq, d))
+    gate = bf16_dev(abi.synth_normal_bf16(SEED, 83, L * hq * d).reshape(L, hq, d))
+    o_ref = paged_prefill_attention(ctx, q, kp, vp, btd, cu, cl, L, gate=gate)
+    wide = torch.zeros((L, hq, 136), dtype=torch.bfloat16, device="cuda")
+    wide[:, :, :d] = gate
+    o = paged_prefill_attention(ctx, q, kp, vp, btd, cu, cl, L, gate=wide[:, :, :d])
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref)
+    bad = torch.zeros((L, hq, 132), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(abi.HkError):
+        paged_prefill_attention(ctx, q, kp, vp, btd, cu, cl, L, gate=bad[:, :, :d])
+    out_bad = torch.zeros((L, hq, 132), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(abi.HkError):
+        paged_prefill_attention(ctx, q, kp, vp, btd, cu, cl, L, out=out_bad[:, :, :d])
+    assert ctx.take_faults() == 0
 
 
 # ---------------------------------------------------------------------------

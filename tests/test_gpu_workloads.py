@@ -1,0 +1,233 @@
+"""GPU parity at the benchmark workloads themselves, against the CPU oracle.
+
+* Varlen paged GQA prefill (bf16): 32 sequences with seeded lengths in [64, 2048], pages of 16
+  from a seeded permutation of a 4096-page pool, RoPE theta 1e7: every sequence against the
+  oracle, 2e-2 relative.
+* Kev-shaped hybrid forward: the bench's exact 64 x 512 batch (same seed, weights, ids and
+  block tables), run whole on the GPU; rows 0, 21, 42 and 63 against the oracle's fp32 forward.
+  Gates on the calibrated probabilities (T = 1.3): fp32 activations 2e-5 (the fp32 gate of
+  crates/huncho-backend/tests/kev_reference.rs:79); fp16 1e-3 (the external-delta gate of
+  crates/huncho-core/src/conformance.rs:30-32); bf16: no farther from the fp32 forward than the
+  oracle's own bf16 flow (bf16 at the reference's storage points) is, on the same rows.
+* ModernBERT-base-shaped encoder (bf16): the bench's 16-row batch (lengths 561 .. 4048); the
+  longest and the shortest rows' hidden states and the mean-pooled logits against the oracle's
+  fp32 and bf16 flows; and the bidirectional attention kernel alone at L = 4096, global and
+  window +-64, against the oracle (2e-2 relative).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from huncho_amd import abi
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from huncho_amd.ops import context_for_torch
+
+    c = context_for_torch(0)
+    yield c
+    c.close()
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def bf16_dev(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def bits_of(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+# ---------------------------------------------------------------------------
+# varlen paged attention, all 32 sequences
+# ---------------------------------------------------------------------------
+
+def test_varlen_paged_attention_all_sequences(ctx):
+    from huncho_amd.ops import paged_prefill_attention, qk_norm_rope_kv_write
+
+    seed, P, pool, hq, hkv, d = 20261201, 16, 4096, 16, 8, 128
+    lengths = abi.synth_uniform_int(seed, 20, 32, 64, 2048).tolist()
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n = int(cu[-1])
+    perm = abi.synth_permutation(seed, 11, pool)
+    need = [(L + P - 1) // P for L in lengths]
+    bt = np.full((32, max(need)), -1, np.int32)
+    k0 = 0
+    for s, m in enumerate(need):
+        bt[s, :m] = perm[k0:k0 + m]
+        k0 += m
+    q = abi.synth_normal_bf16(seed, 21, n * hq * d).reshape(n, hq, d)
+    k = abi.synth_normal_bf16(seed, 22, n * hkv * d).reshape(n, hkv, d)
+    v = abi.synth_normal_bf16(seed, 23, n * hkv * d).reshape(n, hkv, d)
+    tc, ts = abi.rope_table(d, 1e7, max(lengths), True)
+    qd = bf16_dev(q)
+    kp = torch.zeros((pool, hkv, P, d), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    cud = torch.from_numpy(cu).cuda()
+    cl = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    btd = torch.from_numpy(bt).cuda()
+    qk_norm_rope_kv_write(ctx, qd, bf16_dev(k), bf16_dev(v), None, None, 0.0, torch.from_numpy(tc).cuda(),
+                          torch.from_numpy(ts).cuda(), d, cud, cl, btd, kp, vp, qd)
+    o = paged_prefill_attention(ctx, qd, kp, vp, btd, cud, cl, max(lengths))
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    # the oracle on the GPU's RoPE'd q and pages (those are bit-exact against the oracle's own
+    # RoPE and page write: test_gpu_kernels.py)
+    ref = O.paged_attention(bits_of(qd), bits_of(kp), bits_of(vp), bt, cu, lengths, P, 1 / math.sqrt(d))
+    o_np = O.bf16_to_f32(bits_of(o))
+    errs = [rel_err(o_np[cu[s]:cu[s + 1]], ref[cu[s]:cu[s + 1]]) for s in range(32)]
+    print(f"varlen paged attention, 32 sequences ({n} tokens): worst relative error {max(errs):.2e} "
+          f"(sequence {int(np.argmax(errs))}, {lengths[int(np.argmax(errs))]} tokens)")
+    assert max(errs) < 2e-2, errs
+
+
+# ---------------------------------------------------------------------------
+# Kev-shaped hybrid forward at the bench batch
+# ---------------------------------------------------------------------------
+
+KEV_ROWS = [0, 21, 42, 63]
+
+
+def _qwen_cfg(shape):
+    return O.QwenConfig(hidden_size=shape.hidden, num_hidden_layers=shape.n_layers,
+                        num_attention_heads=shape.n_heads, num_key_value_heads=shape.n_kv_heads,
+                        head_dim=shape.head_dim, intermediate_size=shape.intermediate, vocab_size=shape.vocab,
+                        rms_norm_eps=shape.eps, layer_types=shape.layer_types,
+                        linear_conv_kernel_dim=shape.conv_k, linear_key_head_dim=shape.lin_key_dim,
+                        linear_num_key_heads=shape.lin_n_k_heads, linear_num_value_heads=shape.lin_n_v_heads,
+                        linear_value_head_dim=shape.lin_v_dim, rope_theta=shape.rope_theta,
+                        partial_rotary_factor=shape.rotary_dim / shape.head_dim)
+
+
+@pytest.fixture(scope="module")
+def kev_bench_case():
+    """The bench's weights and 64 x 512 ids, and the oracle's fp32 and bf16 forwards of rows
+    0, 21, 42 and 63 (logits and calibrated probabilities)."""
+    from huncho_amd.kev import KevShape, synthetic_weights
+
+    shape = KevShape()
+    weights = synthetic_weights(shape, bench.SEED)
+    lengths = [512] * 64
+    ids = abi.synth_uniform_int(bench.SEED, 901, sum(lengths), 0, shape.vocab - 1)
+    f = {k: O.bf16_to_f32(v).reshape(v.shape) for k, v in weights.items()}
+    head_w = f["decision_head.weight"]
+    out = {}
+    for flow, bf in (("f32", False), ("bf16", True)):
+        model = O.QwenModel(_qwen_cfg(shape), f, bf16=bf)
+        lg = []
+        for r in KEV_ROWS:
+            h = model.forward(ids[r * 512:(r + 1) * 512])
+            lg.append((h[-1].astype(np.float32) @ head_w.T.astype(np.float32)).astype(np.float32))
+        del model
+        lg = np.stack(lg)
+        out[flow] = (lg, np.stack([O.calibrate(x, 1.3) for x in lg]))
+    return dict(shape=shape, weights=weights, lengths=lengths, ids=ids, ref=out)
+
+
+def _gpu_bench_rows(ctx, case, dtype):
+    from huncho_amd.kev import KevModel
+
+    model = KevModel(ctx, case["shape"], case["weights"], dtype)
+    batch = model.prepare(case["lengths"], seed=bench.SEED)
+    ids = torch.from_numpy(case["ids"]).cuda()
+    model.forward_ids(ids, batch)
+    logits = batch["logits"].cpu().numpy()
+    assert ctx.take_faults() == 0
+    model.close()
+    assert np.isfinite(logits).all()
+    lg = logits[KEV_ROWS]
+    return lg, np.stack([abi.calibrate(x, 1.3) for x in lg])
+
+
+def test_kev_bench_batch_fp32(ctx, kev_bench_case):
+    lg, p = _gpu_bench_rows(ctx, kev_bench_case, torch.float32)
+    ref_l, ref_p = kev_bench_case["ref"]["f32"]
+    dp = float(np.abs(p - ref_p).max())
+    dl = rel_err(lg, ref_l)
+    print(f"Kev 64x512 fp32, rows {KEV_ROWS}: max |dp| {dp:.2e}, logits {dl:.2e} relative")
+    assert dp < 2e-5 and dl < 1e-4, (dp, dl)
+
+
+def test_kev_bench_batch_fp16(ctx, kev_bench_case):
+    _, p = _gpu_bench_rows(ctx, kev_bench_case, torch.float16)
+    dp = float(np.abs(p - kev_bench_case["ref"]["f32"][1]).max())
+    print(f"Kev 64x512 fp16, rows {KEV_ROWS}: max |dp| vs the fp32 oracle {dp:.2e}")
+    assert dp < 1e-3, dp
+
+
+def test_kev_bench_batch_bf16(ctx, kev_bench_case):
+    _, p = _gpu_bench_rows(ctx, kev_bench_case, torch.bfloat16)
+    p32 = kev_bench_case["ref"]["f32"][1]
+    p16 = kev_bench_case["ref"]["bf16"][1]
+    dp32 = float(np.abs(p - p32).max())
+    dp16 = float(np.abs(p - p16).max())
+    spread = float(np.abs(p16 - p32).max())
+    print(f"Kev 64x512 bf16, rows {KEV_ROWS}: max |dp| vs the fp32 oracle {dp32:.2e}, vs the oracle's bf16 flow "
+          f"{dp16:.2e} (oracle bf16 vs fp32 {spread:.2e})")
+    assert dp32 <= spread, (dp32, spread)
+
+
+# ---------------------------------------------------------------------------
+# ModernBERT-base-shaped encoder at the bench batch
+# ---------------------------------------------------------------------------
+
+def test_laya_bench_batch_bf16(ctx):
+    from huncho_amd.laya import LayaModel, LayaShape, synthetic_weights
+
+    shape = LayaShape()
+    w = synthetic_weights(shape, bench.SEED)
+    lengths = bench.laya_lengths(16)
+    ids = abi.synth_uniform_int(bench.SEED, 951, sum(lengths), 0, shape.vocab - 1)
+    cu = np.concatenate([[0], np.cumsum(lengths)])
+    rows = [ids[cu[i]:cu[i + 1]].tolist() for i in range(16)]
+    model = LayaModel(ctx, shape, w, torch.bfloat16)
+    logits, hs = model.forward_batch(rows, want_hidden=True)
+    model.close()
+    pick = [int(np.argmax(lengths)), int(np.argmin(lengths))]
+    f = {k: O.bf16_to_f32(v).reshape(v.shape) for k, v in w.items()}
+    cfg = O.BertConfig(hidden_size=768, num_hidden_layers=22, num_attention_heads=12, intermediate_size=1152,
+                       vocab_size=shape.vocab, global_attn_every_n_layers=3, local_attention=128,
+                       global_rope_theta=160000.0, local_rope_theta=10000.0)
+    head = f["head.weight"].astype(np.float64)
+    for i in pick:
+        r32 = O.BertModel(cfg, f, bf16=False).forward([rows[i]])[0]
+        r16 = O.BertModel(cfg, f, bf16=True).forward([rows[i]])[0]
+        eh32 = float(np.abs(hs[i] - r32).max())
+        eh16 = float(np.abs(hs[i] - r16).max())
+        noise = float(np.abs(r16 - r32).max())
+        l32 = (head @ r32.astype(np.float64).mean(0)).astype(np.float32)
+        el = rel_err(logits[i], l32)
+        print(f"Laya bench row {i} ({lengths[i]} tokens) bf16: hidden vs oracle fp32 {eh32:.2e}, vs oracle bf16 "
+              f"{eh16:.2e} (oracle bf16 vs fp32 {noise:.2e}); logits vs fp32 {el:.2e} relative")
+        assert eh32 < 2 * noise and eh16 < 2 * noise, (i, eh32, eh16, noise)
+        assert el < 5e-2, (i, el)
+
+
+@pytest.mark.parametrize("half_window", [-1, 64])
+def test_bidir_attention_4096(ctx, half_window):
+    from huncho_amd.ops import bidir_attention
+
+    L, heads = 4096, 12
+    cu = np.array([0, L], np.int32)
+    qkv = O.round_bf16(abi.synth_normal(bench.SEED, 970 + (half_window % 7), L * 3 * heads * 64)).reshape(L, 3, heads, 64)
+    q, k, v = (np.ascontiguousarray(qkv[:, i]) for i in range(3))
+    ref = O.bidir_attention(q, k, v, cu, half_window)
+    dev = torch.from_numpy(qkv).to(torch.bfloat16).cuda()
+    out = bidir_attention(ctx, dev[:, 0], dev[:, 1], dev[:, 2], torch.from_numpy(cu).cuda(), L, half_window)
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    e = rel_err(out.float().cpu().numpy(), ref)
+    print(f"bidirectional attention L={L}, half window {half_window}: {e:.2e} relative")
+    assert e < 2e-2, e
