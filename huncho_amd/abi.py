@@ -129,6 +129,8 @@ SIGNATURES = {
     "hk_bert_model_destroy": (I, [vp]),
     "hk_bert_workspace_size": (I, [vp, I, C.POINTER(SZ)]),
     "hk_bert_forward": (I, [vp, vp, vp, i32p, I, vp, SZ, vp, vp]),
+    "hk_mean_pool_workspace_size": (I, [I, I, C.POINTER(SZ)]),
+    "hk_mean_pool_head": (I, [vp, I, vp, L, vp, I, I, I, vp, vp, I, vp, vp, SZ]),
     "hk_calibrate": (I, [f32p, I, F, f32p]),
     "hk_synth_normal": (I, [U64, U64, vp, SZ, F, F]),
     "hk_synth_normal_bf16": (I, [U64, U64, vp, SZ, F, F]),

@@ -33,3 +33,7 @@ uint16_t hk_host_f32_to_f16(float x);
 // dtype HK_BF16: bf16 in/out, fp32 accumulation; HK_F32: fp32.
 int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, long ldx, const void* w, long ldw,
                 void* y, long ldy, const void* c, long ldc, float alpha, float beta);
+
+// Argument checks shared by hk_mean_pool_head and its variants (HK_OK or an error set on ctx).
+int hk_mean_pool_check(hk_ctx* ctx, int dtype, const void* x, long x_tok, const int32_t* cu, int n_seqs, int n_tokens,
+                       int width, const void* head_w, int n_out, const float* logits);

@@ -438,8 +438,8 @@ __global__ __launch_bounds__(256) void rope_qk(RopeQkArgs a) {
 
 // Mean pooling in two deterministic passes. Pass 1, grid (sequences, POOL_PARTS): part j of a
 // sequence of L rows sums rows [L j / P, L (j + 1) / P), P = min(POOL_PARTS, L), into the fp32
-// slot row t0 + j of `pool` (slots never overlap another sequence's, since P <= L).
-constexpr int POOL_PARTS = 32;
+// slot row POOL_PARTS s + j of `pool` (every slot pass 2 reads is written first by pass 1, so
+// the pool needs no clearing).
 
 template <typename T>
 __global__ __launch_bounds__(256) void mean_pool_partial(MeanPoolArgs a) {
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(256) void mean_pool_partial(MeanPoolArgs a) {
             s1 += to_f(x[(t + 1) * a.x_tok + i]);
         }
         if (t < tb) s0 += to_f(x[t * a.x_tok + i]);
-        a.pool[(long)(t0 + j) * a.width + i] = s0 + s1;
+        a.pool[((long)seq * POOL_PARTS + j) * a.width + i] = s0 + s1;
     }
 }
 
@@ -476,7 +476,7 @@ __global__ __launch_bounds__(256) void mean_pool_head(MeanPoolArgs a) {
     const int P = min(POOL_PARTS, L);
     for (int i = threadIdx.x; i < a.width; i += blockDim.x) {
         float s = 0.0f;
-        for (int j = 0; j < P; ++j) s += a.pool[(long)(t0 + j) * a.width + i];
+        for (int j = 0; j < P; ++j) s += a.pool[((long)seq * POOL_PARTS + j) * a.width + i];
         pooled[i] = s / (float)L;
     }
     __syncthreads();
@@ -577,7 +577,7 @@ extern "C" int hk_launch_rope_qk(int dtype, const hk::RopeQkArgs* a, int n_seqs,
 }
 
 extern "C" int hk_launch_mean_pool_head(int dtype, const hk::MeanPoolArgs* a, int n_seqs, hipStream_t stream) {
-    HK_BERT_DISPATCH(dtype, mean_pool_partial, dim3(n_seqs, hk::bert::POOL_PARTS), dim3(256), 0, stream, *a);
+    HK_BERT_DISPATCH(dtype, mean_pool_partial, dim3(n_seqs, hk::POOL_PARTS), dim3(256), 0, stream, *a);
     HK_BERT_DISPATCH(dtype, mean_pool_head, dim3(n_seqs), dim3(256), a->width * sizeof(float), stream, *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }

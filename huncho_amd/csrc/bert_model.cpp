@@ -178,7 +178,9 @@ size_t bert_carve(const hk_bert_model* m, char* base, int n, BertBuffers* b) {
     b->att = take((size_t)n * c.hidden * e);
     b->gi = take((size_t)n * 2 * c.intermediate * e);
     b->act = take((size_t)n * c.intermediate * e);
-    b->pool = (float*)take(c.n_out > 0 ? (size_t)n * c.hidden * sizeof(float) : 0);
+    // mean-pool partial sums: POOL_PARTS slot rows per sequence, at most 64 sequences
+    const size_t rows = (size_t)(n < 64 ? n : 64) * hk::POOL_PARTS;
+    b->pool = (float*)take(c.n_out > 0 ? rows * c.hidden * sizeof(float) : 0);
     return off;
 }
 
@@ -202,8 +204,8 @@ extern "C" int hk_bert_forward(hk_bert_model* m, const int32_t* ids, const int32
     if (!m) return HK_ERR_INVALID;
     hk_ctx* ctx = m->ctx;
     const hk_bert_config& c = m->cfg;
-    if (!ids || !cu_dev || !cu_host || !workspace || n_seqs <= 0 || n_seqs > 65535)
-        return hk_fail(ctx, HK_ERR_INVALID, "invalid forward arguments");
+    if (!ids || !cu_dev || !cu_host || !workspace || n_seqs <= 0 || n_seqs > 64)
+        return hk_fail(ctx, HK_ERR_INVALID, "invalid forward arguments (1..64 rows, backend.rs:107-119)");
     if (c.n_out > 0 && !logits) return hk_fail(ctx, HK_ERR_INVALID, "logits output required");
     if (cu_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "cu_seqlens[0] must be 0");
     int max_len = 0;
@@ -259,4 +261,36 @@ extern "C" int hk_bert_forward(hk_bert_model* m, const int32_t* ids, const int32
         BRUN(hk_launch_mean_pool_head(dt, &pa, n_seqs, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "head launch") : 0);
     }
     return HK_OK;
+}
+
+int hk_mean_pool_check(hk_ctx* ctx, int dtype, const void* x, long x_tok, const int32_t* cu, int n_seqs, int n_tokens,
+                       int width, const void* head_w, int n_out, const float* logits) {
+    if (dtype != HK_BF16 && dtype != HK_F16 && dtype != HK_F32) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d", dtype);
+    if (!x || !cu || !head_w || !logits) return hk_fail(ctx, HK_ERR_INVALID, "mean pool: null pointer argument");
+    if (n_seqs <= 0 || n_seqs > 65535 || n_tokens < n_seqs || width <= 0 || width > 2048 || x_tok < width ||
+        n_out <= 0)
+        return hk_fail(ctx, HK_ERR_INVALID, "mean pool: bad geometry (1..65535 rows, width 1..2048, n_out >= 1)");
+    return HK_OK;
+}
+
+extern "C" int hk_mean_pool_workspace_size(int n_seqs, int width, size_t* bytes_out) {
+    if (!bytes_out || n_seqs <= 0 || width <= 0) return HK_ERR_INVALID;
+    *bytes_out = (size_t)n_seqs * hk::POOL_PARTS * width * sizeof(float);
+    return HK_OK;
+}
+
+extern "C" int hk_mean_pool_head(hk_ctx* ctx, int dtype, const void* x, long x_tok, const int32_t* cu, int n_seqs,
+                                 int n_tokens, int width, const void* head_w, const float* head_b, int n_out,
+                                 float* logits, void* workspace, size_t workspace_bytes) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = hk_mean_pool_check(ctx, dtype, x, x_tok, cu, n_seqs, n_tokens, width, head_w, n_out, logits))
+        return rc;
+    const size_t need = (size_t)n_seqs * hk::POOL_PARTS * width * sizeof(float);
+    if (!workspace || workspace_bytes < need)
+        return hk_fail(ctx, HK_ERR_INVALID, "mean pool: workspace of %zu bytes needed", need);
+    hipSetDevice(ctx->device);
+    hk::MeanPoolArgs pa{x, x_tok, cu, n_seqs, n_tokens, width, head_w, head_b, n_out, logits, ctx->fault_dev,
+                        (float*)workspace};
+    return hk_launch_mean_pool_head(dtype, &pa, n_seqs, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "mean pool launch")
+                                                                     : HK_OK;
 }

@@ -45,7 +45,15 @@ struct Pinned {
     int dtype, out, n, in, has_c, index;
 };
 const Pinned kPinned[] = {
-    {0, 0, 0, 0, 0, -1},  // (sentinel)
+    // bf16: [b | a] GDN columns, out_proj / o_proj (+ residual), down_proj (+ residual),
+    // attention q|gate|k|v, MLP gate|up, GDN q|k|v|z
+    {HK_BF16, 32, 32768, 1024, 0, 618524},   {HK_BF16, 1024, 32768, 2048, 1, 618612},
+    {HK_BF16, 1024, 32768, 3584, 1, 618613}, {HK_BF16, 6144, 32768, 1024, 0, 618611},
+    {HK_BF16, 7168, 32768, 1024, 0, 618611}, {HK_BF16, 8192, 32768, 1024, 0, 618611},
+    // fp16, the same shapes
+    {HK_F16, 32, 32768, 1024, 0, 625072},    {HK_F16, 1024, 32768, 2048, 1, 625107},
+    {HK_F16, 1024, 32768, 3584, 1, 624960},  {HK_F16, 6144, 32768, 1024, 0, 625108},
+    {HK_F16, 7168, 32768, 1024, 0, 625108},  {HK_F16, 8192, 32768, 1024, 0, 625108},
 };
 
 typedef std::tuple<int, int, int, int, long, long, long, long, int> Key;

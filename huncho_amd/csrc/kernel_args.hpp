@@ -199,6 +199,9 @@ struct RopeQkArgs {
     int* fault;
 };
 
+// Mean-pool partial sums per sequence (slot rows of MeanPoolArgs::pool).
+constexpr int POOL_PARTS = 32;
+
 struct MeanPoolArgs {
     const void* x;
     long x_tok;
@@ -209,7 +212,7 @@ struct MeanPoolArgs {
     int n_out;
     float* logits;  // [n_seqs][n_out]
     int* fault;
-    float* pool;  // [n_tokens][width] fp32 partial sums (slot rows t0 .. t0 + min(32, L) - 1)
+    float* pool;  // [n_seqs][32][width] fp32 partial sums (sequence s: slot rows 32 s .. 32 s + min(32, L) - 1)
 };
 
 // Readout at request positions (Qwen3_5Backend::readout, qwen3_5.rs:3196-3255): the

@@ -6,6 +6,7 @@ the corresponding hk_* symbol on the context's stream, and raises HkError on fai
 """
 from __future__ import annotations
 
+import ctypes as C
 import math
 
 import torch
@@ -193,4 +194,22 @@ def bidir_attention(ctx: Context, q, k, v, cu_seqlens, max_len, half_window=-1, 
     ctx.check(abi.lib().hk_bidir_attention(
         ctx.h, _dt(q), _p(q), q.stride(0), _p(k), k.stride(0), _p(v), v.stride(0), _p(cu_seqlens),
         cu_seqlens.numel() - 1, tokens, int(max_len), heads, d, int(half_window), float(scale), _p(out), out.stride(0)))
+    return out
+
+
+def mean_pool_head(ctx: Context, x, cu_seqlens, head_w, head_b=None, workspace=None, out=None):
+    """x [tokens, width] (token-strided); head_w [n_out, width] in x's dtype; head_b [n_out] fp32.
+    Returns logits [n_seqs, n_out] fp32 (hk_mean_pool_head)."""
+    _dev(x, cu_seqlens, head_w, head_b, workspace, out)
+    n_seqs = cu_seqlens.numel() - 1
+    n_out, width = head_w.shape
+    need = C.c_size_t()
+    ctx.check(abi.lib().hk_mean_pool_workspace_size(n_seqs, width, C.byref(need)))
+    if workspace is None:
+        workspace = torch.empty(need.value, dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty((n_seqs, n_out), dtype=torch.float32, device=x.device)
+    ctx.check(abi.lib().hk_mean_pool_head(ctx.h, _dt(x), _p(x), x.stride(0), _p(cu_seqlens), n_seqs, x.shape[0], width,
+                                          _p(head_w), _p(head_b), n_out, _p(out), _p(workspace),
+                                          workspace.numel() * workspace.element_size()))
     return out

@@ -367,6 +367,17 @@ int hk_bert_forward(hk_bert_model* m, const int32_t* ids_dev, const int32_t* cu_
                     const int32_t* cu_seqlens_host, int n_seqs, void* workspace_dev, size_t workspace_bytes,
                     float* logits_dev, void* hidden_out_dev);
 
+/* Mean-pooled linear head of the encoder workload over un-padded hidden rows (candle.rs:399-414
+ * hands each row's own tokens to the readout; this head pools them): logits[s][o] = head_b[o] +
+ * head_w[o] . mean of rows cu[s] .. cu[s + 1] - 1 of x, in fp32, each row's sum taken as up to
+ * 32 partial sums added in a fixed order (deterministic). x [n_tokens][width] at token stride
+ * x_tok and head_w [n_out][width] in dtype, head_b [n_out] fp32 or NULL, width <= 2048. The
+ * partial sums go to workspace_dev (hk_mean_pool_workspace_size bytes). */
+int hk_mean_pool_workspace_size(int n_seqs, int width, size_t* bytes_out);
+int hk_mean_pool_head(hk_ctx* ctx, int dtype, const void* x_dev, long x_tok, const int32_t* cu_seqlens_dev, int n_seqs,
+                      int n_tokens, int width, const void* head_w_dev, const float* head_b_dev, int n_out,
+                      float* logits_dev, void* workspace_dev, size_t workspace_bytes);
+
 /* ---- calibration (crates/huncho-core/src/calibration.rs:42-60, 170-173) --------------------------
  * Host-side: fp32 exp((x - max) / T), fp64 ordered sum and divide, fp32 result. Returns
  * HK_ERR_INVALID for a non-finite logit or a non-positive / non-finite temperature. */

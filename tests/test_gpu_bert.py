@@ -68,6 +68,28 @@ def test_bidir_attention_varlen(ctx, dtype, half_window):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mean_pool_head(ctx, dtype):
+    """Rows of 1, 31, 32, 33 and 700 tokens (fewer, equal and more rows than the 32 partial
+    sums): logits against a float64 mean and head on the same values, 1e-5 relative."""
+    from huncho_amd.ops import mean_pool_head
+
+    lengths, width, n_out = [1, 31, 32, 33, 700], 768, 4
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n = int(cu[-1])
+    x = _round(abi.synth_normal(SEED, 40, n * width), dtype).reshape(n, width)
+    w = _round(abi.synth_normal(SEED, 41, n_out * width, 0.0, 0.05), dtype).reshape(n_out, width)
+    b = abi.synth_normal(SEED, 42, n_out)
+    got = mean_pool_head(ctx, torch.from_numpy(x).to(dtype).cuda(), torch.from_numpy(cu).cuda(),
+                         torch.from_numpy(w).to(dtype).cuda(), torch.from_numpy(b).cuda())
+    torch.cuda.synchronize()
+    assert ctx.take_faults() == 0
+    ref = np.stack([w.astype(np.float64) @ x[cu[s]:cu[s + 1]].astype(np.float64).mean(0) + b for s in range(len(lengths))])
+    e = rel_err(got.cpu().numpy(), ref)
+    print(f"mean pool head {dtype}: {e:.2e}")
+    assert e < 1e-5, e
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("width", [768, 100])
 def test_layer_norm(ctx, dtype, width):
     """Widths that take the 16-byte vector path (768) and the scalar path (100)."""

@@ -4,7 +4,7 @@ Qwen3.5 forward (ho_qwen_forward) on the same seeded weights and token ids.
 Gates: calibrated decision probabilities within 1e-3 absolute of the fp32 oracle for fp16
 activations (the qualification external-delta gate, crates/huncho-core/src/conformance.rs:20-48),
 within 2e-5 for fp32 (the fp32 probability gate of crates/huncho-backend/tests/kev_reference.rs:79),
-and inside the measured bf16 rounding envelope for bf16.
+and for bf16 no farther from the fp32 oracle than the oracle's own bf16 flow is on the same rows.
 """
 import numpy as np
 import pytest
@@ -73,9 +73,9 @@ def kev_case():
 
 def test_kev_shaped_bf16_probabilities(ctx, kev_case):
     """bf16 activations: with random-init weights this 24-layer residual stack amplifies
-    rounding, so any bf16 execution sits ~1e-2 from fp32 in probability; the oracle's own
-    bf16 flow (the reference's bf16 rounding points) differs from its fp32 flow by 9.6e-3 on
-    these rows. The gate is that bf16 envelope against both oracle flows."""
+    rounding, so any bf16 execution sits ~1e-2 from fp32 in probability. Gate: the GPU is no
+    farther from the fp32 oracle than the oracle's own bf16 flow (the reference's bf16 rounding
+    points) is, on the same rows."""
     c = kev_case
     model = KevModel(ctx, c["shape"], c["weights"], torch.bfloat16)
     logits, probs = model.forward_batch(c["rows"], temperature=1.3)
@@ -86,15 +86,13 @@ def test_kev_shaped_bf16_probabilities(ctx, kev_case):
     dl = float(np.abs(logits - c["bf16_logits"]).max())
     print(f"bf16 Kev-shaped: max |dp| vs oracle bf16 {dp:.3e}, vs oracle fp32 {dp32:.3e} "
           f"(oracle bf16 vs fp32 {noise:.3e}); max |dlogit| {dl:.3e}")
-    assert dp < 2.5e-2 and dp32 < 2.5e-2, (dp, dp32, noise)
+    assert dp32 <= noise, (dp, dp32, noise)
 
 
 def test_kev_shaped_fp16_probabilities(ctx, kev_case):
     """fp16 activations (same MFMA rate as bf16, 3 more mantissa bits) on the Kev shape:
-    calibrated probabilities within the reference's half-precision gate, 2e-3 absolute of the
-    fp32 forward (kev_reference.rs:71). Measured 8.5e-4 to 1.25e-3: the value moves with the
-    GEMM algorithms hipBLASLt's timing picks on the device, and with the 16-bit MFMA operands
-    of the chunked delta rule."""
+    calibrated probabilities within 1e-3 absolute of the fp32 forward (the external-delta gate,
+    conformance.rs:30-32; the reference's own half-precision gate is 2e-3, kev_reference.rs:71)."""
     c = kev_case
     model = KevModel(ctx, c["shape"], c["weights"], torch.float16)
     logits, probs = model.forward_batch(c["rows"], temperature=1.3)
@@ -103,7 +101,7 @@ def test_kev_shaped_fp16_probabilities(ctx, kev_case):
     dp = float(np.abs(probs - c["f32_probs"]).max())
     dl = float(np.abs(logits - c["f32_logits"]).max())
     print(f"fp16 Kev-shaped: max |dp| vs oracle fp32 {dp:.3e}; max |dlogit| {dl:.3e}")
-    assert dp < 2e-3, dp
+    assert dp < 1e-3, dp
 
 
 def test_kev_shaped_fp32_probabilities(ctx, kev_case):
