@@ -131,6 +131,7 @@ SIGNATURES = {
     "hk_bert_forward": (I, [vp, vp, vp, i32p, I, vp, SZ, vp, vp]),
     "hk_mean_pool_workspace_size": (I, [I, I, C.POINTER(SZ)]),
     "hk_mean_pool_head": (I, [vp, I, vp, L, vp, I, I, I, vp, vp, I, vp, vp, SZ]),
+    "hk_mean_pool_head_noalloc": (I, [vp, I, vp, L, vp, I, I, I, vp, vp, I, vp]),
     "hk_calibrate": (I, [f32p, I, F, f32p]),
     "hk_synth_normal": (I, [U64, U64, vp, SZ, F, F]),
     "hk_synth_normal_bf16": (I, [U64, U64, vp, SZ, F, F]),

@@ -69,6 +69,9 @@ extern "C" int hk_ctx_create(int device_ordinal, hk_ctx** out) {
         delete ctx;
         return HK_ERR_DEVICE;
     }
+    // the no-allocation entry point's scratch address on this device (retried on its first call
+    // if this fails)
+    hk_noalloc_scratch_init(device_ordinal);
     *out = ctx;
     return HK_OK;
 }

@@ -37,3 +37,5 @@ int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, l
 // Argument checks shared by hk_mean_pool_head and its variants (HK_OK or an error set on ctx).
 int hk_mean_pool_check(hk_ctx* ctx, int dtype, const void* x, long x_tok, const int32_t* cu, int n_seqs, int n_tokens,
                        int width, const void* head_w, int n_out, const float* logits);
+// Resolves the no-allocation scratch array's address on `device` (current); bert.hip.
+int hk_noalloc_scratch_init(int device);

@@ -581,3 +581,61 @@ extern "C" int hk_launch_mean_pool_head(int dtype, const hk::MeanPoolArgs* a, in
     HK_BERT_DISPATCH(dtype, mean_pool_head, dim3(n_seqs), dim3(256), a->width * sizeof(float), stream, *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
+
+// ---------------------------------------------------------------------------------------------
+// hk_mean_pool_head_noalloc: hk_mean_pool_head with its partial sums in a file-scope device
+// array instead of a workspace, for callers that cannot allocate. The array holds 64 sequences
+// x 32 partial sums x 2048 columns of fp32 (16 MiB per GPU, held until the process ends). Its
+// device address comes from hipGetSymbolAddress, once per device with that device current
+// (hk_noalloc_scratch_init, called by hk_ctx_create); host code uses only that address, never
+// the array's name. Calls on one GPU share the array: overlapping calls race. Every slot the
+// second pass reads is written by the first pass of the same call, so nothing needs clearing.
+// ---------------------------------------------------------------------------------------------
+#include <mutex>
+
+#include "abi_internal.hpp"
+
+namespace {
+constexpr size_t kNoAllocFloats = (size_t)64 * hk::POOL_PARTS * 2048;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+static __device__ __align__(256) float scratch[kNoAllocFloats];
+
+// Resolves this device's scratch address (the caller has made `device` current). HK_OK once set.
+int hk_noalloc_scratch_init(int device) {
+    if (device < 0 || device >= kMaxDevices) return HK_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device]) return HK_OK;
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return HK_ERR_DEVICE;
+    g_scratch_ptr[device] = ptr;
+    return HK_OK;
+}
+
+extern "C" int hk_mean_pool_head_noalloc(hk_ctx* ctx, int dtype, const void* x, long x_tok, const int32_t* cu,
+                                         int n_seqs, int n_tokens, int width, const void* head_w, const float* head_b,
+                                         int n_out, float* logits) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (int rc = hk_mean_pool_check(ctx, dtype, x, x_tok, cu, n_seqs, n_tokens, width, head_w, n_out, logits))
+        return rc;
+    if ((size_t)n_seqs * hk::POOL_PARTS * width > kNoAllocFloats)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED,
+                       "mean pool without allocation: %d rows x %d columns exceed the fixed scratch of %zu partial "
+                       "sums (64 rows x 32 parts x 2048 columns)",
+                       n_seqs, width, kNoAllocFloats / hk::POOL_PARTS);
+    if (hipSetDevice(ctx->device) != hipSuccess) return hk_fail(ctx, HK_ERR_DEVICE, "hipSetDevice failed");
+    if (int rc = hk_noalloc_scratch_init(ctx->device))
+        return hk_fail(ctx, rc, "hipGetSymbolAddress of the mean-pool scratch failed");
+    void* ptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ptr = g_scratch_ptr[ctx->device];
+    }
+    hk::MeanPoolArgs pa{x, x_tok, cu, n_seqs, n_tokens, width, head_w, head_b, n_out, logits, ctx->fault_dev,
+                        (float*)ptr};
+    return hk_launch_mean_pool_head(dtype, &pa, n_seqs, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "mean pool launch")
+                                                                     : HK_OK;
+}

@@ -378,6 +378,16 @@ int hk_mean_pool_head(hk_ctx* ctx, int dtype, const void* x_dev, long x_tok, con
                       int n_tokens, int width, const void* head_w_dev, const float* head_b_dev, int n_out,
                       float* logits_dev, void* workspace_dev, size_t workspace_bytes);
 
+/* hk_mean_pool_head without a workspace: no counterpart in the reference. It is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops). The partial sums live in a
+ * fixed device array of the library (64 rows x 32 parts x 2048 columns fp32, 16 MiB per GPU, held
+ * until the process ends), so it allocates nothing and calls nothing that does; n_seqs * width
+ * beyond 64 * 2048 returns HK_ERR_UNSUPPORTED before any launch. Calls that overlap on one GPU
+ * share that array and race. Results equal hk_mean_pool_head's bit for bit. */
+int hk_mean_pool_head_noalloc(hk_ctx* ctx, int dtype, const void* x_dev, long x_tok, const int32_t* cu_seqlens_dev,
+                              int n_seqs, int n_tokens, int width, const void* head_w_dev, const float* head_b_dev,
+                              int n_out, float* logits_dev);
+
 /* ---- calibration (crates/huncho-core/src/calibration.rs:42-60, 170-173) --------------------------
  * Host-side: fp32 exp((x - max) / T), fp64 ordered sum and divide, fp32 result. Returns
  * HK_ERR_INVALID for a non-finite logit or a non-positive / non-finite temperature. */

@@ -1,0 +1,70 @@
+"""hk_mean_pool_head_noalloc (the entry point for callers that cannot allocate) against
+hk_mean_pool_head, through the C ABI: two calls in a row, the second with a smaller input, each
+bit-identical to the workspace entry point's logits (same kernels, same summation order); the
+largest accepted input; and a clear rejection beyond the fixed scratch."""
+import numpy as np
+import pytest
+import torch
+
+from huncho_amd import abi
+
+pytestmark = pytest.mark.gpu
+
+SEED = 4711
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from huncho_amd.ops import context_for_torch
+
+    c = context_for_torch(0)
+    yield c
+    c.close()
+
+
+def noalloc(ctx, x, cu, w, b, n_out):
+    fn = abi.lib().hk_mean_pool_head_noalloc
+    n_seqs = cu.numel() - 1
+    out = torch.full((n_seqs, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    rc = fn(ctx.h, abi.HK_BF16 if x.dtype == torch.bfloat16 else abi.HK_F32, x.data_ptr(), x.stride(0),
+            cu.data_ptr(), n_seqs, x.shape[0], x.shape[1], w.data_ptr(), b.data_ptr() if b is not None else None,
+            n_out, out.data_ptr())
+    return rc, out
+
+
+def case(lengths, width, n_out, dtype, stream):
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    n = int(cu[-1])
+    x = torch.from_numpy(abi.synth_normal(SEED, stream, n * width).reshape(n, width)).to(dtype).cuda()
+    w = torch.from_numpy(abi.synth_normal(SEED, stream + 1, n_out * width, 0.0, 0.05).reshape(n_out, width)).to(dtype).cuda()
+    b = torch.from_numpy(abi.synth_normal(SEED, stream + 2, n_out)).cuda()
+    return x, torch.from_numpy(cu).cuda(), w, b
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_noalloc_matches_workspace_entry_twice(ctx, dtype):
+    from huncho_amd.ops import mean_pool_head
+
+    big = case([1 + 37 * i for i in range(40)], 768, 4, dtype, 10)   # 40 rows, 28,900 tokens
+    small = case([5, 64, 33], 100, 3, dtype, 20)                     # then a smaller one
+    for x, cu, w, b in (big, small):
+        ref = mean_pool_head(ctx, x, cu, w, b)
+        rc, got = noalloc(ctx, x, cu, w, b, w.shape[0])
+        torch.cuda.synchronize()
+        assert rc == abi.HK_OK, abi.lib().hk_ctx_last_error(ctx.h)
+        assert ctx.take_faults() == 0
+        assert torch.equal(got, ref), (got, ref)
+
+
+def test_noalloc_limits(ctx):
+    from huncho_amd.ops import mean_pool_head
+
+    x, cu, w, b = case([3] * 64, 2048, 2, torch.bfloat16, 30)  # the largest accepted: 64 rows x 2048
+    rc, got = noalloc(ctx, x, cu, w, b, 2)
+    torch.cuda.synchronize()
+    assert rc == abi.HK_OK and torch.equal(got, mean_pool_head(ctx, x, cu, w, b))
+    x, cu, w, b = case([3] * 65, 2048, 2, torch.bfloat16, 40)  # one row more: rejected before launch
+    rc, got = noalloc(ctx, x, cu, w, b, 2)
+    assert rc == abi.HK_ERR_UNSUPPORTED
+    assert b"scratch" in abi.lib().hk_ctx_last_error(ctx.h)
+    assert torch.isnan(got).all()
