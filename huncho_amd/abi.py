@@ -104,6 +104,9 @@ SIGNATURES = {
     "hk_rms_norm": (I, [vp, I, vp, L, vp, F, I, I, vp, L]),
     "hk_gated_rms_norm": (I, [vp, I, vp, vp, L, I, vp, F, I, I, vp]),
     "hk_swiglu": (I, [vp, I, vp, L, L, I, I, vp]),
+    "hk_lora_merge": (I, [vp, I, vp, I, I, vp, vp, I, F]),
+    "hk_kev_model_identity": (I, [vp, C.c_char_p, SZ, C.POINTER(SZ)]),
+    "hk_bert_model_identity": (I, [vp, C.c_char_p, SZ, C.POINTER(SZ)]),
     "hk_kev_model_create": (I, [vp, I, C.POINTER(KevConfig), C.POINTER(KevLayerWeights), vp, vp, vp, vp,
                                 C.POINTER(vp)]),
     "hk_kev_model_destroy": (I, [vp]),
@@ -154,6 +157,15 @@ def lib() -> C.CDLL:
             fn.argtypes = args
         _lib = L_
     return _lib
+
+
+def identity(fn, handle) -> dict:
+    """An identity call (hk_kev_model_identity / hk_bert_model_identity) as a dict."""
+    need = SZ(0)
+    fn(handle, None, 0, C.byref(need))
+    buf = C.create_string_buffer(need.value)
+    fn(handle, buf, need.value, C.byref(need))
+    return dict(line.split("=", 1) for line in buf.value.decode().splitlines() if "=" in line)
 
 
 def device_count() -> int:

@@ -7,7 +7,11 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
+#include <utility>
+#include <vector>
+
 
 // ---------------------------------------------------------------------------
 // context and errors
@@ -618,4 +622,17 @@ extern "C" int hk_bidir_attention(hk_ctx* ctx, int dtype, const void* q, long q_
                        scale * 1.4426950408889634f, ctx->fault_dev};
     int rc = hk_launch_bidir_attention(dtype, &a, n_seqs, max_len, ctx->stream);
     return rc ? hk_fail(ctx, rc, "bidirectional attention launch failed") : HK_OK;
+}
+
+int hk_write_identity(std::vector<std::pair<std::string, std::string>> kv, char* buf, size_t len, size_t* needed) {
+    std::sort(kv.begin(), kv.end());
+    std::string out;
+    for (auto& e : kv) out += e.first + "=" + e.second + "\n";
+    if (needed) *needed = out.size() + 1;
+    if (buf && len) {
+        const size_t n = out.size() < len - 1 ? out.size() : len - 1;
+        memcpy(buf, out.data(), n);
+        buf[n] = 0;
+    }
+    return HK_OK;
 }

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/huncho_rocm.h"
 #include "kernel_args.hpp"
@@ -39,3 +41,5 @@ int hk_mean_pool_check(hk_ctx* ctx, int dtype, const void* x, long x_tok, const 
                        int width, const void* head_w, int n_out, const float* logits);
 // Resolves the no-allocation scratch array's address on `device` (current); bert.hip.
 int hk_noalloc_scratch_init(int device);
+// Writes sorted "key=value" lines (NUL-terminated, truncated to len) and the full length + 1.
+int hk_write_identity(std::vector<std::pair<std::string, std::string>> kv, char* buf, size_t len, size_t* needed);

@@ -17,6 +17,9 @@
 
 #include <vector>
 
+#include <cstdio>
+#include <string>
+
 #include "abi_internal.hpp"
 
 namespace {
@@ -293,4 +296,21 @@ extern "C" int hk_mean_pool_head(hk_ctx* ctx, int dtype, const void* x, long x_t
                         (float*)workspace};
     return hk_launch_mean_pool_head(dtype, &pa, n_seqs, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "mean pool launch")
                                                                      : HK_OK;
+}
+
+extern "C" int hk_bert_model_identity(hk_bert_model* m, char* buf, size_t len, size_t* needed) {
+    if (!m) return HK_ERR_INVALID;
+    const bool f32 = m->dtype == HK_F32;
+    char dev[96];
+    snprintf(dev, sizeof dev, "rocm:%d (%s, %d CUs)", m->ctx->device, m->ctx->prop.gcnArchName,
+             m->ctx->prop.multiProcessorCount);
+    return hk_write_identity({{"device", dev},
+                              {"native_execution", "huncho-rocm-modernbert-v1"},
+                              {"device_path", "laya-rocm-gfx950-v1"},
+                              {"activation_dtype", f32 ? "fp32" : m->dtype == HK_BF16 ? "bf16" : "fp16"},
+                              {"attention_execution", f32 ? "rocm-varlen-bidir-f32-v1" : "rocm-varlen-bidir-mfma-16bit-v1"},
+                              {"padding", "unpadded-varlen-v1"},
+                              {"projection_kernel", "hipblaslt-pinned-or-heuristic-v1"},
+                              {"library", hk_version()}},
+                             buf, len, needed);
 }

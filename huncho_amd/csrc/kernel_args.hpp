@@ -254,6 +254,8 @@ int hk_launch_final_norm_head(int dtype, const void* x, long x_tok, const int* c
                               void* h_out, hipStream_t st);
 int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st);
 int hk_launch_readout(int dtype, const hk::ReadoutArgs* a, hipStream_t st);
+int hk_launch_lora_merge(int dtype, void* w, long rows, int cols, const float* a, const float* b, int rank, float scale,
+                         hipStream_t st);
 int hk_launch_bidir_attention(int dtype, const hk::BertAttnArgs* a, int n_seqs, int max_len, hipStream_t stream);
 int hk_launch_layer_norm(int dtype, const hk::LayerNormArgs* a, hipStream_t stream);
 int hk_launch_geglu(int dtype, const hk::GegluArgs* a, hipStream_t stream);

@@ -21,6 +21,10 @@
 #include <math.h>
 #include <string.h>
 
+#include <cmath>
+#include <cstdio>
+#include <string>
+
 #include <vector>
 
 #include "kev_internal.hpp"
@@ -480,4 +484,46 @@ int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
         RUN(hk_launch_readout(dt, &ra, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "readout launch") : 0);
     }
     return HK_OK;
+}
+
+extern "C" int hk_lora_merge(hk_ctx* ctx, int dtype, void* w, int rows, int cols, const float* a, const float* b,
+                             int rank, float scale) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (dtype != HK_BF16 && dtype != HK_F16 && dtype != HK_F32) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d", dtype);
+    if (!w || !a || !b || rows <= 0 || cols <= 0 || rank <= 0 || !std::isfinite(scale))
+        return hk_fail(ctx, HK_ERR_INVALID, "lora merge: bad arguments (%d x %d, rank %d)", rows, cols, rank);
+    if ((long)rows * cols > (long)UINT32_MAX * 256)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "lora merge: weight too large");
+    hipSetDevice(ctx->device);
+    return hk_launch_lora_merge(dtype, w, rows, cols, a, b, rank, scale, ctx->stream)
+               ? hk_fail(ctx, HK_ERR_DEVICE, "lora merge launch")
+               : HK_OK;
+}
+
+extern "C" int hk_kev_model_identity(hk_kev_model* m, char* buf, size_t len, size_t* needed) {
+    if (!m) return HK_ERR_INVALID;
+    const bool f32 = m->dtype == HK_F32;
+    const char* dt = f32 ? "fp32" : m->dtype == HK_BF16 ? "bf16" : "fp16";
+    char dev[96];
+    snprintf(dev, sizeof dev, "rocm:%d (%s, %d CUs)", m->ctx->device, m->ctx->prop.gcnArchName,
+             m->ctx->prop.multiProcessorCount);
+    return hk_write_identity(
+        {{"device", dev},
+         {"native_execution", "huncho-rocm-qwen35-v1"},
+         {"device_path", "kev-rocm-gfx950-v1"},
+         {"activation_dtype", dt},
+         {"attention_compute_dtype", "fp32"},
+         {"attention_execution", f32 ? "rocm-paged-flash-mfma-f32-v1" : "rocm-paged-flash-mfma-16bit-v1"},
+         {"gqa_execution", "rocm-group-in-query-tile-v1"},
+         {"paged_attention", "rocm-block-table-lds-gather-v1"},
+         {"kv_storage", "rocm-pool-block-tables-v1"},
+         {"kv_page_tokens", std::to_string(m->cfg.page_size)},
+         {"delta_rule_execution", f32 ? "rocm-chunked-c64-mfma-f32-v1" : "rocm-chunked-c64-mfma-f16-operands-v1"},
+         {"recurrent_state_dtype", "fp32"},
+         {"causal_conv_execution", f32 ? "rocm-gdn-prep-v1" : "rocm-fused-gdn-layer-v1"},
+         {"mlp_gate_execution", "rocm-swiglu-v1"},
+         {"projection_kernel", "hipblaslt-pinned-or-heuristic-v1"},
+         {"pointer_head_dtype", "fp32"},
+         {"library", hk_version()}},
+        buf, len, needed);
 }

@@ -13,6 +13,8 @@
 //   final_norm_head     final RMSNorm of each sequence's last token (1548) and a linear
 //                       decision head in fp32 (the Kev readout runs its projections in
 //                       fp32, kev.rs:161-165)
+//   lora_merge          W = dtype(W + scale * (B A)) in fp32 at load time (merge_lora_into_map,
+//                       1597-1640)
 //   readout             final-normed rows at request positions and the Kev PointerHead
 //                       scores k(h_pos) . q(h_last) / sqrt(head_dim) in fp32
 //                       (Qwen3_5Backend::readout 3196-3255, PointerHead::forward
@@ -575,6 +577,23 @@ __global__ __launch_bounds__(256) void readout(ReadoutArgs a) {
     }
 }
 
+// One thread per weight element: delta = sum_k B[row][k] A[k][col] (k ascending, fp32), then
+// W = T(float(W) + scale * delta), as merge_lora_into_map computes the delta in fp32, scales it
+// and casts the merged sum back to the model dtype.
+template <typename T>
+__global__ __launch_bounds__(256) void lora_merge(void* wv, long rows, int cols, const float* a, const float* b,
+                                                  int rank, float scale) {
+    T* w = (T*)wv;
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * cols) return;
+    const long r = idx / cols;
+    const int c = (int)(idx - r * cols);
+    const float* br = b + r * rank;
+    float acc = 0.0f;
+    for (int k = 0; k < rank; ++k) acc += br[k] * a[(long)k * cols + c];
+    w[idx] = from_f<T>(to_f(w[idx]) + acc * scale);
+}
+
 __global__ void seq_lens_kernel(const int* cu, int n, int* out) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s < n) out[s] = cu[s + 1] - cu[s];
@@ -598,5 +617,13 @@ extern "C" int hk_launch_readout(int dtype, const hk::ReadoutArgs* a, hipStream_
         hipLaunchKernelGGL(hk::readout<f16>, dim3(a->n_positions), dim3(256), lds, st, *a);
     else
         hipLaunchKernelGGL(hk::readout<float>, dim3(a->n_positions), dim3(256), lds, st, *a);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+extern "C" int hk_launch_lora_merge(int dtype, void* w, long rows, int cols, const float* a, const float* b, int rank,
+                                    float scale, hipStream_t st) {
+    const long n = rows * cols;
+    if (n == 0) return HK_OK;
+    HK_DISPATCH3(hk::lora_merge, dim3((unsigned)((n + 255) / 256)), dim3(256), w, rows, cols, a, b, rank, scale);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }

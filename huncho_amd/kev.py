@@ -127,15 +127,55 @@ def _to_device(a: np.ndarray, dtype: torch.dtype, device) -> torch.Tensor:
     return t.to(device).contiguous()
 
 
+def canonical_weight_name(name: str):
+    """canonical_weight_name (qwen3_5.rs:2496-2512): the text-backbone name under
+    model.language_model., or None for names outside it."""
+    if name.startswith(PREFIX) or name.startswith("lm_head."):
+        return name
+    text = name[len("language_model."):] if name.startswith("language_model.") else (
+        name[len("model."):] if name.startswith("model.") else name)
+    if text.startswith(("layers.", "embed_tokens.", "norm.")):
+        return PREFIX + text
+    return None
+
+
+def merge_lora_on_device(ctx: abi.Context, staged: dict, lora: dict, scale: float, hk_dtype: int) -> None:
+    """merge_lora_into_map (qwen3_5.rs:1597-1640) on staged device tensors through hk_lora_merge:
+    every `base_model.model.{t}.lora_A.weight` / `lora_B.weight` pair updates the base weight
+    canonical_weight_name(t + ".weight") in sorted target order."""
+    targets = sorted({k[len("base_model.model."):-len(".lora_A.weight")] for k in lora
+                      if k.startswith("base_model.model.") and k.endswith(".lora_A.weight")})
+    for t in targets:
+        b_key = f"base_model.model.{t}.lora_B.weight"
+        if b_key not in lora:
+            raise ValueError(f"missing LoRA weight `{b_key}`")
+        base = canonical_weight_name(t + ".weight")
+        if base is None:
+            raise ValueError(f"unsupported LoRA target `{t}`")
+        if base not in staged:
+            raise ValueError(f"missing base weight `{base}` required for LoRA merge")
+        w = staged[base]
+        a = torch.from_numpy(np.ascontiguousarray(lora[f"base_model.model.{t}.lora_A.weight"], np.float32)).to(w.device)
+        b = torch.from_numpy(np.ascontiguousarray(lora[b_key], np.float32)).to(w.device)
+        rows, cols = w.shape[0], int(np.prod(w.shape[1:]))
+        if a.shape != (a.shape[0], cols) or b.shape != (rows, a.shape[0]):
+            raise ValueError(f"LoRA shapes {tuple(a.shape)} / {tuple(b.shape)} do not fit `{base}` {tuple(w.shape)}")
+        ctx.check(abi.lib().hk_lora_merge(ctx.h, hk_dtype, w.data_ptr(), rows, cols, a.data_ptr(), b.data_ptr(),
+                                          a.shape[0], float(scale)))
+    torch.cuda.synchronize(next(iter(staged.values())).device if staged else None)
+
+
 class KevModel:
     """hk_kev_model plus its workspace, for varlen batches of independent rows."""
 
     def __init__(self, ctx: abi.Context, shape: KevShape, weights: dict, dtype: torch.dtype = torch.bfloat16,
-                 device=0):
+                 device=0, lora: dict | None = None, lora_scale: float = 1.0):
         self.ctx, self.shape, self.dtype = ctx, shape, dtype
         self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
         self.hk_dtype = {torch.bfloat16: HK_BF16, torch.float16: HK_F16, torch.float32: HK_F32}[dtype]
         staged = {k: _to_device(v, dtype, self.device) for k, v in weights.items()}
+        if lora:
+            merge_lora_on_device(ctx, staged, lora, lora_scale, self.hk_dtype)
         lts = (C.c_int32 * shape.n_layers)(*shape.layer_types)
         cfg = KevConfig(shape.hidden, shape.n_layers, shape.n_heads, shape.n_kv_heads, shape.head_dim,
                         shape.intermediate, shape.vocab, shape.eps, shape.rope_theta, shape.rotary_dim,

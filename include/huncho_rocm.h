@@ -230,6 +230,14 @@ typedef struct {
     const void *q_norm, *k_norm;
 } hk_kev_layer_weights;
 
+/* LoRA merge at load time (merge_lora_into_map, qwen3_5.rs:1597-1640): in place,
+ * w = dtype(w + scale * (b . a)) with the delta formed and added in fp32. w [rows][cols] in dtype
+ * (the base weight, PyTorch [out][in]); a = lora_A [rank][cols] and b = lora_B [rows][rank] as
+ * fp32; scale = lora_alpha / r. Run on the staged checkpoint tensors before hk_kev_model_create,
+ * as the reference merges before building its model. */
+int hk_lora_merge(hk_ctx* ctx, int dtype, void* w_dev, int rows, int cols, const float* a_dev, const float* b_dev,
+                  int rank, float scale);
+
 typedef struct hk_kev_model hk_kev_model;
 
 /* Loads (copies and fuses) the weights; the caller's buffers may be freed afterwards.
@@ -249,6 +257,12 @@ int hk_kev_forward(hk_kev_model* m, const int32_t* ids_dev, const int32_t* cu_se
                    const int32_t* cu_seqlens_host, int n_seqs, const int32_t* block_tables_dev, int bt_stride,
                    int num_pages, void* workspace_dev, size_t workspace_bytes, float* logits_dev,
                    void* hidden_last_dev);
+
+/* Execution identity (the keys Capabilities.extra carries, qwen3_5.rs:2540-2653, which the
+ * engine matches against the calibration key, engine.rs:218-226): sorted "key=value" lines such as
+ * device, native_execution, device_path, attention_execution, delta_rule_execution and
+ * activation_dtype, written to buf (NUL-terminated, truncated to len); *needed = full length + 1. */
+int hk_kev_model_identity(hk_kev_model* m, char* buf, size_t len, size_t* needed);
 
 /* ---- readout at the request's positions (Qwen3_5Backend::readout, qwen3_5.rs:3196-3255;
  * ForwardInput.positions, crates/huncho-core/src/backend.rs:52-58) -----------------------------
@@ -360,6 +374,8 @@ int hk_bert_model_create(hk_ctx* ctx, int dtype, const hk_bert_config* cfg, cons
                          const void* head_w_dev, const float* head_b_dev, hk_bert_model** out);
 int hk_bert_model_destroy(hk_bert_model* m);
 int hk_bert_workspace_size(hk_bert_model* m, int n_tokens, size_t* bytes_out);
+/* Execution identity of the encoder (as hk_kev_model_identity; candle.rs:272-302 capabilities). */
+int hk_bert_model_identity(hk_bert_model* m, char* buf, size_t len, size_t* needed);
 /* Encoder forward of an unpadded varlen batch: ids [n_tokens], cu_seqlens on device and
  * host. Writes the mean-pooled head's logits [n_seqs][n_out] (fp32) and, if hidden_out_dev
  * != NULL, the final-normed hidden states [n_tokens][hidden] in the model dtype. */

@@ -152,3 +152,22 @@ def test_forward_rejects_out_of_vocab_before_work(ctx):
     model.forward_ids(ids, batch)
     assert ctx.take_faults() & abi.HK_FAULT_TOKEN
     model.close()
+
+
+def test_identity_keys(ctx):
+    """The execution-identity keys (Capabilities.extra, qwen3_5.rs:2540-2653) name the device,
+    the dtype and the kernels that ran, so a calibration key cannot silently match another path."""
+    shape = KevShape(hidden=256, n_layers=4, n_heads=2, n_kv_heads=1, intermediate=512, vocab=1000,
+                     lin_n_k_heads=2, lin_n_v_heads=2, rotary_dim=64, n_out=3)
+    seen = {}
+    for dt in (torch.bfloat16, torch.float16, torch.float32):
+        model = KevModel(ctx, shape, synthetic_weights(shape, 3), dt)
+        ident = abi.identity(abi.lib().hk_kev_model_identity, model.h)
+        model.close()
+        for key in ("device", "native_execution", "device_path", "attention_execution", "delta_rule_execution",
+                    "activation_dtype", "kv_page_tokens", "recurrent_state_dtype"):
+            assert key in ident, key
+        assert "gfx950" in ident["device"] and ident["kv_page_tokens"] == "16"
+        seen[dt] = ident
+    assert seen[torch.bfloat16]["activation_dtype"] == "bf16" and seen[torch.float16]["activation_dtype"] == "fp16"
+    assert seen[torch.float32]["delta_rule_execution"] != seen[torch.bfloat16]["delta_rule_execution"]
