@@ -1,0 +1,615 @@
+//! Raw declarations of `include/huncho_rocm.h` (one to one, checked against the header by the
+//! repository's tests/test_rust_binding.py) and a thin RAII layer: `Context`, `Buffer`,
+//! `KevModel`, `KevCache`, `BertModel`. huncho-backend's device branch builds on these; it maps
+//! `HkError` to `huncho_core::error::Error` (`ErrorKind::Unsupported` -> `Error::Unsupported`,
+//! `Invalid` -> `Error::Request`, the rest -> `Error::Backend`, crates/huncho-core/src/error.rs:11-38).
+//!
+//! Threading: a context is used by one thread at a time (the engine serialises calls per model,
+//! crates/huncho-core/src/engine.rs:175-178), so the handles are `Send` and not `Sync`.
+#![allow(non_camel_case_types)]
+
+use std::ffi::{c_char, c_int, c_long, c_void, CStr};
+
+pub const HK_OK: c_int = 0;
+pub const HK_ERR_INVALID: c_int = 1;
+pub const HK_ERR_UNSUPPORTED: c_int = 2;
+pub const HK_ERR_DEVICE: c_int = 3;
+pub const HK_ERR_NOMEM: c_int = 4;
+
+pub const HK_F32: c_int = 0;
+pub const HK_BF16: c_int = 1;
+pub const HK_F16: c_int = 2;
+
+pub const HK_FAULT_SEQLENS: c_int = 1;
+pub const HK_FAULT_PAGE: c_int = 2;
+pub const HK_FAULT_ROPE: c_int = 4;
+pub const HK_FAULT_TOKEN: c_int = 8;
+pub const HK_FAULT_RANGE: c_int = 16;
+
+#[repr(C)]
+pub struct hk_ctx {
+    _private: [u8; 0],
+}
+
+#[repr(C)]
+pub struct hk_kev_model {
+    _private: [u8; 0],
+}
+
+#[repr(C)]
+pub struct hk_kev_cache {
+    _private: [u8; 0],
+}
+
+#[repr(C)]
+pub struct hk_bert_model {
+    _private: [u8; 0],
+}
+
+#[repr(C)]
+pub struct hk_device_info_t {
+    pub name: [c_char; 64],
+    pub compute_units: c_int,
+    pub clock_khz: c_int,
+    pub mem_clock_khz: c_int,
+    pub mem_bus_width: c_int,
+    pub total_mem: usize,
+    pub lds_per_block: usize,
+    pub l2_bytes: c_int,
+}
+
+#[repr(C)]
+pub struct hk_kev_config {
+    pub hidden: c_int,
+    pub n_layers: c_int,
+    pub n_heads: c_int,
+    pub n_kv_heads: c_int,
+    pub head_dim: c_int,
+    pub intermediate: c_int,
+    pub vocab: c_int,
+    pub eps: f32,
+    pub rope_theta: f64,
+    pub rotary_dim: c_int,
+    pub conv_k: c_int,
+    pub lin_key_dim: c_int,
+    pub lin_n_k_heads: c_int,
+    pub lin_n_v_heads: c_int,
+    pub lin_v_dim: c_int,
+    pub page_size: c_int,
+    pub max_context: c_int,
+    pub n_out: c_int,
+    pub layer_types_host: *const i32,
+}
+
+/// Per-layer device weights of the Kev model; null for the other layer type's tensors.
+#[repr(C)]
+#[derive(Clone, Copy)]
+pub struct hk_kev_layer_weights {
+    pub input_norm: *const c_void,
+    pub post_norm: *const c_void,
+    pub gate_proj: *const c_void,
+    pub up_proj: *const c_void,
+    pub down_proj: *const c_void,
+    pub in_qkv: *const c_void,
+    pub in_z: *const c_void,
+    pub in_b: *const c_void,
+    pub in_a: *const c_void,
+    pub out_proj: *const c_void,
+    pub conv_w: *const c_void,
+    pub norm_w: *const c_void,
+    pub a_log: *const c_void,
+    pub dt_bias: *const c_void,
+    pub q_proj: *const c_void,
+    pub k_proj: *const c_void,
+    pub v_proj: *const c_void,
+    pub o_proj: *const c_void,
+    pub q_norm: *const c_void,
+    pub k_norm: *const c_void,
+}
+
+impl Default for hk_kev_layer_weights {
+    fn default() -> Self {
+        let n = std::ptr::null();
+        Self {
+            input_norm: n, post_norm: n, gate_proj: n, up_proj: n, down_proj: n, in_qkv: n, in_z: n, in_b: n,
+            in_a: n, out_proj: n, conv_w: n, norm_w: n, a_log: n, dt_bias: n, q_proj: n, k_proj: n, v_proj: n,
+            o_proj: n, q_norm: n, k_norm: n,
+        }
+    }
+}
+
+#[repr(C)]
+pub struct hk_kev_readout {
+    pub cu_positions_host: *const i32,
+    pub positions_host: *const i32,
+    pub cu_positions_dev: *const i32,
+    pub positions_dev: *const i32,
+    pub hidden_dev: *mut c_void,
+    pub pointer_scores_dev: *mut f32,
+}
+
+#[repr(C)]
+pub struct hk_bert_config {
+    pub hidden: c_int,
+    pub n_layers: c_int,
+    pub n_heads: c_int,
+    pub intermediate: c_int,
+    pub vocab: c_int,
+    pub eps: f32,
+    pub global_every: c_int,
+    pub local_window: c_int,
+    pub global_theta: f64,
+    pub local_theta: f64,
+    pub max_context: c_int,
+    pub n_out: c_int,
+}
+
+#[repr(C)]
+#[derive(Clone, Copy)]
+pub struct hk_bert_layer_weights {
+    pub attn_norm: *const c_void,
+    pub wqkv: *const c_void,
+    pub wo: *const c_void,
+    pub mlp_norm: *const c_void,
+    pub wi: *const c_void,
+    pub wo2: *const c_void,
+}
+
+extern "C" {
+    pub fn hk_ctx_create(device_ordinal: c_int, out: *mut *mut hk_ctx) -> c_int;
+    pub fn hk_ctx_destroy(ctx: *mut hk_ctx) -> c_int;
+    pub fn hk_ctx_set_stream(ctx: *mut hk_ctx, hip_stream: *mut c_void) -> c_int;
+    pub fn hk_ctx_stream(ctx: *mut hk_ctx) -> *mut c_void;
+    pub fn hk_ctx_own_stream(ctx: *mut hk_ctx) -> *mut c_void;
+    pub fn hk_ctx_synchronize(ctx: *mut hk_ctx) -> c_int;
+    pub fn hk_ctx_last_error(ctx: *mut hk_ctx) -> *const c_char;
+    pub fn hk_ctx_device_info(ctx: *mut hk_ctx, out: *mut hk_device_info_t) -> c_int;
+    pub fn hk_ctx_take_faults(ctx: *mut hk_ctx, faults_out: *mut c_int) -> c_int;
+    pub fn hk_device_count(out: *mut c_int) -> c_int;
+    pub fn hk_version() -> *const c_char;
+    pub fn hk_ctx_set_gemm_autotune(ctx: *mut hk_ctx, enable: c_int) -> c_int;
+    pub fn hk_ctx_gemm_plans(
+        ctx: *mut hk_ctx, buf: *mut c_char, len: usize, needed: *mut usize
+    ) -> c_int;
+    pub fn hk_buffer_alloc(ctx: *mut hk_ctx, bytes: usize, dev_out: *mut *mut c_void) -> c_int;
+    pub fn hk_buffer_free(ctx: *mut hk_ctx, dev: *mut c_void) -> c_int;
+    pub fn hk_memcpy_h2d(
+        ctx: *mut hk_ctx, dev_dst: *mut c_void, host_src: *const c_void, bytes: usize
+    ) -> c_int;
+    pub fn hk_memcpy_d2h(
+        ctx: *mut hk_ctx, host_dst: *mut c_void, dev_src: *const c_void, bytes: usize
+    ) -> c_int;
+    pub fn hk_rope_fill_table(
+        rotary_dim: c_int, theta: f64, max_pos: c_int, round_dtype: c_int, cos_host: *mut f32,
+        sin_host: *mut f32
+    ) -> c_int;
+    pub fn hk_qk_norm_rope_kv_write(
+        ctx: *mut hk_ctx, dtype: c_int, q_in_dev: *const c_void, q_in_tok: c_long, q_in_head: c_long,
+        k_in_dev: *const c_void, k_in_tok: c_long, v_in_dev: *const c_void, v_in_tok: c_long,
+        q_norm_eff_dev: *const f32, k_norm_eff_dev: *const f32, eps: f32, rope_cos_dev: *const f32,
+        rope_sin_dev: *const f32, rotary_dim: c_int, rope_max_pos: c_int, cu_seqlens_q_dev: *const i32,
+        context_lens_dev: *const i32, n_seqs: c_int, n_tokens: c_int, block_tables_dev: *const i32,
+        bt_stride: c_int, num_pages: c_int, page_size: c_int, q_heads: c_int, kv_heads: c_int,
+        head_dim: c_int, q_out_dev: *mut c_void, q_out_tok: c_long, q_out_head: c_long,
+        k_pool_dev: *mut c_void, v_pool_dev: *mut c_void
+    ) -> c_int;
+    pub fn hk_paged_kv_write(
+        ctx: *mut hk_ctx, dtype: c_int, k_dev: *const c_void, v_dev: *const c_void,
+        cu_seqlens_q_dev: *const i32, context_lens_dev: *const i32, n_seqs: c_int, n_tokens: c_int,
+        block_tables_dev: *const i32, bt_stride: c_int, num_pages: c_int, page_size: c_int,
+        kv_heads: c_int, head_dim: c_int, k_pool_dev: *mut c_void, v_pool_dev: *mut c_void
+    ) -> c_int;
+    pub fn hk_paged_prefill_attention(
+        ctx: *mut hk_ctx, dtype: c_int, q_dev: *const c_void, q_tok: c_long, q_head: c_long,
+        k_pool_dev: *const c_void, v_pool_dev: *const c_void, num_pages: c_int, page_size: c_int,
+        block_tables_dev: *const i32, bt_stride: c_int, cu_seqlens_q_dev: *const i32,
+        context_lens_dev: *const i32, n_seqs: c_int, n_tokens: c_int, max_q_len: c_int, q_heads: c_int,
+        kv_heads: c_int, head_dim: c_int, scale: f32, gate_dev: *const c_void, gate_tok: c_long,
+        gate_head: c_long, o_dev: *mut c_void, o_tok: c_long, o_head: c_long
+    ) -> c_int;
+    pub fn hk_gated_delta_chunked(
+        ctx: *mut hk_ctx, dtype: c_int, q_dev: *const c_void, q_tok: c_long, k_dev: *const c_void,
+        k_tok: c_long, v_dev: *const c_void, v_tok: c_long, g_dev: *const f32, beta_dev: *const f32,
+        cu_seqlens_dev: *const i32, n_seqs: c_int, n_tokens: c_int, heads: c_int, k_heads: c_int,
+        dk: c_int, dv: c_int, initial_state_dev: *const f32, final_state_dev: *mut f32,
+        o_dev: *mut c_void, o_tok: c_long
+    ) -> c_int;
+    pub fn hk_gdn_prep(
+        ctx: *mut hk_ctx, dtype: c_int, mixed_dev: *const c_void, mixed_tok: c_long,
+        conv_w_dev: *const f32, conv_k: c_int, conv_hist_dev: *const c_void, ba_dev: *const c_void,
+        ba_tok: c_long, b_col: c_int, a_col: c_int, base_g_dev: *const f32, dt_bias_dev: *const f32,
+        cu_seqlens_dev: *const i32, n_seqs: c_int, n_tokens: c_int, heads: c_int, k_heads: c_int,
+        q_out_dev: *mut c_void, k_out_dev: *mut c_void, v_out_dev: *mut c_void, g_out_dev: *mut f32,
+        beta_out_dev: *mut f32, conv_tail_out_dev: *mut c_void
+    ) -> c_int;
+    pub fn hk_gdn_fused(
+        ctx: *mut hk_ctx, dtype: c_int, mixed_dev: *const c_void, mixed_tok: c_long,
+        conv_w_dev: *const f32, conv_k: c_int, conv_hist_dev: *const c_void,
+        conv_tail_out_dev: *mut c_void, ba_dev: *const c_void, ba_tok: c_long, b_col: c_int,
+        a_col: c_int, base_g_dev: *const f32, dt_bias_dev: *const f32, z_dev: *const c_void,
+        z_tok: c_long, norm_w_dev: *const f32, eps: f32, cu_seqlens_dev: *const i32, n_seqs: c_int,
+        n_tokens: c_int, heads: c_int, k_heads: c_int, initial_state_dev: *const f32,
+        final_state_dev: *mut f32, out_dev: *mut c_void, out_tok: c_long
+    ) -> c_int;
+    pub fn hk_rms_norm(
+        ctx: *mut hk_ctx, dtype: c_int, x_dev: *const c_void, x_tok: c_long, w_eff_dev: *const f32,
+        eps: f32, rows: c_int, width: c_int, y_dev: *mut c_void, y_tok: c_long
+    ) -> c_int;
+    pub fn hk_gated_rms_norm(
+        ctx: *mut hk_ctx, dtype: c_int, x_dev: *const c_void, z_dev: *const c_void, z_tok: c_long,
+        heads: c_int, w_dev: *const f32, eps: f32, rows: c_int, width: c_int, y_dev: *mut c_void
+    ) -> c_int;
+    pub fn hk_swiglu(
+        ctx: *mut hk_ctx, dtype: c_int, gu_dev: *const c_void, gu_tok: c_long, up_off: c_long,
+        rows: c_int, width: c_int, y_dev: *mut c_void
+    ) -> c_int;
+    pub fn hk_lora_merge(
+        ctx: *mut hk_ctx, dtype: c_int, w_dev: *mut c_void, rows: c_int, cols: c_int,
+        a_dev: *const f32, b_dev: *const f32, rank: c_int, scale: f32
+    ) -> c_int;
+    pub fn hk_kev_model_create(
+        ctx: *mut hk_ctx, dtype: c_int, cfg: *const hk_kev_config,
+        layers_host: *const hk_kev_layer_weights, embed_dev: *const c_void,
+        final_norm_dev: *const c_void, head_w_dev: *const c_void, head_b_dev: *const f32,
+        out: *mut *mut hk_kev_model
+    ) -> c_int;
+    pub fn hk_kev_model_destroy(m: *mut hk_kev_model) -> c_int;
+    pub fn hk_kev_workspace_size(
+        m: *mut hk_kev_model, n_tokens: c_int, n_seqs: c_int, bytes_out: *mut usize
+    ) -> c_int;
+    pub fn hk_kev_forward(
+        m: *mut hk_kev_model, ids_dev: *const i32, cu_seqlens_dev: *const i32,
+        cu_seqlens_host: *const i32, n_seqs: c_int, block_tables_dev: *const i32, bt_stride: c_int,
+        num_pages: c_int, workspace_dev: *mut c_void, workspace_bytes: usize, logits_dev: *mut f32,
+        hidden_last_dev: *mut c_void
+    ) -> c_int;
+    pub fn hk_kev_model_identity(
+        m: *mut hk_kev_model, buf: *mut c_char, len: usize, needed: *mut usize
+    ) -> c_int;
+    pub fn hk_kev_model_set_pointer_head(
+        m: *mut hk_kev_model, head_dim: c_int, q_w_dev: *const f32, q_b_dev: *const f32,
+        k_w_dev: *const f32, k_b_dev: *const f32
+    ) -> c_int;
+    pub fn hk_kev_forward_readout(
+        m: *mut hk_kev_model, ids_dev: *const i32, cu_seqlens_dev: *const i32,
+        cu_seqlens_host: *const i32, n_seqs: c_int, block_tables_dev: *const i32, bt_stride: c_int,
+        num_pages: c_int, workspace_dev: *mut c_void, workspace_bytes: usize,
+        readout: *const hk_kev_readout, logits_dev: *mut f32
+    ) -> c_int;
+    pub fn hk_kev_cache_create(
+        m: *mut hk_kev_model, max_pages: c_int, max_handles: c_int, out: *mut *mut hk_kev_cache
+    ) -> c_int;
+    pub fn hk_kev_cache_destroy(c: *mut hk_kev_cache) -> c_int;
+    pub fn hk_kev_cache_open(c: *mut hk_kev_cache, handle_out: *mut u64) -> c_int;
+    pub fn hk_kev_cache_fork(c: *mut hk_kev_cache, parent: u64, child_out: *mut u64) -> c_int;
+    pub fn hk_kev_cache_release(c: *mut hk_kev_cache, handle: u64) -> c_int;
+    pub fn hk_kev_cache_tokens(c: *mut hk_kev_cache, handle: u64, tokens_out: *mut c_int) -> c_int;
+    pub fn hk_kev_cache_stats(
+        c: *mut hk_kev_cache, live_handles: *mut c_int, free_pages: *mut c_int
+    ) -> c_int;
+    pub fn hk_kev_cache_workspace_size(
+        c: *mut hk_kev_cache, n_tokens: c_int, n_seqs: c_int, bytes_out: *mut usize
+    ) -> c_int;
+    pub fn hk_kev_forward_cached(
+        c: *mut hk_kev_cache, handles_host: *const u64, n_seqs: c_int, ids_dev: *const i32,
+        cu_seqlens_dev: *const i32, cu_seqlens_host: *const i32, workspace_dev: *mut c_void,
+        workspace_bytes: usize, logits_dev: *mut f32, hidden_last_dev: *mut c_void
+    ) -> c_int;
+    pub fn hk_kev_forward_cached_readout(
+        c: *mut hk_kev_cache, handles_host: *const u64, n_seqs: c_int, ids_dev: *const i32,
+        cu_seqlens_dev: *const i32, cu_seqlens_host: *const i32, workspace_dev: *mut c_void,
+        workspace_bytes: usize, readout: *const hk_kev_readout, logits_dev: *mut f32
+    ) -> c_int;
+    pub fn hk_layer_norm(
+        ctx: *mut hk_ctx, dtype: c_int, x_dev: *const c_void, x_tok: c_long, w_dev: *const f32,
+        eps: f32, rows: c_int, width: c_int, y_dev: *mut c_void, y_tok: c_long
+    ) -> c_int;
+    pub fn hk_bidir_attention(
+        ctx: *mut hk_ctx, dtype: c_int, q_dev: *const c_void, q_tok: c_long, k_dev: *const c_void,
+        k_tok: c_long, v_dev: *const c_void, v_tok: c_long, cu_seqlens_dev: *const i32, n_seqs: c_int,
+        n_tokens: c_int, max_len: c_int, heads: c_int, head_dim: c_int, half_window: c_int, scale: f32,
+        o_dev: *mut c_void, o_tok: c_long
+    ) -> c_int;
+    pub fn hk_bert_model_create(
+        ctx: *mut hk_ctx, dtype: c_int, cfg: *const hk_bert_config,
+        layers_host: *const hk_bert_layer_weights, embed_dev: *const c_void,
+        emb_norm_dev: *const c_void, final_norm_dev: *const c_void, head_w_dev: *const c_void,
+        head_b_dev: *const f32, out: *mut *mut hk_bert_model
+    ) -> c_int;
+    pub fn hk_bert_model_destroy(m: *mut hk_bert_model) -> c_int;
+    pub fn hk_bert_workspace_size(
+        m: *mut hk_bert_model, n_tokens: c_int, bytes_out: *mut usize
+    ) -> c_int;
+    pub fn hk_bert_model_identity(
+        m: *mut hk_bert_model, buf: *mut c_char, len: usize, needed: *mut usize
+    ) -> c_int;
+    pub fn hk_bert_forward(
+        m: *mut hk_bert_model, ids_dev: *const i32, cu_seqlens_dev: *const i32,
+        cu_seqlens_host: *const i32, n_seqs: c_int, workspace_dev: *mut c_void, workspace_bytes: usize,
+        logits_dev: *mut f32, hidden_out_dev: *mut c_void
+    ) -> c_int;
+    pub fn hk_mean_pool_workspace_size(n_seqs: c_int, width: c_int, bytes_out: *mut usize) -> c_int;
+    pub fn hk_mean_pool_head(
+        ctx: *mut hk_ctx, dtype: c_int, x_dev: *const c_void, x_tok: c_long,
+        cu_seqlens_dev: *const i32, n_seqs: c_int, n_tokens: c_int, width: c_int,
+        head_w_dev: *const c_void, head_b_dev: *const f32, n_out: c_int, logits_dev: *mut f32,
+        workspace_dev: *mut c_void, workspace_bytes: usize
+    ) -> c_int;
+    pub fn hk_mean_pool_head_noalloc(
+        ctx: *mut hk_ctx, dtype: c_int, x_dev: *const c_void, x_tok: c_long,
+        cu_seqlens_dev: *const i32, n_seqs: c_int, n_tokens: c_int, width: c_int,
+        head_w_dev: *const c_void, head_b_dev: *const f32, n_out: c_int, logits_dev: *mut f32
+    ) -> c_int;
+    pub fn hk_calibrate(
+        logits_host: *const f32, n: c_int, temperature: f32, probs_host: *mut f32
+    ) -> c_int;
+    pub fn hk_synth_normal(
+        seed: u64, stream: u64, out_host: *mut f32, n: usize, mean: f32, std: f32
+    ) -> c_int;
+    pub fn hk_synth_normal_bf16(
+        seed: u64, stream: u64, out_host: *mut u16, n: usize, mean: f32, std: f32
+    ) -> c_int;
+    pub fn hk_synth_uniform_int(
+        seed: u64, stream: u64, out_host: *mut i32, n: usize, lo: i32, hi: i32
+    ) -> c_int;
+    pub fn hk_synth_permutation(seed: u64, stream: u64, out_host: *mut i32, n: i32) -> c_int;
+}
+
+// ---------------------------------------------------------------------------------------------
+// RAII layer
+// ---------------------------------------------------------------------------------------------
+
+/// How a status code maps onto huncho's flat error type (error.rs:11-38).
+#[derive(Debug, Clone, Copy, PartialEq, Eq)]
+pub enum ErrorKind {
+    Invalid,
+    Unsupported,
+    Device,
+    NoMemory,
+}
+
+#[derive(Debug, Clone)]
+pub struct HkError {
+    pub kind: ErrorKind,
+    pub code: c_int,
+    pub message: String,
+}
+
+impl std::fmt::Display for HkError {
+    fn fmt(&self, f: &mut std::fmt::Formatter<'_>) -> std::fmt::Result {
+        write!(f, "rocm ({:?}): {}", self.kind, self.message)
+    }
+}
+
+impl std::error::Error for HkError {}
+
+pub type Result<T> = std::result::Result<T, HkError>;
+
+/// Turns a status into `Result`, reading the context's last error message.
+pub fn check(ctx: *mut hk_ctx, rc: c_int) -> Result<()> {
+    if rc == HK_OK {
+        return Ok(());
+    }
+    let message = if ctx.is_null() {
+        "no context".to_string()
+    } else {
+        unsafe { CStr::from_ptr(hk_ctx_last_error(ctx)) }.to_string_lossy().into_owned()
+    };
+    let kind = match rc {
+        HK_ERR_INVALID => ErrorKind::Invalid,
+        HK_ERR_UNSUPPORTED => ErrorKind::Unsupported,
+        HK_ERR_NOMEM => ErrorKind::NoMemory,
+        _ => ErrorKind::Device,
+    };
+    Err(HkError { kind, code: rc, message })
+}
+
+/// A device context (`HUNCHO_DEVICE=rocm[:N]`, device.rs:12-72). `new` fails with
+/// `ErrorKind::Unsupported` when no gfx950 GPU is visible.
+pub struct Context(*mut hk_ctx);
+
+unsafe impl Send for Context {}
+
+impl Context {
+    pub fn new(ordinal: usize) -> Result<Self> {
+        let mut h = std::ptr::null_mut();
+        check(std::ptr::null_mut(), unsafe { hk_ctx_create(ordinal as c_int, &mut h) })?;
+        Ok(Self(h))
+    }
+
+    pub fn raw(&self) -> *mut hk_ctx {
+        self.0
+    }
+
+    pub fn synchronize(&self) -> Result<()> {
+        check(self.0, unsafe { hk_ctx_synchronize(self.0) })
+    }
+
+    /// The HK_FAULT_* bits raised since the last call (synchronises).
+    pub fn take_faults(&self) -> Result<c_int> {
+        let mut f = 0;
+        check(self.0, unsafe { hk_ctx_take_faults(self.0, &mut f) })?;
+        Ok(f)
+    }
+}
+
+impl Drop for Context {
+    fn drop(&mut self) {
+        unsafe {
+            hk_ctx_destroy(self.0);
+        }
+    }
+}
+
+/// Device memory owned by a context (hk_buffer_alloc / hk_buffer_free).
+pub struct Buffer {
+    ctx: *mut hk_ctx,
+    pub ptr: *mut c_void,
+    pub bytes: usize,
+}
+
+unsafe impl Send for Buffer {}
+
+impl Buffer {
+    pub fn new(ctx: &Context, bytes: usize) -> Result<Self> {
+        let mut p = std::ptr::null_mut();
+        check(ctx.raw(), unsafe { hk_buffer_alloc(ctx.raw(), bytes.max(1), &mut p) })?;
+        Ok(Self { ctx: ctx.raw(), ptr: p, bytes })
+    }
+
+    pub fn upload(ctx: &Context, host: &[u8]) -> Result<Self> {
+        let b = Self::new(ctx, host.len())?;
+        check(ctx.raw(), unsafe { hk_memcpy_h2d(ctx.raw(), b.ptr, host.as_ptr().cast(), host.len()) })?;
+        Ok(b)
+    }
+
+    pub fn download(&self, host: &mut [u8]) -> Result<()> {
+        let n = host.len().min(self.bytes);
+        check(self.ctx, unsafe { hk_memcpy_d2h(self.ctx, host.as_mut_ptr().cast(), self.ptr, n) })
+    }
+}
+
+impl Drop for Buffer {
+    fn drop(&mut self) {
+        unsafe {
+            hk_buffer_free(self.ctx, self.ptr);
+        }
+    }
+}
+
+/// A Kev/Qwen3.5 model on the device (hk_kev_model_create copies and fuses the weights).
+pub struct KevModel {
+    ctx: *mut hk_ctx,
+    raw: *mut hk_kev_model,
+}
+
+unsafe impl Send for KevModel {}
+
+impl KevModel {
+    /// # Safety
+    /// `layers` holds one entry per layer with device pointers valid for the call.
+    pub unsafe fn create(
+        ctx: &Context, dtype: c_int, cfg: &hk_kev_config, layers: &[hk_kev_layer_weights], embed: *const c_void,
+        final_norm: *const c_void, head_w: *const c_void, head_b: *const f32,
+    ) -> Result<Self> {
+        if layers.len() != cfg.n_layers as usize {
+            return Err(HkError { kind: ErrorKind::Invalid, code: HK_ERR_INVALID, message: "layer count".into() });
+        }
+        let mut m = std::ptr::null_mut();
+        check(ctx.raw(), hk_kev_model_create(ctx.raw(), dtype, cfg, layers.as_ptr(), embed, final_norm, head_w,
+                                             head_b, &mut m))?;
+        Ok(Self { ctx: ctx.raw(), raw: m })
+    }
+
+    pub fn raw(&self) -> *mut hk_kev_model {
+        self.raw
+    }
+
+    pub fn workspace_size(&self, n_tokens: usize, n_seqs: usize) -> Result<usize> {
+        let mut b = 0usize;
+        check(self.ctx, unsafe { hk_kev_workspace_size(self.raw, n_tokens as c_int, n_seqs as c_int, &mut b) })?;
+        Ok(b)
+    }
+
+    /// Capabilities.extra execution keys (qwen3_5.rs:2540-2653) as (key, value) pairs.
+    pub fn identity(&self) -> Vec<(String, String)> {
+        let mut need = 0usize;
+        unsafe { hk_kev_model_identity(self.raw, std::ptr::null_mut(), 0, &mut need) };
+        let mut buf = vec![0 as c_char; need.max(1)];
+        unsafe { hk_kev_model_identity(self.raw, buf.as_mut_ptr(), buf.len(), &mut need) };
+        let text = unsafe { CStr::from_ptr(buf.as_ptr()) }.to_string_lossy().into_owned();
+        text.lines().filter_map(|l| l.split_once('=')).map(|(k, v)| (k.to_string(), v.to_string())).collect()
+    }
+}
+
+impl Drop for KevModel {
+    fn drop(&mut self) {
+        unsafe {
+            hk_kev_model_destroy(self.raw);
+        }
+    }
+}
+
+/// The device prefix cache of a KevModel (the Backend trait's prefill / fork / release_cache).
+pub struct KevCache {
+    ctx: *mut hk_ctx,
+    raw: *mut hk_kev_cache,
+}
+
+unsafe impl Send for KevCache {}
+
+impl KevCache {
+    pub fn new(model: &KevModel, max_pages: usize, max_handles: usize) -> Result<Self> {
+        let mut c = std::ptr::null_mut();
+        check(model.ctx, unsafe { hk_kev_cache_create(model.raw, max_pages as c_int, max_handles as c_int, &mut c) })?;
+        Ok(Self { ctx: model.ctx, raw: c })
+    }
+
+    pub fn raw(&self) -> *mut hk_kev_cache {
+        self.raw
+    }
+
+    pub fn open(&self) -> Result<u64> {
+        let mut h = 0u64;
+        check(self.ctx, unsafe { hk_kev_cache_open(self.raw, &mut h) })?;
+        Ok(h)
+    }
+
+    pub fn fork(&self, parent: u64) -> Result<u64> {
+        let mut h = 0u64;
+        check(self.ctx, unsafe { hk_kev_cache_fork(self.raw, parent, &mut h) })?;
+        Ok(h)
+    }
+
+    pub fn release(&self, handle: u64) -> Result<()> {
+        check(self.ctx, unsafe { hk_kev_cache_release(self.raw, handle) })
+    }
+}
+
+impl Drop for KevCache {
+    fn drop(&mut self) {
+        unsafe {
+            hk_kev_cache_destroy(self.raw);
+        }
+    }
+}
+
+/// A ModernBERT encoder on the device (the Laya backend's model).
+pub struct BertModel {
+    ctx: *mut hk_ctx,
+    raw: *mut hk_bert_model,
+}
+
+unsafe impl Send for BertModel {}
+
+impl BertModel {
+    /// # Safety
+    /// `layers` holds one entry per layer with device pointers valid for the call.
+    pub unsafe fn create(
+        ctx: &Context, dtype: c_int, cfg: &hk_bert_config, layers: &[hk_bert_layer_weights], embed: *const c_void,
+        emb_norm: *const c_void, final_norm: *const c_void, head_w: *const c_void, head_b: *const f32,
+    ) -> Result<Self> {
+        let mut m = std::ptr::null_mut();
+        check(ctx.raw(), hk_bert_model_create(ctx.raw(), dtype, cfg, layers.as_ptr(), embed, emb_norm, final_norm,
+                                              head_w, head_b, &mut m))?;
+        Ok(Self { ctx: ctx.raw(), raw: m })
+    }
+
+    pub fn raw(&self) -> *mut hk_bert_model {
+        self.raw
+    }
+
+    pub fn workspace_size(&self, n_tokens: usize) -> Result<usize> {
+        let mut b = 0usize;
+        check(self.ctx, unsafe { hk_bert_workspace_size(self.raw, n_tokens as c_int, &mut b) })?;
+        Ok(b)
+    }
+}
+
+impl Drop for BertModel {
+    fn drop(&mut self) {
+        unsafe {
+            hk_bert_model_destroy(self.raw);
+        }
+    }
+}
