@@ -111,6 +111,30 @@ def kernel_rooflines(ctx, shape, n_seqs, seq_len, dtype, iters):
     attn_flops = 4.0 * hq * d * seq_len * (seq_len + 1) / 2 * n_seqs
     attn_bytes = n * (2 * hq + 2 * hkv) * d * 2
 
+    # the varlen paged GQA prefill batch: 32 sequences with seeded lengths in [64, 2048], pages
+    # of 16 from a seeded permutation of a 4096-page pool (the compute-bound attention shape)
+    vl = [int(x) for x in abi.synth_uniform_int(20261201, 20, 32, 64, 2048)]
+    vn = sum(vl)
+    vcu = torch.from_numpy(np.concatenate([[0], np.cumsum(vl)]).astype(np.int32)).to(dev)
+    vlens = torch.tensor(vl, dtype=torch.int32, device=dev)
+    vperm = abi.synth_permutation(20261201, 11, 4096)
+    vneed = [(L + P - 1) // P for L in vl]
+    vbt_np = np.full((32, max(vneed)), -1, np.int32)
+    k0 = 0
+    for s_, m_ in enumerate(vneed):
+        vbt_np[s_, :m_] = vperm[k0:k0 + m_]
+        k0 += m_
+    vbt = torch.from_numpy(vbt_np).to(dev)
+    vkp = torch.randn((4096, hkv, P, d), generator=g, device=dev, dtype=torch.float32).to(dtype)
+    vvp = torch.randn((4096, hkv, P, d), generator=g, device=dev, dtype=torch.float32).to(dtype)
+    vq = torch.randn((vn, hq, d), generator=g, device=dev, dtype=torch.float32).to(dtype)
+    vo = torch.empty_like(vq)
+    t_var = time_launches(lambda: paged_prefill_attention(ctx, vq, vkp, vvp, vbt, vcu, vlens, max(vl), out=vo),
+                          iters, stream)
+    var_flops = sum(4.0 * hq * d * L * (L + 1) / 2 for L in vl)
+    var_bytes = vn * (2 * hq + 2 * hkv) * d * 2
+    del vkp, vvp, vq, vo
+
     # the fused Gated DeltaNet layer kernel the forward runs: in_proj rows [q | k | v | z]
     # (8192 columns) and [b | a] rows as the GEMMs write them, conv weights, A_log, dt_bias
     H, Hk = shape.lin_n_v_heads, shape.lin_n_k_heads
@@ -142,6 +166,7 @@ def kernel_rooflines(ctx, shape, n_seqs, seq_len, dtype, iters):
     torch.cuda.synchronize()
     return {
         "attention": {"seconds": t_attn, "flops": attn_flops, "bytes": attn_bytes},
+        "attention_varlen": {"seconds": t_var, "flops": var_flops, "bytes": var_bytes},
         "delta_rule_fused": {"seconds": t_fused, "flops": gdn_flops, "bytes": fused_bytes},
         "delta_rule": {"seconds": t_gdn, "flops": gdn_flops, "bytes": gdn_bytes},
     }
@@ -596,6 +621,13 @@ def run_kev(args, dtype):
                      "frac": round(attn_achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": traffic_of("attention"),
                      "us_per_launch": round(a["seconds"] * 1e6, 2), "flops_per_launch": a["flops"],
                      "hbm_frac": round(a["bytes"] / a["seconds"] / HBM_PEAK, 4)},
+        "roofline_attention_varlen": {
+            "kernel": "paged_prefill_attn (32 sequences, lengths 64..2048, no gate)", "bound": "mfma",
+            "achieved": round(kr["attention_varlen"]["flops"] / kr["attention_varlen"]["seconds"] / 1e12, 2),
+            "peak": MFMA_PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+            "frac": round(kr["attention_varlen"]["flops"] / kr["attention_varlen"]["seconds"] / MFMA_PEAK_BF16, 4),
+            "us_per_launch": round(kr["attention_varlen"]["seconds"] * 1e6, 2),
+            "flops_per_launch": kr["attention_varlen"]["flops"]},
         "roofline_delta_rule": hbm_line("gdn_chunk16<fused> (the forward's Gated DeltaNet layer kernel)", gf,
                                         "delta_rule_fused"),
         "roofline_delta_rule_standalone": hbm_line("gdn_chunk16 (standalone recurrence)", gd, "delta_rule"),

@@ -87,6 +87,7 @@ SIGNATURES = {
     "hk_ctx_take_faults": (I, [vp, C.POINTER(I)]),
     "hk_ctx_set_gemm_autotune": (I, [vp, I]),
     "hk_ctx_gemm_plans": (I, [vp, C.c_char_p, SZ, C.POINTER(SZ)]),
+    "hk_linear": (I, [vp, I, I, vp, L, vp, L, I, I, I, vp, L, vp, L]),
     "hk_buffer_alloc": (I, [vp, C.c_size_t, C.POINTER(vp)]),
     "hk_buffer_free": (I, [vp, vp]),
     "hk_memcpy_h2d": (I, [vp, vp, vp, C.c_size_t]),

@@ -43,3 +43,7 @@ int hk_mean_pool_check(hk_ctx* ctx, int dtype, const void* x, long x_tok, const 
 int hk_noalloc_scratch_init(int device);
 // Writes sorted "key=value" lines (NUL-terminated, truncated to len) and the full length + 1.
 int hk_write_identity(std::vector<std::pair<std::string, std::string>> kv, char* buf, size_t len, size_t* needed);
+// The library's MFMA GEMM with a fused epilogue (hk::EPI_*); HK_ERR_UNSUPPORTED, with no error
+// message set, for shapes or dtypes it does not cover.
+int hk_gemm_native(hk_ctx* ctx, int dtype, int epi, int n, int out, int in, const void* x, long ldx, const void* w,
+                   long ldw, void* y, long ldy, const void* c, long ldc);

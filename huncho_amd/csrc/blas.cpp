@@ -324,3 +324,33 @@ extern "C" int hk_ctx_gemm_plans(hk_ctx* ctx, char* buf, size_t len, size_t* nee
     }
     return HK_OK;
 }
+
+// The library's own MFMA GEMM (gemm.hip) for 16-bit operands: N a multiple of 256, K of 64, rows
+// 16-byte aligned. Returns HK_ERR_UNSUPPORTED (without an error message) for other shapes.
+int hk_gemm_native(hk_ctx* ctx, int dtype, int epi, int n, int out, int in, const void* x, long ldx, const void* w,
+                   long ldw, void* y, long ldy, const void* c, long ldc) {
+    if (dtype != HK_BF16 && dtype != HK_F16) return HK_ERR_UNSUPPORTED;
+    if (out % 256 || in % 64 || n < 0 || ldx % 8 || ldw % 8 || ldy % 8 || (epi == hk::EPI_RESIDUAL && ldc % 8) ||
+        (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y | (uintptr_t)(c ? c : y)) & 15))
+        return HK_ERR_UNSUPPORTED;
+    if (n == 0) return HK_OK;
+    hk::GemmArgs a{x, w, c, y, ldx, ldw, ldc, ldy, n, out, in};
+    return hk_launch_gemm(dtype, epi, &a, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "gemm launch failed") : HK_OK;
+}
+
+extern "C" int hk_linear(hk_ctx* ctx, int dtype, int epilogue, const void* x, long ldx, const void* w, long ldw,
+                         int rows, int out, int in, const void* c, long ldc, void* y, long ldy) {
+    if (!ctx) return HK_ERR_INVALID;
+    if (!x || !w || !y || rows < 0 || out <= 0 || in <= 0 || epilogue < 0 || epilogue > 2 ||
+        (epilogue == hk::EPI_RESIDUAL && !c))
+        return hk_fail(ctx, HK_ERR_INVALID, "linear: bad arguments");
+    const int y_cols = epilogue == hk::EPI_SWIGLU ? out / 2 : out;
+    if (ldx < in || ldw < in || ldy < y_cols || (c && ldc < out))
+        return hk_fail(ctx, HK_ERR_INVALID, "linear: row strides smaller than the rows");
+    hipSetDevice(ctx->device);
+    const int rc = hk_gemm_native(ctx, dtype, epilogue, rows, out, in, x, ldx, w, ldw, y, ldy, c, ldc);
+    if (rc == HK_ERR_UNSUPPORTED)
+        return hk_fail(ctx, rc, "linear: 16-bit dtype, out %% 256 == 0, in %% 64 == 0 and 16-byte aligned rows "
+                                "are required (got out %d, in %d)", out, in);
+    return rc;
+}

@@ -1,0 +1,240 @@
+// gemm.hip - dense projections on gfx950 MFMA: Y[m][n] = sum_k X[m][k] W[n][k] (candle Linear,
+// crates/huncho-backend/src/qwen3_5.rs:306-515) with fused epilogues:
+//   EPI_STORE     Y = T(acc)
+//   EPI_RESIDUAL  Y = T(acc + C)            (the residual add of DecoderLayer::forward, 1083-1104)
+//   EPI_SWIGLU    Y = T(silu(T(g)) * T(u))   (Mlp::forward 1020-1031 / gate_cpu::silu_mul 8-47:
+//                                            gate and up are the rounded GEMM outputs, as the
+//                                            reference stores them, then silu(g) * u in fp32)
+// bf16 / fp16 operands, fp32 accumulation (v_mfma_f32_32x32x16_{bf16,f16}).
+//
+// Tiling: one workgroup of 4 waves (one per SIMD) computes a 256 (n) x 256 (m) tile; wave
+// (wn, wm) owns n rows 128 wn .. + 127 and m rows 128 wm .. + 127 as 4 x 4 MFMA blocks of
+// 32 x 32 (256 fp32 accumulators per lane, in AGPRs). With one wave per SIMD the LDS reads are
+// software-pipelined: the fragments of the next k16 step are read while the 16 MFMAs of the
+// current one run, across the per-step barrier too (scheduling fences keep that order). The W tile is the MFMA A operand and the X tile the B operand, so each
+// lane's accumulator holds one output row m (lane % 32) and 16 columns n in 4 runs of 4
+// consecutive ones: outputs leave as 8-byte stores, and with the SwiGLU weight layout below a
+// lane holds each gate column and its up column.
+// K steps of 32: W and X tiles (256 rows x 64 B each) go from global memory straight into LDS
+// (global_load_lds_dwordx4) through a ring of 4 stages (4 x 32 KB), issued 3 steps ahead, so a
+// step's loads have three steps of MFMA work (about 1.3 us) to arrive from the L2 or the
+// Infinity Cache. A row's 16-byte chunk c sits at physical chunk c ^ ((row >> 2) & 3): the 16
+// rows that one 16-lane group of a ds_read_b128 reads then land in 16 distinct 16-byte slots of
+// the 256-byte bank row.
+// Tiles: the grid is (tiles); tile ids are taken XCD-major (workgroup b runs on XCD b % 8, and
+// the tiles of one XCD form a contiguous range), and inside an XCD's range 4 m-panels are swept
+// across all n-panels before the next 4, so the operand slices the concurrent tiles share stay
+// in that XCD's L2.
+//
+// SwiGLU layout: the fused weight holds blocks of 32 rows, [gate rows 16 b .. 16 b + 15 |
+// up rows 16 b .. 16 b + 15]; output column 16 b + i pairs fused rows 32 b + i and 32 b + 16 + i,
+// which one lane holds at accumulator elements (jj, r) and (jj + 2, r).
+#include "common.hpp"
+#include "kernel_args.hpp"
+
+namespace hk {
+namespace gemm {
+
+constexpr int BM = 256, BN = 256, BK = 32, NTHREADS = 256, NWAVES = 4, STAGES = 4;
+constexpr int MB = 4;                     // 32-row m blocks per wave
+constexpr int ROW_BYTES = BK * 2;         // 64
+constexpr int TILE_BYTES = 256 * ROW_BYTES;  // one operand tile of one stage: 16 KB
+constexpr size_t LDS_BYTES = (size_t)STAGES * 2 * TILE_BYTES;
+// s_waitcnt encoding of vmcnt(n) with expcnt and lgkmcnt at their maxima (vmcnt bits 3:0 and
+// 15:14)
+constexpr int vmcnt_enc(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+// vmcnt(8): the copies of the stage issued after this one may stay in flight (each wave issues 8
+// copies per stage)
+constexpr int VMCNT_1STAGE = vmcnt_enc(8);
+
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+
+template <typename T> __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+
+template <typename T, int EPI>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_xwt(GemmArgs a) {
+    typedef typename Mma16<T>::v8 v8;
+    typedef typename Mma16<T>::v4 v4;
+    extern __shared__ __attribute__((aligned(16))) char gsm[];
+    // An AGPR clobber keeps the compiler from marking the kernel AGPR-free, so it selects the
+    // MFMA form that accumulates in AGPRs: the 256 accumulators live there and the VGPRs hold
+    // operands and addresses (otherwise they sit in VGPRs and shuttle through AGPRs as spills).
+    asm volatile("" ::: "a0");
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wn = wave >> 1, wm = wave & 1;
+    const int n_tiles_n = a.N / BN, n_tiles_m = (a.M + BM - 1) / BM;
+    const int total = n_tiles_n * n_tiles_m;
+    // XCD-major tile order, then 4 m-panels across every n-panel (4 gave 7 % more than 8 or 2
+    // at 16384 x 4096 x 8192)
+    const int b = blockIdx.x;
+    int t = b;
+    if ((total & 7) == 0) t = (b & 7) * (total >> 3) + (b >> 3);
+    const int group = 4 * n_tiles_n;
+    const int g0 = (t / group) * 4;
+    const int gm = min(4, n_tiles_m - g0);
+    const int tm = g0 + (t % group) % gm, tn = (t % group) / gm;
+    const int n0 = tn * BN, m0 = tm * BM;
+
+    // copies: lane i of a copy writes LDS row R0 + i / 4 at physical chunk i % 4, holding logical
+    // chunk (i % 4) ^ swz(row) of that row; a wave copies rows 64 wave .. + 63 of each operand
+    // tile (4 copies of 16 rows). For copy c the row is 64 wave + 16 c + i / 4, so swz(row) =
+    // (i / 16) & 3 (the same for every copy), and copy c adds 16 c rows.
+    const int crow = lane >> 2, cpc = lane & 3;
+    const int lc = cpc ^ ((crow >> 2) & 3);
+    const T* const wsrc = (const T*)a.w + (long)(n0 + 64 * wave + crow) * a.ldw + 8 * lc;
+    const long xr0 = m0 + 64 * wave + crow;
+    // X rows past M read row M - 1 (their outputs are not stored)
+    const bool x_tail = m0 + BM > a.M;
+    const T* const xbase = (const T*)a.x;
+    const unsigned lbase = lds_address(gsm);
+    auto load_step = [&](int ks, int buf) {
+        const unsigned wb = lbase + buf * 2 * TILE_BYTES, xb = wb + TILE_BYTES;
+        const long ko = (long)ks * BK;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const unsigned dst = (unsigned)((64 * wave + 16 * c) * ROW_BYTES);
+            copy_x4(wsrc + (long)(16 * c) * a.ldw + ko, wb + dst);
+            const long xr = x_tail ? min(xr0 + 16 * c, (long)a.M - 1) : xr0 + 16 * c;
+            copy_x4(xbase + xr * a.ldx + 8 * lc + ko, xb + dst);
+        }
+    };
+
+    // MFMA operand reads: block i (32 rows) of this wave's rows, k16-step s of the 32: lane l reads
+    // row 32 i + l % 32, logical chunk 2 s + l / 32. The blocks start at multiples of 16 rows, so
+    // the swizzle depends on l % 32 alone and block i adds 32 i rows (2 KB).
+    const int g = lane >> 5, lr = lane & 31;
+    const int sw = swz(lr);
+    const int abase = (128 * wn + lr) * ROW_BYTES, bbase = (128 * wm + lr) * ROW_BYTES;
+    f32x16 acc[4][MB];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) acc[i][j] = f32x16{};
+
+    const int nk = a.K / BK;
+    // fragments of k16 step (ks, s2) live in set s2: af/bf[s2][block]
+    v8 af[2][4], bf[2][MB];
+    auto read_frags = [&](int ks, int s2) {
+        const char* wt = gsm + (ks % STAGES) * 2 * TILE_BYTES;
+        const char* xt = wt + TILE_BYTES;
+        const int co = ((2 * s2 + g) ^ sw) << 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[s2][i] = *(const v8*)(wt + abase + co + 2048 * i);
+#pragma unroll
+        for (int j = 0; j < MB; ++j) bf[s2][j] = *(const v8*)(xt + bbase + co + 2048 * j);
+    };
+    auto mfmas = [&](int s2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < MB; ++j) acc[i][j] = Mma16<T>::mma(af[s2][i], bf[s2][j], acc[i][j]);
+    };
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+        if (st < nk) load_step(st, st);
+    // step 0's copies (steps 1 and 2 may still fly)
+    if (nk >= 3)
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(16));
+    else if (nk == 2)
+        __builtin_amdgcn_s_waitcnt(VMCNT_1STAGE);
+    else
+        __builtin_amdgcn_s_waitcnt(VMCNT0);
+    __syncthreads();
+    read_frags(0, 0);
+    for (int ks = 0; ks < nk; ++ks) {
+        read_frags(ks, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(0);
+        __builtin_amdgcn_sched_barrier(0);
+        // step ks + 1's copies are done (step ks + 2's may still fly); the barrier publishes every
+        // wave's, and every wave has finished reading step ks - 1's buffer, which takes step ks + 3
+        if (ks + 1 < nk) {
+            if (ks + 2 < nk)
+                __builtin_amdgcn_s_waitcnt(VMCNT_1STAGE);
+            else
+                __builtin_amdgcn_s_waitcnt(VMCNT0);
+            __syncthreads();
+            if (ks + STAGES - 1 < nk) load_step(ks + STAGES - 1, (ks + STAGES - 1) % STAGES);
+            read_frags(ks + 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // epilogue: lane holds output row m = m0 + 128 wm + 32 j + lr and, per block i, columns
+    // n = n0 + 128 wn + 32 i + 8 jj + 4 g + r (jj, r = 0..3) at element 4 jj + r
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+        const int m = m0 + 32 * MB * wm + 32 * j + lr;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (EPI == EPI_SWIGLU) {
+                // fused rows 32 blk + (8 jj + 4 g + r): gate for jj < 2, its up at jj + 2
+                const int blk = (n0 + 128 * wn + 32 * i) >> 5;
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    v4 o;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float gv = to_f(from_f<T>(acc[i][j][4 * jj + r]));
+                        const float uv = to_f(from_f<T>(acc[i][j][4 * (jj + 2) + r]));
+                        o[r] = from_f<T>(silu_f<T>(gv) * uv);
+                    }
+                    *(v4*)((T*)a.y + (long)m * a.ldy + 16 * blk + 8 * jj + 4 * g) = o;
+                }
+            } else {
+                const int nb = n0 + 128 * wn + 32 * i;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int n = nb + 8 * jj + 4 * g;
+                    v4 o;
+                    if (EPI == EPI_RESIDUAL) {
+                        const v4 cv = *(const v4*)((const T*)a.c + (long)m * a.ldc + n);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[r] = from_f<T>(acc[i][j][4 * jj + r] + to_f(cv[r]));
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[r] = from_f<T>(acc[i][j][4 * jj + r]);
+                    }
+                    *(v4*)((T*)a.y + (long)m * a.ldy + n) = o;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace gemm
+}  // namespace hk
+
+template <typename T, int EPI>
+static int launch_gemm(const hk::GemmArgs* a, hipStream_t stream) {
+    static bool configured = false;
+    auto kern = hk::gemm::gemm_xwt<T, EPI>;
+    if (!configured) {
+        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)hk::gemm::LDS_BYTES) != hipSuccess)
+            return HK_ERR_DEVICE;
+        configured = true;
+    }
+    const int tiles = (a->N / hk::gemm::BN) * ((a->M + hk::gemm::BM - 1) / hk::gemm::BM);
+    hipLaunchKernelGGL(kern, dim3(tiles), dim3(hk::gemm::NTHREADS), hk::gemm::LDS_BYTES, stream, *a);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+// dtype16: 1 = bf16, 2 = fp16. Shapes are validated by the caller: N % 256 == 0, K % 64 == 0,
+// M >= 1, 16-byte aligned rows (ld % 8 == 0).
+extern "C" int hk_launch_gemm(int dtype16, int epi, const hk::GemmArgs* a, hipStream_t stream) {
+    using namespace hk;
+    if (a->M == 0) return HK_OK;
+    if (dtype16 == DT_BF16) {
+        if (epi == EPI_RESIDUAL) return launch_gemm<bf16, EPI_RESIDUAL>(a, stream);
+        if (epi == EPI_SWIGLU) return launch_gemm<bf16, EPI_SWIGLU>(a, stream);
+        return launch_gemm<bf16, EPI_STORE>(a, stream);
+    }
+    if (epi == EPI_RESIDUAL) return launch_gemm<f16, EPI_RESIDUAL>(a, stream);
+    if (epi == EPI_SWIGLU) return launch_gemm<f16, EPI_SWIGLU>(a, stream);
+    return launch_gemm<f16, EPI_STORE>(a, stream);
+}

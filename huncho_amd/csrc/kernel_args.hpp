@@ -234,6 +234,17 @@ struct ReadoutArgs {
     int* fault;
 };
 
+// Dense projection Y = X W^T with a fused epilogue (gemm.hip).
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2 };
+struct GemmArgs {
+    const void* x;  // [M][K], row stride ldx
+    const void* w;  // [N][K], row stride ldw
+    const void* c;  // EPI_RESIDUAL: [M][N], row stride ldc (may alias y)
+    void* y;        // [M][N] (EPI_SWIGLU: [M][N / 2])
+    long ldx, ldw, ldc, ldy;
+    int M, N, K;
+};
+
 }  // namespace hk
 
 extern "C" {
@@ -254,6 +265,7 @@ int hk_launch_final_norm_head(int dtype, const void* x, long x_tok, const int* c
                               void* h_out, hipStream_t st);
 int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st);
 int hk_launch_readout(int dtype, const hk::ReadoutArgs* a, hipStream_t st);
+int hk_launch_gemm(int dtype16, int epi, const hk::GemmArgs* a, hipStream_t stream);
 int hk_launch_lora_merge(int dtype, void* w, long rows, int cols, const float* a, const float* b, int rank, float scale,
                          hipStream_t st);
 int hk_launch_bidir_attention(int dtype, const hk::BertAttnArgs* a, int n_seqs, int max_len, hipStream_t stream);

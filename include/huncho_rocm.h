@@ -100,6 +100,20 @@ const char* hk_version(void);
 int hk_ctx_set_gemm_autotune(hk_ctx* ctx, int enable);
 int hk_ctx_gemm_plans(hk_ctx* ctx, char* buf, size_t len, size_t* needed);
 
+/* Dense projection on the library's own MFMA kernel (candle Linear, qwen3_5.rs:306-515), 16-bit
+ * dtypes: y [rows][.] = epilogue(x [rows][in] . w [out][in]^T), fp32 accumulation, with
+ *   epilogue 0: y = acc                      (y [rows][out])
+ *   epilogue 1: y = acc + c                  (the residual add of DecoderLayer::forward,
+ *                                             1083-1104; c [rows][out] may alias y)
+ *   epilogue 2: y = silu(g) * u              (Mlp::forward 1020-1031 and gate_cpu::silu_mul 8-47,
+ *                                             g and u rounded to the dtype first as the reference
+ *                                             stores them; w holds blocks of 32 rows [16 gate rows |
+ *                                             the 16 matching up rows], y [rows][out / 2], output
+ *                                             column 16 b + i from w rows 32 b + i and 32 b + 16 + i)
+ * out must be a multiple of 256 and in of 64; rows and pointers 16-byte aligned. */
+int hk_linear(hk_ctx* ctx, int dtype, int epilogue, const void* x_dev, long ldx, const void* w_dev, long ldw,
+              int rows, int out, int in, const void* c_dev, long ldc, void* y_dev, long ldy);
+
 /* ---- device memory for callers without a HIP binding (the Rust FFI crate): plain
  * hipMalloc / hipFree on the context's device, stream-ordered copies on the context's
  * stream. hk_memcpy_d2h returns after the copy has completed. -------------------------- */

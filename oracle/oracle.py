@@ -379,8 +379,11 @@ _EFFECTIVE = {"input_norm_eff", "post_norm_eff", "q_norm_eff", "k_norm_eff"}
 PREFIX = "model.language_model."
 
 
-def merge_lora(weights: dict, lora: dict, scale: float) -> dict:
-    """qwen3_5.rs:1597-1640 + canonical_weight_name (2496-2512): W += scale * (B @ A), fp32."""
+def merge_lora(weights: dict, lora: dict, scale: float, bf16: bool = False) -> dict:
+    """qwen3_5.rs:1597-1640 + canonical_weight_name (2496-2512): W += scale * (B @ A), the delta in
+    fp32. With bf16=True the base weights are bf16 values first (load_base_tensor_files casts
+    every tensor to the model dtype, 2467-2470, before the merge at 2283) and the merged sum is
+    rounded to bf16 again (`.to_dtype(dtype)`, 1631)."""
     out = dict(weights)
     targets = sorted({k[len("base_model.model."):-len(".lora_A.weight")] for k in lora
                       if k.startswith("base_model.model.") and k.endswith(".lora_A.weight")})
@@ -391,7 +394,9 @@ def merge_lora(weights: dict, lora: dict, scale: float) -> dict:
         if not name.startswith(PREFIX):
             name = PREFIX + (name[len("model."):] if name.startswith("model.") else name)
         delta = (b @ a).astype(np.float32) * np.float32(scale)
-        out[name] = (f32(out[name]) + delta).astype(np.float32)
+        base = round_bf16(out[name]) if bf16 else f32(out[name])
+        merged = (base + delta).astype(np.float32)
+        out[name] = round_bf16(merged) if bf16 else merged
     return out
 
 

@@ -1,0 +1,86 @@
+"""The library's MFMA GEMM (hk_linear) against a float64 product of the same bf16 / fp16 values.
+
+Gates: every output within 1 unit in the last place of the dtype (at most 2^-7 relative for bf16,
+which has 8 significant bits, and 2^-10 for fp16) of the exact result rounded once (the fp32
+accumulation order differs); the SwiGLU epilogue against silu(round(g)) * round(u) from the
+float64 products, within 2 ulp."""
+import numpy as np
+import pytest
+import torch
+
+from huncho_amd import abi
+
+pytestmark = pytest.mark.gpu
+
+EPS = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from huncho_amd.ops import context_for_torch
+
+    c = context_for_torch(0)
+    yield c
+    c.close()
+
+
+def linear(ctx, x, w, epi=0, c=None, out_cols=None):
+    rows, k = x.shape
+    n = w.shape[0]
+    y = torch.empty((rows, out_cols or n), dtype=x.dtype, device=x.device)
+    dt = abi.HK_BF16 if x.dtype == torch.bfloat16 else abi.HK_F16
+    ctx.check(abi.lib().hk_linear(ctx.h, dt, epi, x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), rows, n, k,
+                                  c.data_ptr() if c is not None else None, c.stride(0) if c is not None else 0,
+                                  y.data_ptr(), y.stride(0)))
+    torch.cuda.synchronize()
+    return y
+
+
+def within_ulp(got, want, dtype, ulps, k=64):
+    """ulps units in the last place of `want`, plus the fp32 accumulation's absolute error over k
+    products (where a residual cancels the product, that error dominates a tiny result)."""
+    g, w = got.double(), want.double()
+    return bool(((g - w).abs() <= w.abs() * EPS[dtype] * ulps + 4e-7 * k).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,n,k", [(300, 256, 64), (1000, 512, 1024), (4096, 1024, 2048)])
+def test_store_and_residual(ctx, dtype, rows, n, k):
+    g = torch.Generator(device="cuda").manual_seed(rows + n + k)
+    x = (torch.randn((rows, k), generator=g, device="cuda") * 0.5).to(dtype)
+    w = (torch.randn((n, k), generator=g, device="cuda") * 0.05).to(dtype)
+    ref = x.double() @ w.double().T
+    y = linear(ctx, x, w)
+    assert within_ulp(y, ref.to(dtype), dtype, 1, k), float((y.double() - ref).abs().max())
+    r = torch.randn((rows, n), generator=g, device="cuda").to(dtype)
+    y2 = linear(ctx, x, w, epi=1, c=r)
+    assert within_ulp(y2, (ref + r.double()).to(dtype), dtype, 1, k)
+    # in place on the residual stream (c aliases y)
+    r2 = r.clone()
+    ctx.check(abi.lib().hk_linear(ctx.h, abi.HK_BF16 if dtype == torch.bfloat16 else abi.HK_F16, 1, x.data_ptr(),
+                                  k, w.data_ptr(), k, rows, n, k, r2.data_ptr(), n, r2.data_ptr(), n))
+    torch.cuda.synchronize()
+    assert torch.equal(r2, y2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_swiglu_epilogue(ctx, dtype):
+    rows, inter, k = 777, 384, 256
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = (torch.randn((rows, k), generator=g, device="cuda") * 0.5).to(dtype)
+    wg = (torch.randn((inter, k), generator=g, device="cuda") * 0.1).to(dtype)
+    wu = (torch.randn((inter, k), generator=g, device="cuda") * 0.1).to(dtype)
+    # blocks of 32 rows: [16 gate rows | the 16 matching up rows]
+    wf = torch.stack([wg.view(-1, 16, k), wu.view(-1, 16, k)], dim=1).reshape(2 * inter, k).contiguous()
+    y = linear(ctx, x, wf, epi=2, out_cols=inter)
+    gv = (x.double() @ wg.double().T).to(dtype).float()
+    uv = (x.double() @ wu.double().T).to(dtype).float()
+    ref = (gv / (1 + torch.exp(-gv)) * uv).to(dtype)
+    assert within_ulp(y, ref, dtype, 2, k), float((y.float() - ref.float()).abs().max())
+
+
+def test_rejects_unsupported_shapes(ctx):
+    x = torch.zeros((64, 64), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((100, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(abi.HkError):
+        linear(ctx, x, w)
