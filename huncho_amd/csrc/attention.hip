@@ -62,12 +62,14 @@ constexpr size_t ATTN16_LDS = 4 * TILE_ELEMS * 2;  // K and V, double-buffered: 
 constexpr float RESCALE_LOG2 = 8.0f;  // exponents may run up to 2^8 above the row max in use
 
 // The 16-byte chunk c of key row r sits at chunk c ^ swz(r) in a V tile and c ^ swzk(r) in a
-// K tile. The V swizzle depends only on row bits 0, 1 and 4, so the transposing V reads of P.V
-// can add key offsets of 4, 8 and 32 rows to one per-lane address. The K swizzle serves the
+// K tile. The V swizzle depends only on row bits 0 and 1, so the transposing V reads of P.V can
+// add key offsets of 4, 8 and 32 rows to one per-lane address; with XOR masks 0, 4, 8, 12 the 32
+// lanes of each half of a ds_read_b64_tr_b16 (256 bytes) cover all 64 banks once (the earlier
+// mask 2 (r & 3) + 8 bit4(r) left every half 2-way conflicted). The K swizzle serves the
 // permuted-row reads of S^T = K Q^T: a 16-lane group reads rows {0-7, 16-23} (or {8-15, 24-31})
 // at one logical chunk, and swzk maps those rows to 16 distinct chunks, one 16-byte slot each
-// of the 256-byte bank row (the V swizzle gives only 8 distinct, even, chunks there).
-__device__ __forceinline__ int swz(int r) { return 2 * (r & 3) + 8 * ((r >> 4) & 1); }
+// of the 256-byte bank row.
+__device__ __forceinline__ int swz(int r) { return 4 * (r & 3); }
 __device__ __forceinline__ int swzk(int r) { return (r & 7) | (((r >> 4) & 1) << 3); }
 __device__ __forceinline__ int lds_off_k(int r, int c) { return r * KV_ROW + 8 * (c ^ swzk(r)); }
 
