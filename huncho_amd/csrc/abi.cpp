@@ -458,10 +458,11 @@ extern "C" int hk_paged_prefill_attention(hk_ctx* ctx, int dtype, const void* q,
     return rc ? hk_fail(ctx, rc, "attention launch failed") : HK_OK;
 }
 
-extern "C" int hk_gated_delta_chunked(hk_ctx* ctx, int dtype, const void* q, long q_tok, const void* k, long k_tok,
-                                      const void* v, long v_tok, const float* g, const float* beta, const int32_t* cu,
-                                      int n_seqs, int n_tokens, int heads, int k_heads, int dk, int dv,
-                                      const float* initial_state, float* final_state, void* o, long o_tok) {
+int hk_gated_delta_chunked_rows(hk_ctx* ctx, int dtype, const void* q, long q_tok, const void* k, long k_tok,
+                                const void* v, long v_tok, const float* g, const float* beta, const int32_t* cu,
+                                int n_seqs, int n_tokens, int heads, int k_heads, int dk, int dv,
+                                const float* initial_state, float* final_state, void* o, long o_tok,
+                                const float* const* init_rows, float* const* final_rows) {
     if (!ctx) return HK_ERR_INVALID;
     if (int rc = check_dtype(ctx, dtype)) return rc;
     if (dk != 128 || dv != 128) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dk=%d dv=%d: only 128x128 is implemented", dk, dv);
@@ -478,15 +479,24 @@ extern "C" int hk_gated_delta_chunked(hk_ctx* ctx, int dtype, const void* q, lon
     }
     hipSetDevice(ctx->device);
     hk::GdnArgs a{q, k, v, q_tok, k_tok, v_tok, heads / k_heads, g, beta, (long)heads, cu, initial_state,
-                  final_state, o, o_tok, heads, n_tokens, ctx->fault_dev};
+                  final_state, o, o_tok, heads, n_tokens, ctx->fault_dev, init_rows, final_rows};
     int rc = hk_launch_gated_delta_chunked(dtype, &a, n_seqs, ctx->stream);
     return rc ? hk_fail(ctx, rc, "gated delta launch failed") : HK_OK;
 }
 
-extern "C" int hk_gdn_prep(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
-                           const void* conv_hist, const void* ba, long ba_tok, int b_col, int a_col, const float* base_g,
-                           const float* dt_bias, const int32_t* cu, int n_seqs, int n_tokens, int heads, int k_heads,
-                           void* q_out, void* k_out, void* v_out, float* g_out, float* beta_out, void* conv_tail_out) {
+extern "C" int hk_gated_delta_chunked(hk_ctx* ctx, int dtype, const void* q, long q_tok, const void* k, long k_tok,
+                                      const void* v, long v_tok, const float* g, const float* beta, const int32_t* cu,
+                                      int n_seqs, int n_tokens, int heads, int k_heads, int dk, int dv,
+                                      const float* initial_state, float* final_state, void* o, long o_tok) {
+    return hk_gated_delta_chunked_rows(ctx, dtype, q, q_tok, k, k_tok, v, v_tok, g, beta, cu, n_seqs, n_tokens, heads,
+                                       k_heads, dk, dv, initial_state, final_state, o, o_tok, nullptr, nullptr);
+}
+
+int hk_gdn_prep_rows(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
+                     const void* conv_hist, const void* ba, long ba_tok, int b_col, int a_col, const float* base_g,
+                     const float* dt_bias, const int32_t* cu, int n_seqs, int n_tokens, int heads, int k_heads,
+                     void* q_out, void* k_out, void* v_out, float* g_out, float* beta_out, void* conv_tail_out,
+                     const void* const* hist_rows, void* const* tail_rows) {
     if (!ctx) return HK_ERR_INVALID;
     if (int rc = check_dtype(ctx, dtype)) return rc;
     REQUIRE(heads > 0 && k_heads > 0 && heads % k_heads == 0, "heads %d not a multiple of k_heads %d", heads, k_heads);
@@ -500,9 +510,18 @@ extern "C" int hk_gdn_prep(hk_ctx* ctx, int dtype, const void* mixed, long mixed
     hipSetDevice(ctx->device);
     hk::PrepArgs a{mixed, mixed_tok, conv_w, conv_k, conv_hist, ba, ba_tok, b_col, a_col, base_g, dt_bias, cu, n_seqs,
                    n_tokens, k_heads, heads, 1.0f / sqrtf(128.0f), q_out, k_out, v_out, g_out, beta_out,
-                   ctx->fault_dev};
+                   ctx->fault_dev, hist_rows, tail_rows};
     int rc = hk_launch_gdn_prep(dtype, &a, conv_tail_out, ctx->stream);
     return rc ? hk_fail(ctx, rc, "gdn_prep launch failed") : HK_OK;
+}
+
+extern "C" int hk_gdn_prep(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
+                           const void* conv_hist, const void* ba, long ba_tok, int b_col, int a_col, const float* base_g,
+                           const float* dt_bias, const int32_t* cu, int n_seqs, int n_tokens, int heads, int k_heads,
+                           void* q_out, void* k_out, void* v_out, float* g_out, float* beta_out, void* conv_tail_out) {
+    return hk_gdn_prep_rows(ctx, dtype, mixed, mixed_tok, conv_w, conv_k, conv_hist, ba, ba_tok, b_col, a_col, base_g,
+                            dt_bias, cu, n_seqs, n_tokens, heads, k_heads, q_out, k_out, v_out, g_out, beta_out,
+                            conv_tail_out, nullptr, nullptr);
 }
 
 extern "C" int hk_rms_norm(hk_ctx* ctx, int dtype, const void* x, long x_tok, const float* w, float eps, int rows,

@@ -155,14 +155,19 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_f32(GdnArgs a) {
     const float* kg = (const float*)a.k + (long)kh * DK;
     const float* vg = (const float*)a.v + (long)h * DV;
     float* og = (float*)a.o + (long)h * DV;
-    const long sbase = ((long)seq * H + h) * DK * DV;
+    // this sequence's state rows [H][dk][dv] (per-row pointer tables or contiguous arrays)
+    const float* const s0 = a.init_rows ? a.init_rows[seq]
+                                        : (a.initial_state ? a.initial_state + (long)seq * H * DK * DV : nullptr);
+    float* const s1 = a.final_rows ? a.final_rows[seq]
+                                   : (a.final_state ? a.final_state + (long)seq * H * DK * DV : nullptr);
+    const long sbase = (long)h * DK * DV;
 
     f32x16 S[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-            S[rb][j] = a.initial_state ? a.initial_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] : 0.0f;
+            S[rb][j] = s0 ? s0[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] : 0.0f;
 
     for (int c0 = 0; c0 < T; c0 += CH) {
         const int Lc = min(CH, T - c0);
@@ -308,11 +313,11 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_f32(GdnArgs a) {
                     S[rb] = mfma_f32(Kc[(tb * 32 + acc_row(j, g)) * F_KSTR + rb * 32 + col], dl[tb][j], S[rb]);
         }
     }
-    if (a.final_state) {
+    if (s1) {
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a.final_state[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] = S[rb][j];
+            for (int j = 0; j < 16; ++j) s1[sbase + (long)(rb * 32 + acc_row(j, g)) * DV + dvc] = S[rb][j];
     }
 }
 

@@ -122,6 +122,10 @@ struct PrepArgs {
     float* g_out;
     float* beta_out;
     int* fault;
+    // per-sequence conv rows [conv_dim][K-1] (replace hist / the tail output when set; a null
+    // entry is a zero history / no tail)
+    const void* const* hist_rows;
+    void* const* tail_rows;
 };
 
 struct NormArgs {

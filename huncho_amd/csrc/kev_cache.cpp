@@ -69,8 +69,7 @@ extern "C" int hk_kev_cache_create(hk_kev_model* m, int max_pages, int max_handl
     if (!m || !out) return HK_ERR_INVALID;
     hk_ctx* ctx = m->ctx;
     const hk_kev_config& cfg = m->cfg;
-    if (m->dtype == HK_F32 || cfg.conv_k != 4)
-        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "the prefix cache needs a 16-bit model with conv kernel 4");
+    if (cfg.conv_k != 4) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "the prefix cache needs conv kernel 4");
     if (max_pages <= 0 || max_handles <= 0 || max_handles > 4096)
         return hk_fail(ctx, HK_ERR_INVALID, "max_pages %d / max_handles %d out of range", max_pages, max_handles);
     hk_kev_cache* c = new hk_kev_cache();

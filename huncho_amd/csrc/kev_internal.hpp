@@ -64,6 +64,16 @@ int kev_validate_readout(hk_kev_model* m, const int32_t* cu_host, int n_seqs, co
 size_t kev_workspace_bytes(const hk_kev_model* m, int n, int n_seqs, int num_pages);
 
 // The fused Gated DeltaNet layer with optional per-sequence row tables (abi.cpp).
+int hk_gated_delta_chunked_rows(hk_ctx* ctx, int dtype, const void* q, long q_tok, const void* k, long k_tok,
+                                const void* v, long v_tok, const float* g, const float* beta, const int32_t* cu,
+                                int n_seqs, int n_tokens, int heads, int k_heads, int dk, int dv,
+                                const float* initial_state, float* final_state, void* o, long o_tok,
+                                const float* const* init_rows, float* const* final_rows);
+int hk_gdn_prep_rows(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
+                     const void* conv_hist, const void* ba, long ba_tok, int b_col, int a_col, const float* base_g,
+                     const float* dt_bias, const int32_t* cu, int n_seqs, int n_tokens, int heads, int k_heads,
+                     void* q_out, void* k_out, void* v_out, float* g_out, float* beta_out, void* conv_tail_out,
+                     const void* const* hist_rows, void* const* tail_rows);
 int hk_gdn_fused_rows(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok, const float* conv_w, int conv_k,
                       const void* conv_hist, void* conv_tail_out, const void* ba, long ba_tok, int b_col, int a_col,
                       const float* base_g, const float* dt_bias, const void* z, long z_tok, const float* norm_w,

@@ -388,8 +388,7 @@ int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
 
     const int32_t* ctx_lens = view ? view->ctx_lens_dev : b.ctx_lens;
     if (view) {
-        if (dt == HK_F32 || c.conv_k != 4 || m->gdn_rows % 8 != 0)
-            return hk_fail(ctx, HK_ERR_UNSUPPORTED, "cached continuation needs the fused 16-bit Gated DeltaNet path");
+        if (c.conv_k != 4) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "cached continuation needs conv kernel 4");
         int n_attn = 0, n_gdn = 0;
         for (int l = 0; l < c.n_layers; ++l) (m->layers[l].type == 0 ? n_gdn : n_attn)++;
         if ((int)view->k_pools.size() != n_attn || (int)view->v_pools.size() != n_attn ||
@@ -419,11 +418,14 @@ int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
                                       view ? view->init_rows[gi] : nullptr, view ? view->final_rows[gi] : nullptr,
                                       view ? view->hist_rows[gi] : nullptr, view ? view->tail_rows[gi] : nullptr));
             } else {
-                RUN(hk_gdn_prep(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, b.ba, m->ba_rows, b_col, a_col, L.base_g,
-                                L.dt_bias, cu_dev, n_seqs, n, Hv, Hk, b.q, b.k, b.v, b.g, b.beta, nullptr));
-                RUN(hk_gated_delta_chunked(ctx, dt, b.q, (long)Hk * 128, b.k, (long)Hk * 128, b.v, (long)Hv * 128,
-                                           b.g, b.beta, cu_dev, n_seqs, n, Hv, Hk, 128, 128, nullptr, nullptr, b.o,
-                                           (long)Hv * 128));
+                // the cache's per-sequence conv tails and states, as in the fused path
+                RUN(hk_gdn_prep_rows(ctx, dt, b.big, rows, L.conv_w, c.conv_k, nullptr, b.ba, m->ba_rows, b_col, a_col,
+                                     L.base_g, L.dt_bias, cu_dev, n_seqs, n, Hv, Hk, b.q, b.k, b.v, b.g, b.beta, nullptr,
+                                     view ? view->hist_rows[gi] : nullptr, view ? view->tail_rows[gi] : nullptr));
+                RUN(hk_gated_delta_chunked_rows(ctx, dt, b.q, (long)Hk * 128, b.k, (long)Hk * 128, b.v, (long)Hv * 128,
+                                                b.g, b.beta, cu_dev, n_seqs, n, Hv, Hk, 128, 128, nullptr, nullptr, b.o,
+                                                (long)Hv * 128, view ? view->init_rows[gi] : nullptr,
+                                                view ? view->final_rows[gi] : nullptr));
                 RUN(hk_gated_rms_norm(ctx, dt, b.o, (char*)b.big + (size_t)m->conv_dim * e, rows, Hv, L.norm_w, c.eps,
                                       n * Hv, 128, b.o));
             }

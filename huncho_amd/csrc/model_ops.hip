@@ -46,6 +46,14 @@ __device__ __forceinline__ int seq_of(const int* cu, int n, int t) {
 
 constexpr int HW = 128;  // head width of the GDN heads
 
+// Conv history [conv_dim][K-1] of sequence s: its row of the per-sequence table, or its slice
+// of the contiguous history, or null (zero history)
+template <typename T>
+__device__ __forceinline__ const T* hist_of(const PrepArgs& a, int s, int conv_dim) {
+    if (a.hist_rows) return (const T*)a.hist_rows[s];
+    return a.hist ? (const T*)a.hist + (long)s * conv_dim * (a.K - 1) : nullptr;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
     const int t = blockIdx.x;
@@ -60,6 +68,7 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
     const int conv_dim = 2 * key_dim + a.Hv * HW;
     const int rows = 2 * a.Hk + a.Hv;
     const int K = a.K;
+    const T* hist = hist_of<T>(a, s, conv_dim);
     for (int r = wave; r < rows; r += 4) {
         float x[2];
 #pragma unroll
@@ -71,8 +80,8 @@ __global__ __launch_bounds__(256) void gdn_prep(PrepArgs a) {
                 float xv;
                 if (tt >= start) {
                     xv = to_f(((const T*)a.mixed)[(long)tt * a.mixed_tok + c]);
-                } else if (a.hist) {
-                    xv = to_f(((const T*)a.hist)[((long)s * conv_dim + c) * (K - 1) + (tt - start + K - 1)]);
+                } else if (hist) {
+                    xv = to_f(hist[(long)c * (K - 1) + (tt - start + K - 1)]);
                 } else {
                     continue;
                 }
@@ -149,10 +158,12 @@ __global__ __launch_bounds__(256) void gdn_prep_vec4(PrepArgs a) {
             v8 x = *(const v8*)((const T*)a.mixed + (long)tt * a.mixed_tok + c0);
 #pragma unroll
             for (int e = 0; e < 8; ++e) dst[e] = to_f(x[e]);
-        } else if (a.hist && tt >= st - 3) {
+        } else if (tt >= st - 3) {
+            const T* hist = hist_of<T>(a, sq, conv_dim);
+            if (hist) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                dst[e] = to_f(((const T*)a.hist)[((long)sq * conv_dim + c0 + e) * 3 + (tt - st + 3)]);
+                for (int e = 0; e < 8; ++e) dst[e] = to_f(hist[(long)(c0 + e) * 3 + (tt - st + 3)]);
+            }
         }
     };
     float win[3][8];
@@ -224,18 +235,18 @@ __global__ void conv_tail(PrepArgs a, void* tail_out, int conv_dim) {
     if (c >= conv_dim) return;
     const int start = a.cu_seqlens[s], len = a.cu_seqlens[s + 1] - start, K = a.K;
     if (start < 0 || len < 0 || start + len > a.n_tokens) return;
+    T* const dst = a.tail_rows ? (T*)a.tail_rows[s] : (T*)tail_out + (long)s * conv_dim * (K - 1);
+    if (!dst) return;
+    // a missing history is K-1 zeros in front of x
+    const T* const hist = hist_of<T>(a, s, conv_dim);
     for (int i = 0; i < K - 1; ++i) {
-        const int idx = len + (a.hist ? K - 1 : 0) - (K - 1) + i;  // index in [history, x]
+        const int idx = len + i;  // index in [history (K-1), x]
         T v = from_f<T>(0.0f);
-        if (idx >= 0) {
-            if (a.hist) {
-                v = idx < K - 1 ? ((const T*)a.hist)[((long)s * conv_dim + c) * (K - 1) + idx]
-                                : ((const T*)a.mixed)[(long)(start + idx - (K - 1)) * a.mixed_tok + c];
-            } else {
-                v = ((const T*)a.mixed)[(long)(start + idx) * a.mixed_tok + c];
-            }
-        }
-        ((T*)tail_out)[((long)s * conv_dim + c) * (K - 1) + i] = v;
+        if (idx >= K - 1)
+            v = ((const T*)a.mixed)[(long)(start + idx - (K - 1)) * a.mixed_tok + c];
+        else if (hist)
+            v = hist[(long)c * (K - 1) + idx];
+        dst[(long)c * (K - 1) + i] = v;
     }
 }
 
@@ -433,7 +444,7 @@ extern "C" int hk_launch_gdn_prep(int dtype, const PrepArgs* a, void* tail_out, 
     } else if (a->n_tokens > 0) {
         HK_DISPATCH3(gdn_prep, dim3(a->n_tokens), dim3(256), *a);
     }
-    if (tail_out) {
+    if (tail_out || a->tail_rows) {
         dim3 grid((conv_dim_v + 255) / 256, a->n_seqs);
         HK_DISPATCH3(conv_tail, grid, dim3(256), *a, tail_out, conv_dim_v);
     }

@@ -315,7 +315,8 @@ int hk_kev_forward_readout(hk_kev_model* m, const int32_t* ids_dev, const int32_
  * copy-on-write tails as qwen3_5/kv_pages.rs:18-98, 307-341). A handle holds its tokens' K/V in
  * pages of a pool shared by all handles (reference counted), plus the recurrent state and conv
  * tail of every Gated DeltaNet layer. Handles are process-unique, never reused (lib.rs:64-76).
- * 16-bit models only. Calls on one cache are not thread-safe (the engine serialises them). --- */
+ * Models of every activation dtype with conv kernel 4. Calls on one cache are not thread-safe
+ * (the engine serialises them). --- */
 typedef struct hk_kev_cache hk_kev_cache;
 /* Pools of max_pages pages (page_size tokens of every KV head of every attention layer) and at
  * most max_handles live handles (the reference: 64). */

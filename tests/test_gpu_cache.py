@@ -12,6 +12,8 @@ a parent is unchanged by its branches, kv_pages.rs:307-341 copy-on-write tails):
 fp16 activations: calibrated probabilities within 1e-3 of the fp32 oracle's full-sequence
 forward (the qualification gate, conformance.rs:20-48), and continued vs fresh on the GPU
 within 2e-3 (different chunk partitions of the same recurrence round differently in fp16).
+fp32 activations: continued and forked rows within 2e-5 of the oracle and of a fresh forward.
+(The bf16 cache at the Kev shape itself is in test_gpu_workloads.py.)
 """
 import numpy as np
 import pytest
@@ -188,4 +190,46 @@ def test_failures_commit_nothing(setup):
     with pytest.raises(abi.HkError):
         cache.release(h)
     assert cache.stats() == (0, 4)
+    cache.close()
+
+
+# ---------------------------------------------------------------------------
+# fp32 activations: the unfused Gated DeltaNet path (gdn_prep + gdn_chunk_f32) with the
+# cache's per-sequence state and conv-tail rows
+# ---------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def model32(setup):
+    shape = KevShape(**SHAPE)
+    m = KevModel(setup["ctx"], shape, synthetic_weights(shape, SEED, std=0.05), torch.float32)
+    yield m
+    m.close()
+
+
+def test_fp32_continuation_and_fork(setup, model32):
+    """fp32: prefill + continuation at splits on and off page/chunk boundaries, and a parent
+    with a fork continuing together from a shared partial tail page, each within the fp32
+    probability gate (2e-5, crates/huncho-backend/tests/kev_reference.rs:79) of the oracle's
+    full-sequence forward and of a fresh fp32 forward."""
+    cache = KevCache(model32, max_pages=64)
+    full = toks(80, 150)
+    hs = [cache.prefill(full[:cut]) for cut in (17, 64, 100)]
+    _, p_cont, _ = cache.continue_rows(hs, [full[cut:] for cut in (17, 64, 100)], TEMP)
+    p_ref = setup["oracle_probs"](full)
+    p_fresh = fresh_probs(model32, [full])[0]
+    d_ref, d_fresh = float(np.abs(p_cont - p_ref).max()), float(np.abs(p_cont - p_fresh).max())
+    print(f"fp32 continuation: vs fp32 oracle {d_ref:.2e}, vs fresh {d_fresh:.2e}")
+    assert d_ref < 2e-5 and d_fresh < 2e-5, (d_ref, d_fresh)
+    for h in hs:
+        cache.release(h)
+    prefix, s1, s2 = toks(81, 21), toks(82, 9), toks(83, 40)
+    parent = cache.prefill(prefix)
+    child = cache.fork(parent)
+    _, p, _ = cache.continue_rows([parent, child], [s1, s2], TEMP)
+    for row, whole in zip(p, (prefix + s1, prefix + s2)):
+        d = float(np.abs(row - setup["oracle_probs"](whole)).max())
+        assert d < 2e-5, d
+    cache.release(parent)
+    cache.release(child)
+    assert cache.stats() == (0, 64)
     cache.close()

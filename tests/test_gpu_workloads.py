@@ -234,3 +234,43 @@ def test_bidir_attention_4096(ctx, half_window):
     e = rel_err(out.float().cpu().numpy(), ref)
     print(f"bidirectional attention L={L}, half window {half_window}: {e:.2e} relative")
     assert e < 2e-2, e
+
+
+# ---------------------------------------------------------------------------
+# the device prefix cache at the Kev shape in bf16
+# ---------------------------------------------------------------------------
+
+CACHE_ROWS = [(0, 200), (27, 17), (45, 320), (63, 448)]  # (bench row, cached prefix length)
+
+
+def test_kev_cache_continuation_bf16(ctx, kev_bench_case):
+    """Four bench rows prefilled to different lengths (on and off page and chunk boundaries) and
+    continued together to 512 tokens through hk_kev_forward_cached: the same bf16 gate against
+    the fp32 oracle as the whole-batch forward (no farther than the oracle's own bf16 flow), and
+    within that spread of a fresh forward of the same rows (the two split the recurrence into
+    different chunks, which round differently in bf16)."""
+    from huncho_amd.kev import KevCache, KevModel
+
+    case = kev_bench_case
+    model = KevModel(ctx, case["shape"], case["weights"], torch.bfloat16)
+    cache = KevCache(model, max_pages=4 * 512 // 16 + 8)
+    rows = [case["ids"][r * 512:(r + 1) * 512].tolist() for r, _ in CACHE_ROWS]
+    hs = [cache.prefill(row[:cut]) for row, (_, cut) in zip(rows, CACHE_ROWS)]
+    _, p_cont, _ = cache.continue_rows(hs, [row[cut:] for row, (_, cut) in zip(rows, CACHE_ROWS)], 1.3)
+    assert [cache.tokens(h) for h in hs] == [512] * 4
+    _, p_fresh = model.forward_batch(rows, temperature=1.3)
+    assert ctx.take_faults() == 0
+    for h in hs:
+        cache.release(h)
+    assert cache.stats() == (0, 4 * 512 // 16 + 8)
+    cache.close()
+    model.close()
+    pick = [KEV_ROWS.index(r) for r, _ in CACHE_ROWS]
+    p32 = case["ref"]["f32"][1][pick]
+    p16 = case["ref"]["bf16"][1][pick]
+    spread = float(np.abs(p16 - p32).max())
+    d32 = float(np.abs(p_cont - p32).max())
+    d_fresh = float(np.abs(p_cont - p_fresh).max())
+    print(f"Kev cache bf16, rows {CACHE_ROWS}: continued vs fp32 oracle {d32:.2e}, vs fresh {d_fresh:.2e} "
+          f"(oracle bf16 vs fp32 {spread:.2e})")
+    assert d32 <= spread and d_fresh <= spread, (d32, d_fresh, spread)
