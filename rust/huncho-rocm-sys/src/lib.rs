@@ -171,6 +171,11 @@ extern "C" {
     pub fn hk_ctx_gemm_plans(
         ctx: *mut hk_ctx, buf: *mut c_char, len: usize, needed: *mut usize
     ) -> c_int;
+    pub fn hk_linear(
+        ctx: *mut hk_ctx, dtype: c_int, epilogue: c_int, x_dev: *const c_void, ldx: c_long,
+        w_dev: *const c_void, ldw: c_long, rows: c_int, out: c_int, in_: c_int, c_dev: *const c_void,
+        ldc: c_long, y_dev: *mut c_void, ldy: c_long,
+    ) -> c_int;
     pub fn hk_buffer_alloc(ctx: *mut hk_ctx, bytes: usize, dev_out: *mut *mut c_void) -> c_int;
     pub fn hk_buffer_free(ctx: *mut hk_ctx, dev: *mut c_void) -> c_int;
     pub fn hk_memcpy_h2d(
