@@ -573,6 +573,13 @@ int hk_gdn_fused_rows(hk_ctx* ctx, int dtype, const void* mixed, long mixed_tok,
     REQUIRE(heads > 0 && k_heads > 0 && heads % k_heads == 0, "heads %d not a multiple of k_heads %d", heads, k_heads);
     REQUIRE(n_seqs > 0 && n_seqs <= 65535 && n_tokens >= 0, "bad batch geometry");
     REQUIRE(mixed && conv_w && ba && base_g && dt_bias && z && norm_w && cu && out, "null pointer argument");
+    {  // the kernel addresses a sequence's rows with 32-bit byte offsets (24-bit row strides)
+        const long esz = dtype == HK_F32 ? 4 : 2, lim = 1L << 32;
+        REQUIRE(n_tokens < (1 << 24) && mixed_tok * esz < (1 << 24) && z_tok * esz < (1 << 24) &&
+                    out_tok * esz < (1 << 24) && n_tokens * mixed_tok * esz < lim && n_tokens * z_tok * esz < lim &&
+                    n_tokens * out_tok * esz < lim,
+                "fused Gated DeltaNet layer: token rows or the batch too large for 32-bit row offsets");
+    }
     REQUIRE(((uintptr_t)conv_w & 15) == 0, "conv weights must be 16-byte aligned");
     const long conv_dim = (2L * k_heads + heads) * 128;
     REQUIRE(mixed_tok >= conv_dim && mixed_tok % 8 == 0 && ((uintptr_t)mixed & 15) == 0,

@@ -71,6 +71,37 @@ template <> struct M16<f16> {
 template <typename T> __device__ __forceinline__ float f(T x) { return (float)x; }
 template <typename T> __device__ __forceinline__ float rnd(float x) { return (float)(T)x; }
 
+// a.x b.x + a.y b.y as one VOP3P instruction with an inline zero accumulator (the builtin's
+// accumulating VOP2 form first copies the zero into its destination register)
+__device__ __forceinline__ float dot2_0(bf16x2 a, bf16x2 b) {
+    float d;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+__device__ __forceinline__ float dot2_0(f16x2 a, f16x2 b) {
+    float d;
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+// The two halves of a packed 16-bit pair in fp32 (bf16: a shift and a mask). The empty asm
+// hides the pair's origin, or the compiler rebuilds each half from its own single conversion.
+__device__ __forceinline__ unsigned opaque(bf16x2 p) {
+    unsigned u = __builtin_bit_cast(unsigned, p);
+    asm("" : "+v"(u));
+    return u;
+}
+__device__ __forceinline__ float lo_f(bf16x2 p) { return __builtin_bit_cast(float, opaque(p) << 16); }
+__device__ __forceinline__ float hi_f(bf16x2 p) { return __builtin_bit_cast(float, opaque(p) & 0xffff0000u); }
+__device__ __forceinline__ float lo_f(f16x2 p) { return (float)p[0]; }
+__device__ __forceinline__ float hi_f(f16x2 p) { return (float)p[1]; }
+// (a, b) rounded to T (one packed conversion), then held as an fp16 pair: the fp16 MFMA operand
+// of two values stored in the activation dtype (bf16 values in range are exact in fp16)
+__device__ __forceinline__ f16x2 to_ct(bf16x2 p) { return f16x2{(f16)lo_f(p), (f16)hi_f(p)}; }
+__device__ __forceinline__ f16x2 to_ct(f16x2 p) { return p; }
+template <typename T> __device__ __forceinline__ f16x2 rnd_ct(float a, float b) {
+    return to_ct(typename M16<T>::v2{(T)a, (T)b});
+}
+
 constexpr int CH = 64, DK = 128, DV = 128, NTHREADS = 256;
 constexpr int RS = DK + 8;  // row stride (elements) of the Q / K / V tiles [64][136]
 constexpr int AS = CH + 4;  // fp32 row stride of A / T [64][68]
@@ -164,8 +195,10 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
     // MFMA operands and LDS tiles are fp16 (CT) for both activation dtypes: bf16 activations
     // are exact in fp16 (inside its range), and every intermediate rounded to an operand (R, A,
     // T, delta, the state S, Aqk) keeps 11 significant bits instead of bf16's 8. The reference
-    // runs this recurrence in fp32 (delta_cpu.rs:95-131); its bf16 storage points (conv output,
-    // normalised q and k, beta, the recurrence output) are rounded to T as before.
+    // runs this recurrence in fp32 (delta_cpu.rs:95-131); its activation-dtype storage points
+    // (the conv output, beta, the recurrence output) are rounded to T, and the normalised q and
+    // k, which it keeps in fp32, only to the fp16 operand (fused mode; standalone mode takes q
+    // and k in T).
     typedef f16 CT;
     typedef typename M16<CT>::v8 v8;
     typedef typename M16<CT>::v4 v4;
@@ -248,15 +281,25 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
             };
             // all three windows are loaded before the first conv, so the chunk waits for one
             // memory round trip
+            // Addresses: a wave-uniform base per tensor (this sequence's first row, the head's
+            // columns) plus one 32-bit byte offset per row shared by the three tensors (the host
+            // keeps n_tokens * mixed_tok * sizeof(T) below 2^32 and the row stride below 2^24)
             tv8 raw[3][7];
-#pragma unroll
-            for (int tsr = 0; tsr < 3; ++tsr)
+            {
+                const char* const mb = (const char*)fa.mixed + (long)t0 * fa.mixed_tok * (long)sizeof(T);
+                const char* const base[3] = {mb + (long)kh * 128 * sizeof(T),
+                                             mb + ((long)fa.Hk + kh) * 128 * sizeof(T),
+                                             mb + (2L * fa.Hk + h) * 128 * sizeof(T)};
+                const unsigned row_b = (unsigned)(fa.mixed_tok * sizeof(T));
 #pragma unroll
                 for (int i = 0; i < 7; ++i) {
                     const int p = c0 + r0 - 3 + i;
-                    const int pc = p < 0 ? 0 : (p >= Tn ? Tn - 1 : p);
-                    raw[tsr][i] = *(const tv8*)((const T*)fa.mixed + (long)(t0 + pc) * fa.mixed_tok + tcol(tsr));
+                    const unsigned pc = (unsigned)(p < 0 ? 0 : (p >= Tn ? Tn - 1 : p));
+                    const unsigned off = __umul24(pc, row_b) + 16u * j;
+#pragma unroll
+                    for (int tsr = 0; tsr < 3; ++tsr) raw[tsr][i] = *(const tv8*)(base[tsr] + off);
                 }
+            }
             if (c0 + r0 == 0) {  // windows start 3 positions before the sequence
 #pragma unroll
                 for (int tsr = 0; tsr < 3; ++tsr) {
@@ -291,27 +334,30 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float acc = dot2(w23[e], tv2{raw[tsr][i + 2][e], raw[tsr][i + 3][e]},
-                                               dot2(w01[e], tv2{raw[tsr][i][e], raw[tsr][i + 1][e]}, 0.0f));
+                                               dot2_0(w01[e], tv2{raw[tsr][i][e], raw[tsr][i + 1][e]}));
                         y[e] = silu(acc);
                     }
+                    // the conv output is stored in T (qwen3_5.rs:843), held exactly in CT
+                    f16x2 o[4];
                     if (tsr < 2) {  // conv output stored in the activation dtype, then l2norm over
                                     // the head's 128 channels (16 lanes); q also takes the scale
-                        float ss = 0.0f;
+                        tv2 p[4];
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            y[e] = rnd<T>(y[e]);
-                            ss += y[e] * y[e];
-                        }
+                        for (int m = 0; m < 4; ++m) p[m] = tv2{(T)y[2 * m], (T)y[2 * m + 1]};
+                        float ss = dot2_0(p[0], p[0]);
+#pragma unroll
+                        for (int m = 1; m < 4; ++m) ss = dot2(p[m], p[m], ss);
                         ss = sum16(ss);
-                        const float inv = fast_rsqrt(ss + 1e-6f);
+                        const float inv = fast_rsqrt(ss + 1e-6f) * (tsr == 0 ? fa.scale : 1.0f);
+                        // the normalised q and k stay fp32 in the reference (l2norm returns
+                        // fp32, qwen3_5.rs:204-210, 923-924): rounded only to the fp16 operand
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) y[e] = tsr == 0 ? (y[e] * inv) * fa.scale : y[e] * inv;
+                        for (int m = 0; m < 4; ++m) o[m] = f16x2{(f16)(lo_f(p[m]) * inv), (f16)(hi_f(p[m]) * inv)};
+                    } else {
+#pragma unroll
+                        for (int m = 0; m < 4; ++m) o[m] = rnd_ct<T>(y[2 * m], y[2 * m + 1]);
                     }
-                    // stored at the reference's rounding point (T), held exactly in CT
-                    v8 o;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) o[e] = (CT)rnd<T>(y[e]);
-                    *(v8*)(dst + el(r0 + i, 8 * j)) = o;
+                    *(v8*)(dst + el(r0 + i, 8 * j)) = __builtin_bit_cast(v8, o);
                 }
             }
         } else {
@@ -520,10 +566,11 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
         float gz[4][8];
         if (FUSED) {
             tv8 zv[4];
+            const char* const zb = (const char*)fa.z + ((long)t0 * fa.z_tok + (long)h * DV) * (long)sizeof(T);
 #pragma unroll
             for (int pass = 0; pass < 4; ++pass) {
-                const long tt = t0 + c0 + min(pass * 16 + rrow, Lc - 1);
-                zv[pass] = *(const tv8*)((const T*)fa.z + tt * fa.z_tok + (long)h * DV + 8 * rsub);
+                const unsigned tt = (unsigned)(c0 + min(pass * 16 + rrow, Lc - 1));
+                zv[pass] = *(const tv8*)(zb + (__umul24(tt, (unsigned)(fa.z_tok * sizeof(T))) + 16u * rsub));
             }
 #pragma unroll
             for (int pass = 0; pass < 4; ++pass)
@@ -532,6 +579,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
         }
         __syncthreads();
         // ---------------- P4: O -> HBM (gated RMSNorm when fused) ----------------
+        char* const ob = (char*)a.o + ((long)t0 * a.o_tok + (long)h * DV) * (long)sizeof(T);
 #pragma unroll
         for (int pass = 0; pass < 4; ++pass) {
             const int r = pass * 16 + rrow;
@@ -551,7 +599,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
                 tv8 y;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) y[e] = (T)((x[e] * inv) * gz[pass][e]);
-                if (r < Lc) *(tv8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
+                if (r < Lc) *(tv8*)(ob + (__umul24((unsigned)(c0 + r), (unsigned)(a.o_tok * sizeof(T))) + 16u * rsub)) = y;
             } else if (r < Lc) {
                 tv8 y;
                 float ss = 0.0f;
