@@ -68,6 +68,10 @@ class KevReadout(C.Structure):
                 ("positions_dev", vp), ("hidden_dev", vp), ("pointer_scores_dev", vp)]
 
 
+class PrefillWork(C.Structure):
+    _fields_ = [("forward_calls", C.c_uint64), ("processed_tokens", C.c_uint64), ("chunked_prefills", C.c_uint64)]
+
+
 class BertLayerWeights(C.Structure):
     _fields_ = [(n, vp) for n in BERT_LAYER_FIELDS]
 
@@ -125,6 +129,12 @@ SIGNATURES = {
     "hk_kev_cache_tokens": (I, [vp, C.c_uint64, C.POINTER(I)]),
     "hk_kev_cache_stats": (I, [vp, C.POINTER(I), C.POINTER(I)]),
     "hk_kev_cache_workspace_size": (I, [vp, I, I, C.POINTER(SZ)]),
+    "hk_kev_cache_prefill_cached": (I, [vp, i32p, vp, I, SZ, I, vp, SZ, C.POINTER(C.c_uint64), C.POINTER(I),
+                                        C.POINTER(PrefillWork)]),
+    "hk_kev_cache_begin_resumable": (I, [vp, i32p, I, SZ, C.POINTER(C.c_uint64), C.POINTER(I)]),
+    "hk_kev_cache_advance_resumable": (I, [vp, C.c_uint64, vp, I, vp, SZ, C.POINTER(PrefillWork), C.POINTER(I)]),
+    "hk_kev_cache_clear_prefixes": (I, [vp]),
+    "hk_kev_cache_prefix_stats": (I, [vp, C.POINTER(I), C.POINTER(SZ)]),
     "hk_kev_forward_cached": (I, [vp, C.POINTER(C.c_uint64), I, vp, vp, i32p, vp, SZ, vp, vp]),
     "hk_layer_norm": (I, [vp, I, vp, L, vp, F, I, I, vp, L]),
     "hk_bidir_attention": (I, [vp, I, vp, L, vp, L, vp, L, vp, I, I, I, I, I, I, F, vp, L]),

@@ -13,9 +13,18 @@
 //   * a continuation commits only after the whole forward succeeded: new pages are taken
 //     from the free list, the state is written to the handle's second state buffer, and the
 //     token count, page list and active state buffer change only when the call returns OK;
-//   * at most max_handles live handles (the reference allows 64, qwen3_5.rs:3257-3265).
+//   * at most max_handles live handles (the reference allows 64, qwen3_5.rs:3257-3265);
+//   * exact-prefix retention under a charged-byte budget (prefill_cached, qwen3_5.rs:2850-2865,
+//     2975-3031; PrefixSnapshots 1215-1234, FIFO eviction, at most 16 snapshots): a retained
+//     prefix is an immutable snapshot (a private clone: shared pages, its own state) that a
+//     later identical prefix clones instead of recomputing;
+//   * resumable chunked prefill (begin / advance_resumable_prefill, qwen3_5.rs:2867-2934): a
+//     pending handle advances one chunk per call, cannot be forked or continued until it is
+//     complete, and is retained when it completes.
 #include <string.h>
 
+#include <deque>
+#include <map>
 #include <unordered_map>
 #include <vector>
 
@@ -33,6 +42,20 @@ struct KevHandle {
 
 }  // namespace
 
+namespace {
+
+struct Pending {  // a resumable prefill in progress: its whole prefix and retention budget
+    std::vector<int32_t> tokens;
+    size_t max_bytes = 0;
+};
+
+struct Snapshot {  // a retained prefix
+    KevHandle h;
+    size_t bytes = 0;  // charged bytes
+};
+
+}  // namespace
+
 struct hk_kev_cache {
     hk_kev_model* m = nullptr;
     int max_pages = 0, max_handles = 0, P = 0, n_attn = 0, n_gdn = 0, bt_stride = 0;
@@ -43,6 +66,10 @@ struct hk_kev_cache {
     std::vector<int> free_list;
     std::unordered_map<uint64_t, KevHandle> handles;
     uint64_t next_id = 1;
+    std::map<std::vector<int32_t>, Snapshot> prefixes;  // retained exact prefixes
+    std::deque<std::vector<int32_t>> fifo;             // their insertion order
+    size_t prefix_bytes = 0;
+    std::unordered_map<uint64_t, Pending> pending;     // resumable prefills in progress
 };
 
 static void free_handle_buffers(KevHandle& h) {
@@ -107,6 +134,7 @@ extern "C" int hk_kev_cache_destroy(hk_kev_cache* c) {
     hipSetDevice(c->m->ctx->device);
     hipStreamSynchronize(c->m->ctx->stream);
     for (auto& kv : c->handles) free_handle_buffers(kv.second);
+    for (auto& kv : c->prefixes) free_handle_buffers(kv.second.h);
     for (void* p : c->k_pools) hipFree(p);
     for (void* p : c->v_pools) hipFree(p);
     delete c;
@@ -127,17 +155,12 @@ extern "C" int hk_kev_cache_open(hk_kev_cache* c, uint64_t* handle_out) {
     return HK_OK;
 }
 
-extern "C" int hk_kev_cache_fork(hk_kev_cache* c, uint64_t parent, uint64_t* child_out) {
-    if (!c || !child_out) return HK_ERR_INVALID;
+// A private clone of p into h (fresh buffers): p's pages (reference counted), a copy of its
+// committed recurrent state and conv tails.
+static int clone_handle(hk_kev_cache* c, const KevHandle& p, KevHandle& h) {
     hk_ctx* ctx = c->m->ctx;
-    auto it = c->handles.find(parent);
-    if (it == c->handles.end()) return hk_fail(ctx, HK_ERR_INVALID, "unknown cache handle %llu", (unsigned long long)parent);
-    if ((int)c->handles.size() >= c->max_handles)
-        return hk_fail(ctx, HK_ERR_NOMEM, "cache holds its maximum of %d live handles", c->max_handles);
     hipSetDevice(ctx->device);
-    KevHandle h;
     if (int rc = alloc_handle_buffers(c, h)) return rc;
-    const KevHandle& p = it->second;
     h.tokens = p.tokens;
     h.pages = p.pages;
     if (p.tokens > 0) {
@@ -150,6 +173,29 @@ extern "C" int hk_kev_cache_fork(hk_kev_cache* c, uint64_t parent, uint64_t* chi
         }
     }
     for (int pg : h.pages) ++c->refs[pg];
+    return HK_OK;
+}
+
+// Drops h's pages (returned to the pool when no other holder is left) and frees its buffers.
+static void drop_handle(hk_kev_cache* c, KevHandle& h) {
+    hipSetDevice(c->m->ctx->device);
+    hipStreamSynchronize(c->m->ctx->stream);  // queued work may still read the pages or the state
+    for (int pg : h.pages)
+        if (--c->refs[pg] == 0) c->free_list.push_back(pg);
+    h.pages.clear();
+    free_handle_buffers(h);
+}
+
+extern "C" int hk_kev_cache_fork(hk_kev_cache* c, uint64_t parent, uint64_t* child_out) {
+    if (!c || !child_out) return HK_ERR_INVALID;
+    hk_ctx* ctx = c->m->ctx;
+    auto it = c->handles.find(parent);
+    if (it == c->handles.end()) return hk_fail(ctx, HK_ERR_INVALID, "unknown cache handle %llu", (unsigned long long)parent);
+    if (c->pending.count(parent)) return hk_fail(ctx, HK_ERR_INVALID, "a partial prefill cannot be forked");
+    if ((int)c->handles.size() >= c->max_handles)
+        return hk_fail(ctx, HK_ERR_NOMEM, "cache holds its maximum of %d live handles", c->max_handles);
+    KevHandle h;
+    if (int rc = clone_handle(c, it->second, h)) return rc;
     const uint64_t id = c->next_id++;
     c->handles.emplace(id, std::move(h));
     *child_out = id;
@@ -161,12 +207,9 @@ extern "C" int hk_kev_cache_release(hk_kev_cache* c, uint64_t handle) {
     hk_ctx* ctx = c->m->ctx;
     auto it = c->handles.find(handle);
     if (it == c->handles.end()) return hk_fail(ctx, HK_ERR_INVALID, "unknown cache handle %llu", (unsigned long long)handle);
-    hipSetDevice(ctx->device);
-    hipStreamSynchronize(ctx->stream);  // queued work may still read the pages or the state
-    for (int pg : it->second.pages)
-        if (--c->refs[pg] == 0) c->free_list.push_back(pg);
-    free_handle_buffers(it->second);
+    drop_handle(c, it->second);
     c->handles.erase(it);
+    c->pending.erase(handle);
     return HK_OK;
 }
 
@@ -187,12 +230,13 @@ extern "C" int hk_kev_cache_stats(hk_kev_cache* c, int* live_handles, int* free_
 }
 
 // Per-call tables after the model workspace: block tables, context lengths and the Gated
-// DeltaNet row tables (4 per linear layer).
+// DeltaNet row tables (4 per linear layer), then the prefill slot (one row's cu_seqlens for
+// the library's own prefill chunks).
 static size_t table_bytes(const hk_kev_cache* c, int n_seqs) {
     const size_t bt = (size_t)n_seqs * c->bt_stride * sizeof(int32_t);
     const size_t lens = (size_t)n_seqs * sizeof(int32_t);
     const size_t rows = (size_t)c->n_gdn * 4 * n_seqs * sizeof(void*);
-    return ((bt + 255) & ~(size_t)255) + ((lens + 255) & ~(size_t)255) + ((rows + 255) & ~(size_t)255);
+    return ((bt + 255) & ~(size_t)255) + ((lens + 255) & ~(size_t)255) + ((rows + 255) & ~(size_t)255) + 256;
 }
 
 extern "C" int hk_kev_cache_workspace_size(hk_kev_cache* c, int n_tokens, int n_seqs, size_t* bytes_out) {
@@ -203,7 +247,7 @@ extern "C" int hk_kev_cache_workspace_size(hk_kev_cache* c, int n_tokens, int n_
 
 static int forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids,
                           const int32_t* cu_dev, const int32_t* cu_host, void* workspace, size_t workspace_bytes,
-                          float* logits, void* hidden_last, const hk_kev_readout* readout);
+                          float* logits, void* hidden_last, const hk_kev_readout* readout, bool prefill = false);
 
 extern "C" int hk_kev_forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids,
                                      const int32_t* cu_dev, const int32_t* cu_host, void* workspace,
@@ -222,15 +266,17 @@ extern "C" int hk_kev_forward_cached_readout(hk_kev_cache* c, const uint64_t* ha
                           readout);
 }
 
+// prefill: the library's own prefill chunk of a pending (or new) handle; no outputs are read
 static int forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_seqs, const int32_t* ids,
                           const int32_t* cu_dev, const int32_t* cu_host, void* workspace, size_t workspace_bytes,
-                          float* logits, void* hidden_last, const hk_kev_readout* readout) {
+                          float* logits, void* hidden_last, const hk_kev_readout* readout, bool prefill) {
     if (!c) return HK_ERR_INVALID;
     hk_kev_model* m = c->m;
     hk_ctx* ctx = m->ctx;
     const hk_kev_config& cfg = m->cfg;
     if (!handles_host || !ids || !cu_dev || !cu_host || !workspace || n_seqs <= 0 || n_seqs > 64)
         return hk_fail(ctx, HK_ERR_INVALID, "invalid cached forward arguments (1..64 rows)");
+    if (!prefill && cfg.n_out > 0 && !logits && !readout) return hk_fail(ctx, HK_ERR_INVALID, "logits output required");
     if (cu_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "cu_seqlens[0] must be 0");
     // validate every row before any work (qwen3_5.rs:2656-2725)
     std::vector<KevHandle*> hs(n_seqs);
@@ -240,6 +286,9 @@ static int forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_s
             return hk_fail(ctx, HK_ERR_INVALID, "unknown cache handle %llu", (unsigned long long)handles_host[s]);
         for (int r = 0; r < s; ++r)
             if (handles_host[r] == handles_host[s]) return hk_fail(ctx, HK_ERR_INVALID, "row %d repeats a handle", s);
+        if (!prefill && c->pending.count(handles_host[s]))
+            return hk_fail(ctx, HK_ERR_INVALID, "handle %llu is a partial prefill: advance it to completion first",
+                           (unsigned long long)handles_host[s]);
         hs[s] = &it->second;
         const int len = cu_host[s + 1] - cu_host[s];
         if (len <= 0) return hk_fail(ctx, HK_ERR_INVALID, "cached continuation requires nonempty tokens (row %d)", s);
@@ -362,5 +411,206 @@ static int forward_cached(hk_kev_cache* c, const uint64_t* handles_host, int n_s
         h.tokens = lens[s];
         h.cur ^= 1;
     }
+    return HK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// exact-prefix retention and resumable chunked prefill
+// ---------------------------------------------------------------------------
+
+// Charged bytes of a retained prefix of `tokens` tokens, ModelCache::retention_bytes
+// (qwen3_5.rs:1161-1185) on this cache's storage: 8 per token + 512, and per layer 512 plus
+// the bytes it holds (attention: its K and V pages; Gated DeltaNet: the fp32 recurrent state
+// and the conv tail).
+static size_t retention_bytes(const hk_kev_cache* c, int tokens) {
+    const size_t pages = (size_t)(tokens + c->P - 1) / c->P;
+    return (size_t)tokens * 8 + 512 + (size_t)(c->n_attn + c->n_gdn) * 512 + (size_t)c->n_attn * pages * 2 * c->page_bytes +
+           (size_t)c->n_gdn * (c->state_layer + c->conv_layer);
+}
+
+// PrefixSnapshots::trim (qwen3_5.rs:1222-1233): evict the oldest snapshots until the retained
+// bytes fit max_bytes - incoming, and, when one is about to be added, until fewer than 16 remain.
+static void trim_prefixes(hk_kev_cache* c, size_t max_bytes, size_t incoming) {
+    const size_t cap = max_bytes > incoming ? max_bytes - incoming : 0;
+    while (c->prefix_bytes > cap || (c->prefixes.size() >= 16 && incoming > 0)) {
+        if (c->fifo.empty()) break;
+        auto it = c->prefixes.find(c->fifo.front());
+        c->fifo.pop_front();
+        if (it == c->prefixes.end()) continue;
+        c->prefix_bytes -= it->second.bytes;
+        drop_handle(c, it->second.h);
+        c->prefixes.erase(it);
+    }
+}
+
+// retain_prefix (qwen3_5.rs:3017-3041): keep one immutable snapshot of a completed prefix if its
+// charged bytes fit the budget; a snapshot that cannot be made leaves the prefix uncached.
+static void retain_prefix(hk_kev_cache* c, const KevHandle& h, const std::vector<int32_t>& key, size_t max_bytes) {
+    if (c->prefixes.count(key)) return;
+    const size_t bytes = retention_bytes(c, (int)key.size());
+    if (bytes > max_bytes) return;
+    Snapshot snap;
+    if (clone_handle(c, h, snap.h) != HK_OK) return;
+    trim_prefixes(c, max_bytes, bytes);
+    snap.bytes = bytes;
+    c->prefixes.emplace(key, std::move(snap));
+    c->fifo.push_back(key);
+    c->prefix_bytes += bytes;
+}
+
+// validate_prefix (qwen3_5.rs:3003-3015)
+static int validate_prefix(hk_kev_cache* c, const int32_t* ids_host, int n) {
+    const hk_kev_config& cfg = c->m->cfg;
+    if (!ids_host || n <= 0 || n > cfg.max_context)
+        return hk_fail(c->m->ctx, HK_ERR_INVALID, "prefill must be nonempty, contain valid token ids and fit max_context");
+    for (int i = 0; i < n; ++i)
+        if (ids_host[i] < 0 || ids_host[i] >= cfg.vocab)
+            return hk_fail(c->m->ctx, HK_ERR_INVALID,
+                           "prefill must be nonempty, contain valid token ids and fit max_context");
+    return HK_OK;
+}
+
+// A new caller handle cloned from a retained snapshot.
+static int clone_snapshot(hk_kev_cache* c, const Snapshot& snap, uint64_t* handle_out) {
+    KevHandle h;
+    if (int rc = clone_handle(c, snap.h, h)) return rc;
+    const uint64_t id = c->next_id++;
+    c->handles.emplace(id, std::move(h));
+    *handle_out = id;
+    return HK_OK;
+}
+
+// One prefill chunk ids_dev[0 .. len) appended to handle id (no outputs read).
+static int run_chunk(hk_kev_cache* c, uint64_t id, const int32_t* ids_dev, int len, void* workspace,
+                     size_t workspace_bytes) {
+    const size_t model_ws = (kev_workspace_bytes(c->m, len, 1, 0) + 255) & ~(size_t)255;
+    if (model_ws + table_bytes(c, 1) > workspace_bytes)
+        return hk_fail(c->m->ctx, HK_ERR_INVALID, "workspace too small: %zu < %zu (hk_kev_cache_workspace_size of a chunk)",
+                       workspace_bytes, model_ws + table_bytes(c, 1));
+    int32_t* cu_dev = (int32_t*)((char*)workspace + model_ws + table_bytes(c, 1) - 256);
+    const int32_t cu_host[2] = {0, len};
+    hipSetDevice(c->m->ctx->device);
+    if (hipMemcpyAsync(cu_dev, cu_host, sizeof(cu_host), hipMemcpyHostToDevice, c->m->ctx->stream) != hipSuccess)
+        return hk_fail(c->m->ctx, HK_ERR_DEVICE, "prefill cu_seqlens upload failed");
+    // forward_cached synchronises the stream before it returns, so cu_host outlives the copy
+    return forward_cached(c, &id, 1, ids_dev, cu_dev, cu_host, workspace, workspace_bytes, nullptr, nullptr, nullptr,
+                          true);
+}
+
+static void count_chunk(hk_prefill_work* work, int len, bool second) {
+    if (!work) return;
+    work->forward_calls += 1;
+    work->processed_tokens += (uint64_t)len;
+    if (second) work->chunked_prefills += 1;
+}
+
+extern "C" int hk_kev_cache_prefill_cached(hk_kev_cache* c, const int32_t* ids_host, const int32_t* ids_dev,
+                                           int n_tokens, size_t max_bytes, int chunk_tokens, void* workspace,
+                                           size_t workspace_bytes, uint64_t* handle_out, int* hit_out,
+                                           hk_prefill_work* work) {
+    if (!c || !handle_out || !hit_out) return HK_ERR_INVALID;
+    hk_ctx* ctx = c->m->ctx;
+    if (int rc = validate_prefix(c, ids_host, n_tokens)) return rc;
+    if (!ids_dev || !workspace || chunk_tokens < 0)
+        return hk_fail(ctx, HK_ERR_INVALID, "invalid prefill arguments");
+    trim_prefixes(c, max_bytes, 0);
+    if ((int)c->handles.size() >= c->max_handles)
+        return hk_fail(ctx, HK_ERR_NOMEM, "cache holds its maximum of %d live handles", c->max_handles);
+    std::vector<int32_t> key(ids_host, ids_host + n_tokens);
+    if (max_bytes > 0) {
+        auto it = c->prefixes.find(key);
+        if (it != c->prefixes.end()) {
+            if (int rc = clone_snapshot(c, it->second, handle_out)) return rc;
+            *hit_out = 1;
+            return HK_OK;
+        }
+    }
+    // compute_prefix (qwen3_5.rs:2937-2971): a new handle, the prefix in chunks of chunk_tokens
+    // (0: one call)
+    uint64_t id = 0;
+    if (int rc = hk_kev_cache_open(c, &id)) return rc;
+    const int step = chunk_tokens > 0 ? chunk_tokens : n_tokens;
+    for (int off = 0, index = 0; off < n_tokens; off += step, ++index) {
+        const int len = n_tokens - off < step ? n_tokens - off : step;
+        count_chunk(work, len, index == 1);
+        if (int rc = run_chunk(c, id, ids_dev + off, len, workspace, workspace_bytes)) {
+            hk_kev_cache_release(c, id);
+            return rc;
+        }
+    }
+    retain_prefix(c, c->handles.at(id), key, max_bytes);
+    *handle_out = id;
+    *hit_out = 0;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_begin_resumable(hk_kev_cache* c, const int32_t* ids_host, int n_tokens, size_t max_bytes,
+                                            uint64_t* handle_out, int* hit_out) {
+    if (!c || !handle_out || !hit_out) return HK_ERR_INVALID;
+    hk_ctx* ctx = c->m->ctx;
+    if (int rc = validate_prefix(c, ids_host, n_tokens)) return rc;
+    if ((int)c->handles.size() >= c->max_handles)
+        return hk_fail(ctx, HK_ERR_NOMEM, "cache holds its maximum of %d live handles", c->max_handles);
+    trim_prefixes(c, max_bytes, 0);
+    std::vector<int32_t> key(ids_host, ids_host + n_tokens);
+    if (max_bytes > 0) {
+        auto it = c->prefixes.find(key);
+        if (it != c->prefixes.end()) {
+            if (int rc = clone_snapshot(c, it->second, handle_out)) return rc;
+            *hit_out = 1;
+            return HK_OK;
+        }
+    }
+    uint64_t id = 0;
+    if (int rc = hk_kev_cache_open(c, &id)) return rc;
+    Pending p;
+    p.tokens = std::move(key);
+    p.max_bytes = max_bytes;
+    c->pending.emplace(id, std::move(p));
+    *handle_out = id;
+    *hit_out = 0;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_advance_resumable(hk_kev_cache* c, uint64_t handle, const int32_t* ids_dev,
+                                              int chunk_tokens, void* workspace, size_t workspace_bytes,
+                                              hk_prefill_work* work, int* complete_out) {
+    if (!c || !complete_out) return HK_ERR_INVALID;
+    hk_ctx* ctx = c->m->ctx;
+    auto pit = c->pending.find(handle);
+    if (pit == c->pending.end()) return hk_fail(ctx, HK_ERR_INVALID, "unknown or completed resumable prefill handle");
+    auto hit = c->handles.find(handle);
+    if (hit == c->handles.end()) return hk_fail(ctx, HK_ERR_INVALID, "unknown resumable cache handle");
+    if (!ids_dev || !workspace || chunk_tokens <= 0)
+        return hk_fail(ctx, HK_ERR_INVALID, "resumable prefill needs the prefix ids and a chunk size > 0");
+    const int n = (int)pit->second.tokens.size();
+    const int off = hit->second.tokens;
+    const int end = n < off + chunk_tokens ? n : off + chunk_tokens;
+    // work counts every native attempt, failed ones included (backend.rs:413-425)
+    count_chunk(work, end - off, off == chunk_tokens);
+    if (int rc = run_chunk(c, handle, ids_dev + off, end - off, workspace, workspace_bytes)) return rc;
+    const bool complete = end == n;
+    if (complete) {
+        Pending p = std::move(pit->second);
+        c->pending.erase(pit);
+        retain_prefix(c, c->handles.at(handle), p.tokens, p.max_bytes);
+    }
+    *complete_out = complete ? 1 : 0;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_clear_prefixes(hk_kev_cache* c) {
+    if (!c) return HK_ERR_INVALID;
+    for (auto& kv : c->prefixes) drop_handle(c, kv.second.h);
+    c->prefixes.clear();
+    c->fifo.clear();
+    c->prefix_bytes = 0;
+    return HK_OK;
+}
+
+extern "C" int hk_kev_cache_prefix_stats(hk_kev_cache* c, int* count_out, size_t* bytes_out) {
+    if (!c || !count_out || !bytes_out) return HK_ERR_INVALID;
+    *count_out = (int)c->prefixes.size();
+    *bytes_out = c->prefix_bytes;
     return HK_OK;
 }

@@ -285,6 +285,8 @@ extern "C" int hk_kev_workspace_size(hk_kev_model* m, int n_tokens, int n_seqs, 
 extern "C" int hk_kev_forward(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev, const int32_t* cu_host,
                               int n_seqs, const int32_t* bt, int bt_stride, int num_pages, void* workspace,
                               size_t workspace_bytes, float* logits, void* hidden_last) {
+    if (!m) return HK_ERR_INVALID;
+    if (m->cfg.n_out > 0 && !logits) return hk_fail(m->ctx, HK_ERR_INVALID, "logits output required");
     return kev_forward_impl(m, ids, cu_dev, cu_host, n_seqs, bt, bt_stride, num_pages, workspace, workspace_bytes,
                             logits, hidden_last, nullptr, nullptr);
 }
@@ -362,7 +364,7 @@ int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
     const hk_kev_config& c = m->cfg;
     if (!ids || !cu_dev || !cu_host || !bt || !workspace || n_seqs <= 0 || bt_stride <= 0 || num_pages <= 0)
         return hk_fail(ctx, HK_ERR_INVALID, "invalid forward arguments");
-    if (c.n_out > 0 && !logits && !readout) return hk_fail(ctx, HK_ERR_INVALID, "logits output required");
+    // (callers check that the outputs they need are given; a null logits skips the head)
     if (cu_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "cu_seqlens[0] must be 0");
     int max_len = 0;
     for (int s = 0; s < n_seqs; ++s) {

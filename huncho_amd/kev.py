@@ -450,6 +450,50 @@ class KevCache:
             raise
         return h
 
+    def _prefix_ids(self, tokens):
+        ids = np.ascontiguousarray(np.asarray(tokens, np.int64).astype(np.int32))
+        return ids, torch.from_numpy(ids).to(self.model.device)
+
+    def prefill_cached(self, tokens, max_bytes: int, chunk_tokens: int = 0, work: abi.PrefillWork | None = None):
+        """Backend::prefill_cached: (handle, hit). An identical retained prefix is cloned (hit);
+        otherwise the prefix is computed in chunks of chunk_tokens (0: one forward) and retained
+        if its charged bytes fit max_bytes."""
+        ids, dev = self._prefix_ids(tokens)
+        step = chunk_tokens if chunk_tokens > 0 else max(len(ids), 1)
+        ws = self._workspace(min(step, max(len(ids), 1)), 1)
+        h, hit = C.c_uint64(), C.c_int()
+        self.ctx.check(abi.lib().hk_kev_cache_prefill_cached(
+            self.h, ids.ctypes.data_as(C.POINTER(C.c_int32)), dev.data_ptr(), len(ids), max_bytes, chunk_tokens,
+            ws.data_ptr(), ws.numel(), C.byref(h), C.byref(hit), C.byref(work) if work is not None else None))
+        return h.value, bool(hit.value)
+
+    def begin_resumable(self, tokens, max_bytes: int):
+        """Backend::begin_resumable_prefill: (handle, hit); a miss leaves the handle pending."""
+        ids, _ = self._prefix_ids(tokens)
+        h, hit = C.c_uint64(), C.c_int()
+        self.ctx.check(abi.lib().hk_kev_cache_begin_resumable(
+            self.h, ids.ctypes.data_as(C.POINTER(C.c_int32)), len(ids), max_bytes, C.byref(h), C.byref(hit)))
+        return h.value, bool(hit.value)
+
+    def advance_resumable(self, handle: int, tokens, chunk_tokens: int, work: abi.PrefillWork | None = None) -> bool:
+        """Backend::advance_resumable_prefill: appends the next chunk; True once complete."""
+        _, dev = self._prefix_ids(tokens)
+        ws = self._workspace(chunk_tokens, 1)
+        done = C.c_int()
+        self.ctx.check(abi.lib().hk_kev_cache_advance_resumable(
+            self.h, handle, dev.data_ptr(), chunk_tokens, ws.data_ptr(), ws.numel(),
+            C.byref(work) if work is not None else None, C.byref(done)))
+        return bool(done.value)
+
+    def clear_prefixes(self) -> None:
+        self.ctx.check(abi.lib().hk_kev_cache_clear_prefixes(self.h))
+
+    def prefix_stats(self):
+        """(retained snapshots, their charged bytes)"""
+        n, b = C.c_int(), C.c_size_t()
+        self.ctx.check(abi.lib().hk_kev_cache_prefix_stats(self.h, C.byref(n), C.byref(b)))
+        return n.value, b.value
+
     def fork_batch(self, parent: int, suffixes, temperature: float = 1.0):
         """forward_fork_batch: one private branch of `parent` per suffix, evaluated together; the
         parent is left unchanged and every branch is released, on success or failure."""

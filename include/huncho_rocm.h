@@ -349,6 +349,48 @@ int hk_kev_forward_cached_readout(hk_kev_cache* c, const uint64_t* handles_host,
                                   const int32_t* cu_seqlens_dev, const int32_t* cu_seqlens_host, void* workspace_dev,
                                   size_t workspace_bytes, const hk_kev_readout* readout, float* logits_dev);
 
+/* Work counters of the prefill calls (PrefillWork, crates/huncho-core/src/backend.rs:85-89):
+ * native forward calls (failed attempts included), tokens processed, and prefills that took a
+ * second chunk. */
+typedef struct hk_prefill_work {
+    uint64_t forward_calls;
+    uint64_t processed_tokens;
+    uint64_t chunked_prefills;
+} hk_prefill_work;
+
+/* Backend::prefill_cached / prefill_cached_with_work (backend.rs:371-395; qwen3_5.rs:2850-2865,
+ * 2937-3041): a new handle holding a prefix, given on the host (ids_host: the key and the checks)
+ * and on the device (ids_dev: the same ids). With max_bytes > 0 an identical retained prefix is
+ * cloned (hit = 1, no model work). Otherwise the prefix is computed in chunks of chunk_tokens (0:
+ * one forward) and, if its charged bytes (8 per token + 512, and per layer 512 plus its pages,
+ * recurrent state and conv tail: ModelCache::retention_bytes, qwen3_5.rs:1161-1185) fit
+ * max_bytes, kept as an immutable snapshot; older snapshots are evicted first in, first out to
+ * make room, and at most 16 are kept (qwen3_5.rs:1215-1234). Snapshots hold pool pages (shared
+ * with the handles cloned from them) until evicted or cleared. workspace: at least
+ * hk_kev_cache_workspace_size(c, largest chunk, 1) bytes. Synchronises the stream. work may be
+ * NULL. */
+int hk_kev_cache_prefill_cached(hk_kev_cache* c, const int32_t* ids_host, const int32_t* ids_dev, int n_tokens,
+                                size_t max_bytes, int chunk_tokens, void* workspace_dev, size_t workspace_bytes,
+                                uint64_t* handle_out, int* hit_out, hk_prefill_work* work);
+/* Backend::begin_resumable_prefill (backend.rs:399-414; qwen3_5.rs:2873-2897): validates the
+ * prefix and returns either a clone of an identical retained prefix (hit = 1, complete) or an
+ * empty pending handle (hit = 0; no model work). A pending handle cannot be forked or continued
+ * until it is complete; releasing it cancels the prefill. */
+int hk_kev_cache_begin_resumable(hk_kev_cache* c, const int32_t* ids_host, int n_tokens, size_t max_bytes,
+                                 uint64_t* handle_out, int* hit_out);
+/* Backend::advance_resumable_prefill (backend.rs:416-425; qwen3_5.rs:2899-2934): appends the next
+ * chunk (at most chunk_tokens > 0) of a pending prefix (ids_dev: the whole prefix on the device).
+ * complete = 1 once the prefix is whole; it is then retained as by prefill_cached and the handle
+ * is an ordinary one. A failed chunk commits nothing and still counts as work. */
+int hk_kev_cache_advance_resumable(hk_kev_cache* c, uint64_t handle, const int32_t* ids_dev, int chunk_tokens,
+                                   void* workspace_dev, size_t workspace_bytes, hk_prefill_work* work,
+                                   int* complete_out);
+/* Backend::clear_prefix_cache (backend.rs:427-430): drops every retained snapshot; handles
+ * cloned from them keep their own state and page references. */
+int hk_kev_cache_clear_prefixes(hk_kev_cache* c);
+/* The number of retained snapshots and their charged bytes. */
+int hk_kev_cache_prefix_stats(hk_kev_cache* c, int* count_out, size_t* bytes_out);
+
 /* ---- ModernBERT encoder (the Laya backend: candle ModernBert, crates/huncho-backend/src/
  * candle.rs:65-117 load, 319-416 forward; config normalisation 157-203) ----------------------
  * LayerNorm without bias: y = (x - mean) / sqrt(var + eps) * w, w fp32 [width], width <= 2048. */

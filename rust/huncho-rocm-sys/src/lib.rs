@@ -129,6 +129,14 @@ pub struct hk_kev_readout {
 }
 
 #[repr(C)]
+#[derive(Default, Clone, Copy)]
+pub struct hk_prefill_work {
+    pub forward_calls: u64,
+    pub processed_tokens: u64,
+    pub chunked_prefills: u64,
+}
+
+#[repr(C)]
 pub struct hk_bert_config {
     pub hidden: c_int,
     pub n_layers: c_int,
@@ -304,6 +312,24 @@ extern "C" {
         c: *mut hk_kev_cache, handles_host: *const u64, n_seqs: c_int, ids_dev: *const i32,
         cu_seqlens_dev: *const i32, cu_seqlens_host: *const i32, workspace_dev: *mut c_void,
         workspace_bytes: usize, readout: *const hk_kev_readout, logits_dev: *mut f32
+    ) -> c_int;
+    pub fn hk_kev_cache_prefill_cached(
+        c: *mut hk_kev_cache, ids_host: *const i32, ids_dev: *const i32, n_tokens: c_int,
+        max_bytes: usize, chunk_tokens: c_int, workspace_dev: *mut c_void, workspace_bytes: usize,
+        handle_out: *mut u64, hit_out: *mut c_int, work: *mut hk_prefill_work
+    ) -> c_int;
+    pub fn hk_kev_cache_begin_resumable(
+        c: *mut hk_kev_cache, ids_host: *const i32, n_tokens: c_int, max_bytes: usize,
+        handle_out: *mut u64, hit_out: *mut c_int
+    ) -> c_int;
+    pub fn hk_kev_cache_advance_resumable(
+        c: *mut hk_kev_cache, handle: u64, ids_dev: *const i32, chunk_tokens: c_int,
+        workspace_dev: *mut c_void, workspace_bytes: usize, work: *mut hk_prefill_work,
+        complete_out: *mut c_int
+    ) -> c_int;
+    pub fn hk_kev_cache_clear_prefixes(c: *mut hk_kev_cache) -> c_int;
+    pub fn hk_kev_cache_prefix_stats(
+        c: *mut hk_kev_cache, count_out: *mut c_int, bytes_out: *mut usize
     ) -> c_int;
     pub fn hk_layer_norm(
         ctx: *mut hk_ctx, dtype: c_int, x_dev: *const c_void, x_tok: c_long, w_dev: *const f32,

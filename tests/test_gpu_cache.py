@@ -233,3 +233,116 @@ def test_fp32_continuation_and_fork(setup, model32):
     cache.release(child)
     assert cache.stats() == (0, 64)
     cache.close()
+
+
+# ---------------------------------------------------------------------------
+# exact-prefix retention (prefill_cached) and resumable chunked prefill
+# ---------------------------------------------------------------------------
+
+def retention_bytes(n_tokens, esz=2):
+    """ModelCache::retention_bytes (qwen3_5.rs:1161-1185) on the cache's storage."""
+    shape = KevShape(**SHAPE)
+    n_attn = sum(1 for t in shape.layer_types if t == 1)
+    n_gdn = shape.n_layers - n_attn
+    page_bytes = shape.n_kv_heads * shape.page_size * shape.head_dim * esz
+    pages = -(-n_tokens // shape.page_size)
+    state = shape.lin_n_v_heads * 128 * 128 * 4
+    conv = shape.conv_dim * 3 * esz
+    return 8 * n_tokens + 512 + shape.n_layers * 512 + n_attn * pages * 2 * page_bytes + n_gdn * (state + conv)
+
+
+def test_prefill_cached_hit_clones_the_prefix(setup):
+    """A retained prefix is cloned on an identical request (hit, no model work); the clone and the
+    original continue identically, and continuing them leaves the snapshot unchanged."""
+    model, cache = setup["model"], KevCache(setup["model"], max_pages=64)
+    prefix, s1, s2 = toks(90, 100), toks(91, 20), toks(92, 33)
+    budget = 1 << 40
+    w = abi.PrefillWork()
+    h1, hit1 = cache.prefill_cached(prefix, budget, work=w)
+    assert not hit1 and (w.forward_calls, w.processed_tokens, w.chunked_prefills) == (1, 100, 0)
+    assert cache.prefix_stats() == (1, retention_bytes(100))
+    h2, hit2 = cache.prefill_cached(prefix, budget, work=w)
+    assert hit2 and (w.forward_calls, w.processed_tokens) == (1, 100) and cache.tokens(h2) == 100
+    _, p1, _ = cache.continue_rows([h1], [s1], TEMP)
+    _, p2, _ = cache.continue_rows([h2], [s1], TEMP)
+    assert np.array_equal(p1, p2)  # the same pages and state, the same computation
+    h3, hit3 = cache.prefill_cached(prefix, budget)
+    assert hit3
+    _, p3, _ = cache.continue_rows([h3], [s2], TEMP)
+    d = float(np.abs(p3[0] - setup["oracle_probs"](prefix + s2)).max())
+    print(f"clone of a retained prefix, continued: vs fp32 oracle {d:.2e}")
+    assert d < 1e-3, d
+    for h in (h1, h2, h3):
+        cache.release(h)
+    assert cache.stats()[0] == 0 and cache.stats()[1] < 64  # the snapshot still holds its pages
+    cache.clear_prefixes()
+    assert cache.prefix_stats() == (0, 0) and cache.stats() == (0, 64)
+    cache.close()
+
+
+def test_prefill_cached_chunks_and_budget(setup):
+    """Chunked prefill equals the whole-prefix prefill; the byte budget decides what is retained
+    and evicts first in, first out."""
+    model, cache = setup["model"], KevCache(setup["model"], max_pages=64)
+    a, b, suffix = toks(93, 150), toks(94, 40), toks(95, 17)
+    w = abi.PrefillWork()
+    h, hit = cache.prefill_cached(a, 0, chunk_tokens=64, work=w)  # budget 0: nothing retained
+    assert not hit and (w.forward_calls, w.processed_tokens, w.chunked_prefills) == (3, 150, 1)
+    assert cache.prefix_stats() == (0, 0)
+    _, p, _ = cache.continue_rows([h], [suffix], TEMP)
+    d_fresh = float(np.abs(p - fresh_probs(model, [a + suffix])).max())
+    d_ref = float(np.abs(p[0] - setup["oracle_probs"](a + suffix)).max())
+    print(f"3-chunk prefill + continuation: vs fresh {d_fresh:.2e}, vs fp32 oracle {d_ref:.2e}")
+    assert d_fresh < 2e-3 and d_ref < 1e-3, (d_fresh, d_ref)
+    cache.release(h)
+    # a budget below the prefix's charged bytes retains nothing
+    h, _ = cache.prefill_cached(b, retention_bytes(40) - 1)
+    assert cache.prefix_stats() == (0, 0)
+    cache.release(h)
+    # a budget for one: the second prefix evicts the first
+    one = max(retention_bytes(40), retention_bytes(150))
+    ha, _ = cache.prefill_cached(a, one)
+    hb, _ = cache.prefill_cached(b, one)
+    assert cache.prefix_stats() == (1, retention_bytes(40))
+    ha2, hit_a = cache.prefill_cached(a, one)
+    assert not hit_a
+    for x in (ha, hb, ha2):
+        cache.release(x)
+    cache.clear_prefixes()
+    assert cache.stats() == (0, 64)
+    cache.close()
+
+
+def test_resumable_prefill(setup):
+    """begin / advance_resumable_prefill: one chunk per call, the partial handle can be neither
+    forked nor continued, completion retains the prefix, cancelling frees the pages."""
+    model, cache = setup["model"], KevCache(setup["model"], max_pages=64)
+    prefix, suffix = toks(96, 150), toks(97, 21)
+    budget = 1 << 40
+    h, hit = cache.begin_resumable(prefix, budget)
+    assert not hit and cache.tokens(h) == 0
+    with pytest.raises(abi.HkError):
+        cache.fork(h)
+    with pytest.raises(abi.HkError):
+        cache.continue_rows([h], [suffix])
+    w = abi.PrefillWork()
+    done = [cache.advance_resumable(h, prefix, 64, w) for _ in range(3)]
+    assert done == [False, False, True] and cache.tokens(h) == 150
+    assert (w.forward_calls, w.processed_tokens, w.chunked_prefills) == (3, 150, 1)
+    with pytest.raises(abi.HkError):  # completed: no longer pending
+        cache.advance_resumable(h, prefix, 64, w)
+    _, p, _ = cache.continue_rows([h], [suffix], TEMP)
+    d = float(np.abs(p[0] - setup["oracle_probs"](prefix + suffix)).max())
+    print(f"resumable prefill (3 chunks) + continuation: vs fp32 oracle {d:.2e}")
+    assert d < 1e-3, d
+    h2, hit2 = cache.begin_resumable(prefix, budget)  # retained at completion
+    assert hit2 and cache.tokens(h2) == 150
+    for x in (h, h2):
+        cache.release(x)
+    cache.clear_prefixes()
+    free0 = cache.stats()[1]
+    h3, _ = cache.begin_resumable(toks(98, 100), budget)
+    assert not cache.advance_resumable(h3, toks(98, 100), 40)
+    cache.release(h3)  # cancel mid-way
+    assert cache.stats() == (0, free0) and cache.prefix_stats() == (0, 0)
+    cache.close()
