@@ -22,9 +22,10 @@
 // Work split: one workgroup of 4 waves (256 threads) per (sequence, value head), two
 // workgroups per CU (79,360 B of LDS each, <= 256 registers per lane), so 2 waves share each
 // SIMD. Wave w owns value columns 32w..32w+31 of the fp32 state S [128 x 128] as two 16-column
-// tiles, held for the whole sequence in sixteen 16x16 MFMA accumulators
-// (v_mfma_f32_16x16x32_{bf16,f16}; lane l: column l % 16, rows 4 (l / 16) + r). Intermediates (K S, R, delta) stay in accumulator layout and feed the
-// next product as its B operand: each product's reduction index is permuted to the
+// tiles, held for the whole sequence in sixteen 16x16 MFMA accumulators (v_mfma_f32_16x16x32_f16
+// for both activation dtypes; lane l: column l % 16, rows 4 (l / 16) + r). Intermediates (K S,
+// R, delta) stay in accumulator layout and feed the next product as its B operand: each
+// product's reduction index is permuted to the
 // accumulator's row order (element e of lane group q <-> index 32 s + 4 q + e, or
 // 32 s + 16 + 4 q + e - 4 for e >= 4), and the A operands are read from LDS in that order.
 //
