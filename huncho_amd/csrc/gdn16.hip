@@ -404,42 +404,45 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
         __syncthreads();
         // ---------------- P1: A, Aqk tiles; K S0, Q S0 ----------------
         // lower tile pairs p = (ti, si), si <= ti: wave w takes pairs w, w + 4, w + 8; upper tiles
-        // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3) of A and Aqk are zeroed, wave w taking w and w + 4
+        // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3) of A and Aqk are zeroed, wave w taking w and w + 4.
+        // The products are formed transposed (K_s as the A operand): lane (q4, j) holds keys
+        // s = 16 si + 4 q4 + r of query / key row t = 16 ti + j, four consecutive columns of
+        // row t of A and Aqk, written as one vector each.
         for (int p = wave; p < 10; p += 4) {
             const int ti = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
             const int si = p - (ti * (ti + 1)) / 2;
             f32x4 kk = f32x4{0.f, 0.f, 0.f, 0.f}, qk = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const v8 b = *(const v8*)(Ks + el(16 * si + j, 32 * ks + 8 * q4));
-                kk = M16<CT>::mma(*(const v8*)(Ks + el(16 * ti + j, 32 * ks + 8 * q4)), b, kk);
-                qk = M16<CT>::mma(*(const v8*)(Qs + el(16 * ti + j, 32 * ks + 8 * q4)), b, qk);
+                const v8 ka = *(const v8*)(Ks + el(16 * si + j, 32 * ks + 8 * q4));
+                kk = M16<CT>::mma(ka, *(const v8*)(Ks + el(16 * ti + j, 32 * ks + 8 * q4)), kk);
+                qk = M16<CT>::mma(ka, *(const v8*)(Qs + el(16 * ti + j, 32 * ks + 8 * q4)), qk);
             }
-            const int s = 16 * si + j, t4 = 16 * ti + 4 * q4;
-            const float gs = Gs[s];
-            const f32x4 gt = *(const f32x4*)(Gs + t4);
-            const f32x4 bt = *(const f32x4*)(Bs + t4);
+            const int t = 16 * ti + j, s4 = 16 * si + 4 * q4;
+            const float gt = Gs[t], bt = Bs[t];
+            const f32x4 gs = *(const f32x4*)(Gs + s4);
+            f32x4 av, qv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int t = t4 + r;
+                const int s = s4 + r;
                 // exp(G_t - G_s) may overflow above the diagonal; the selects drop it there
-                const float ex = __expf(gt[r] - gs);
+                const float ex = __expf(gt - gs[r]);
                 const float dec = s <= t ? ex : 0.0f;
-                Am[t * AS + s] = s < t ? bt[r] * dec * kk[r] : 0.0f;
-                Aq[t * TS + s] = (CT)(dec * qk[r]);
+                av[r] = s < t ? bt * dec * kk[r] : 0.0f;
+                qv[r] = dec * qk[r];
             }
+            *(f32x4*)(Am + t * AS + s4) = av;
+            *(v4*)(Aq + t * TS + s4) = pack1<CT>(qv);
         }
         for (int u = wave; u < 6; u += 4) {
             const int ti = u < 3 ? 0 : u < 5 ? 1 : 2;
             const int si = u < 3 ? u + 1 : u < 5 ? u - 1 : 3;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = 16 * ti + 4 * q4 + r, s = 16 * si + j;
-                Am[t * AS + s] = 0.0f;
-                Aq[t * TS + s] = (CT)0.0f;
-            }
+            const int t = 16 * ti + j, s4 = 16 * si + 4 * q4;
+            *(f32x4*)(Am + t * AS + s4) = f32x4{0.f, 0.f, 0.f, 0.f};
+            *(v4*)(Aq + t * TS + s4) = v4{};
         }
-        // per token tile tt and column tile cw: R = beta (V - e^G K S0), Og = e^G Q S0
+        // per token tile tt and column tile cw: R = beta (V - e^G K S0) and, transposed (lane
+        // (q4, j): value columns 16 cw + 4 q4 + r of token 16 tt + j), Og = e^G Q S0
         f32x4 R[2][4], Og[2][4];
         {
             v8 Sb[2][4];  // S as the B operand of K S0 / Q S0 (k-step s: dk 32 s ..)
@@ -459,11 +462,12 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
 #pragma unroll
                     for (int cw = 0; cw < 2; ++cw) {
                         ksa[cw] = M16<CT>::mma(kop, Sb[cw][s], ksa[cw]);
-                        qsa[cw] = M16<CT>::mma(qop, Sb[cw][s], qsa[cw]);
+                        qsa[cw] = M16<CT>::mma(Sb[cw][s], qop, qsa[cw]);  // (Q S0)^T
                     }
                 }
                 const f32x4 gt = *(const f32x4*)(Gs + 16 * tt + 4 * q4);
                 const f32x4 bt = *(const f32x4*)(Bs + 16 * tt + 4 * q4);
+                const float egj = __expf(Gs[16 * tt + j]);  // e^G of the token of (Q S0)^T
 #pragma unroll
                 for (int cw = 0; cw < 2; ++cw) {
                     // V[16 tt + 4 q4 + r][32 wave + 16 cw + j] through a transposing read: source
@@ -476,7 +480,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
                         const float eg = __expf(gt[r]);
                         // R rounded to CT: it is a 16-bit MFMA operand
                         R[cw][tt][r] = rnd<CT>(bt[r] * (f(vv[r]) - eg * ksa[cw][r]));
-                        Og[cw][tt][r] = eg * qsa[cw][r];
+                        Og[cw][tt][r] = egj * qsa[cw][r];
                     }
                 }
             }
@@ -510,19 +514,22 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
 #pragma unroll
             for (int jj = 0; jj <= i; ++jj) {
                 const v4 aq = *(const v4*)(Aq + (16 * i + j) * TS + 16 * jj + 4 * q4);
+                // (Aqk_ij delta_j)^T = delta_j^T Aqk_ij^T: the delta tile in accumulator layout is
+                // the A operand delta_j^T, the row-major Aqk read the B operand Aqk_ij^T
 #pragma unroll
-                for (int cw = 0; cw < 2; ++cw) Og[cw][i] = M16<CT>::mma16(aq, dbk[cw][jj], Og[cw][i]);
+                for (int cw = 0; cw < 2; ++cw) Og[cw][i] = M16<CT>::mma16(dbk[cw][jj], aq, Og[cw][i]);
             }
         }
-        // O staged over V (dead since P1)
+        // O staged over V (dead since P1): four consecutive columns of one token row per lane,
+        // at the reference's output rounding (T), held exactly in CT
         CT* Os = Vs;
 #pragma unroll
         for (int cw = 0; cw < 2; ++cw)
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)  // the reference's output rounding (T), held exactly in CT
-                    Os[el(16 * tt + 4 * q4 + r, 32 * wave + 16 * cw + j)] = (CT)rnd<T>(Og[cw][tt][r]);
+            for (int tt = 0; tt < 4; ++tt) {
+                const f16x2 lo = rnd_ct<T>(Og[cw][tt][0], Og[cw][tt][1]), hi = rnd_ct<T>(Og[cw][tt][2], Og[cw][tt][3]);
+                *(v4*)(Os + el(16 * tt + j, 32 * wave + 16 * cw + 4 * q4)) = v4{lo[0], lo[1], hi[0], hi[1]};
+            }
         const float glast = Gs[CH - 1];
         const float eglast = __expf(glast);
         v8 Db[2][2];

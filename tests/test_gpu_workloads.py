@@ -251,8 +251,9 @@ def test_kev_cache_continuation_bf16(ctx, kev_bench_case):
     """Four bench rows prefilled to different lengths (on and off page and chunk boundaries) and
     continued together to 512 tokens through hk_kev_forward_cached: the same bf16 gate against
     the fp32 oracle as the whole-batch forward (no farther than the oracle's own bf16 flow), and
-    within that spread of a fresh forward of the same rows (the two split the recurrence into
-    different chunks, which round differently in bf16)."""
+    within twice that spread of a fresh forward of the same rows: the two split the recurrence
+    into different chunks, which round differently in bf16, so each is its own bf16 result, and
+    two results that each pass the gate can differ by up to twice it."""
     from huncho_amd.kev import KevCache, KevModel
 
     case = kev_bench_case
@@ -277,4 +278,4 @@ def test_kev_cache_continuation_bf16(ctx, kev_bench_case):
     d_fresh = float(np.abs(p_cont - p_fresh).max())
     print(f"Kev cache bf16, rows {CACHE_ROWS}: continued vs fp32 oracle {d32:.2e}, vs fresh {d_fresh:.2e} "
           f"(oracle bf16 vs fp32 {spread:.2e})")
-    assert d32 <= spread and d_fresh <= spread, (d32, d_fresh, spread)
+    assert d32 <= spread and d_fresh <= 2 * spread, (d32, d_fresh, spread)
