@@ -279,3 +279,47 @@ def test_kev_cache_continuation_bf16(ctx, kev_bench_case):
     print(f"Kev cache bf16, rows {CACHE_ROWS}: continued vs fp32 oracle {d32:.2e}, vs fresh {d_fresh:.2e} "
           f"(oracle bf16 vs fp32 {spread:.2e})")
     assert d32 <= spread and d_fresh <= 2 * spread, (d32, d_fresh, spread)
+
+
+# ---------------------------------------------------------------------------
+# the bf16 gap layer by layer
+# ---------------------------------------------------------------------------
+
+GAP_DEPTHS = [1, 2, 3, 4, 8, 12, 16, 20, 24]
+
+
+def test_kev_bf16_gap_per_layer(ctx, kev_bench_case):
+    """Where the bf16 forward leaves the oracle's flows, layer by layer: the bench's row 0 (512
+    tokens) through the first L layers of the bench model (then the final norm), for L in
+    GAP_DEPTHS; the final-normed last-token hidden row of the GPU against the oracle's bf16
+    flow (bf16 at the reference's storage points) and fp32 flow. Every depth stays within twice
+    the oracle's own bf16-vs-fp32 distance of the fp32 flow (two bf16 results that each sit
+    within it can differ by up to twice it); the table is printed for the design notes."""
+    import dataclasses
+
+    from huncho_amd.kev import KevModel
+
+    case = kev_bench_case
+    row = case["ids"][:512]
+    f = {k: O.bf16_to_f32(v).reshape(v.shape) for k, v in case["weights"].items()}
+    print("\n  L  type  gpu-vs-bf16flow  gpu-vs-fp32flow  bf16flow-vs-fp32flow   (max |dh| / max |h|, last token)")
+    worst = []
+    for L in GAP_DEPTHS:
+        shape = dataclasses.replace(case["shape"], n_layers=L)
+        model = KevModel(ctx, shape, case["weights"], torch.bfloat16)
+        hid, _, _ = model.forward_readout([row.tolist()], [[511]], want_hidden=True)
+        model.close()
+        assert ctx.take_faults() == 0
+        cfg = _qwen_cfg(shape)
+        h16 = O.QwenModel(cfg, f, bf16=True).forward(row)[-1].astype(np.float64)
+        h32 = O.QwenModel(cfg, f, bf16=False).forward(row)[-1].astype(np.float64)
+        g = np.asarray(hid[0], np.float64)
+        scale = float(np.abs(h32).max())
+        e16 = float(np.abs(g - h16).max()) / scale
+        e32 = float(np.abs(g - h32).max()) / scale
+        spread = float(np.abs(h16 - h32).max()) / scale
+        kind = "attn" if shape.layer_types[-1] == 1 else "gdn"
+        print(f" {L:2d}  {kind:4s}  {e16:15.3e}  {e32:15.3e}  {spread:20.3e}")
+        worst.append((L, e32, spread))
+    for L, e32, spread in worst:
+        assert e32 <= 2 * spread, (L, e32, spread)
