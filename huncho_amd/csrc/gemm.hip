@@ -15,12 +15,13 @@
 // lane's accumulator holds one output row m (lane % 32) and 16 columns n in 4 runs of 4
 // consecutive ones: outputs leave as 8-byte stores, and with the SwiGLU weight layout below a
 // lane holds each gate column and its up column.
-// K steps of 32: W and X tiles (256 rows x 64 B each) go from global memory straight into LDS
-// (global_load_lds_dwordx4) through a ring of 4 stages (4 x 32 KB), issued 3 steps ahead, so a
-// step's loads have three steps of MFMA work (about 1.3 us) to arrive from the L2 or the
-// Infinity Cache. A row's 16-byte chunk c sits at physical chunk c ^ ((row >> 2) & 3): the 16
-// rows that one 16-lane group of a ds_read_b128 reads then land in 16 distinct 16-byte slots of
-// the 256-byte bank row.
+// K steps of 64: W and X tiles (256 rows x 128 B each, whole 128-byte lines) go from global
+// memory straight into LDS (global_load_lds_dwordx4, 8 rows per copy) through two buffers
+// (2 x 64 KB); a step's copies are issued when it starts and have the step's 64 MFMAs per wave
+// to arrive. (K steps of 32 through a 4-stage ring read half lines per row and were 5-8 %
+// slower.) A row's 16-byte chunk c sits at physical chunk c ^ ((row >> 1) & 7): the 16 rows
+// that one 16-lane group of a ds_read_b128 reads, two per 256-byte bank row, then land in 16
+// distinct 16-byte slots.
 // Tiles: the grid is (tiles); tile ids are taken XCD-major (workgroup b runs on XCD b % 8, and
 // the tiles of one XCD form a contiguous range), and inside an XCD's range 4 m-panels are swept
 // across all n-panels before the next 4, so the operand slices the concurrent tiles share stay
@@ -35,19 +36,13 @@
 namespace hk {
 namespace gemm {
 
-constexpr int BM = 256, BN = 256, BK = 32, NTHREADS = 256, NWAVES = 4, STAGES = 4;
+constexpr int BM = 256, BN = 256, BK = 64, NTHREADS = 256, NWAVES = 4, STAGES = 2;
 constexpr int MB = 4;                     // 32-row m blocks per wave
-constexpr int ROW_BYTES = BK * 2;         // 64
-constexpr int TILE_BYTES = 256 * ROW_BYTES;  // one operand tile of one stage: 16 KB
+constexpr int ROW_BYTES = BK * 2;         // 128
+constexpr int TILE_BYTES = 256 * ROW_BYTES;  // one operand tile of one stage: 32 KB
 constexpr size_t LDS_BYTES = (size_t)STAGES * 2 * TILE_BYTES;
-// s_waitcnt encoding of vmcnt(n) with expcnt and lgkmcnt at their maxima (vmcnt bits 3:0 and
-// 15:14)
-constexpr int vmcnt_enc(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
-// vmcnt(8): the copies of the stage issued after this one may stay in flight (each wave issues 8
-// copies per stage)
-constexpr int VMCNT_1STAGE = vmcnt_enc(8);
 
-__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
 template <typename T> __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
@@ -80,11 +75,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_xwt(GemmArgs a) {
     // chunk (i % 4) ^ swz(row) of that row; a wave copies rows 64 wave .. + 63 of each operand
     // tile (4 copies of 16 rows). For copy c the row is 64 wave + 16 c + i / 4, so swz(row) =
     // (i / 16) & 3 (the same for every copy), and copy c adds 16 c rows.
-    const int crow = lane >> 2, cpc = lane & 3;
-    const int lc = cpc ^ ((crow >> 2) & 3);
-    const T* const wsrc = (const T*)a.w + (long)(n0 + 64 * wave + crow) * a.ldw + 8 * lc;
+    // BK 64: lane i of copy c writes LDS row 64 wave + 8 c + i / 8 at physical chunk i % 8,
+    // holding logical chunk (i % 8) ^ swz(row) = (i % 8) ^ (4 (c & 1) + (i / 8) / 2)
+    const int crow = lane >> 3, cpc = lane & 7;
+    const int lc0 = cpc ^ (crow >> 1), lc1 = cpc ^ (4 + (crow >> 1));
+    const T* const wsrc = (const T*)a.w + (long)(n0 + 64 * wave + crow) * a.ldw;
     const long xr0 = m0 + 64 * wave + crow;
-    // X rows past M read row M - 1 (their outputs are not stored)
     const bool x_tail = m0 + BM > a.M;
     const T* const xbase = (const T*)a.x;
     const unsigned lbase = lds_address(gsm);
@@ -92,10 +88,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_xwt(GemmArgs a) {
         const unsigned wb = lbase + buf * 2 * TILE_BYTES, xb = wb + TILE_BYTES;
         const long ko = (long)ks * BK;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const unsigned dst = (unsigned)((64 * wave + 16 * c) * ROW_BYTES);
-            copy_x4(wsrc + (long)(16 * c) * a.ldw + ko, wb + dst);
-            const long xr = x_tail ? min(xr0 + 16 * c, (long)a.M - 1) : xr0 + 16 * c;
+        for (int c = 0; c < 8; ++c) {
+            const int lc = (c & 1) ? lc1 : lc0;
+            const unsigned dst = (unsigned)((64 * wave + 8 * c) * ROW_BYTES);
+            copy_x4(wsrc + (long)(8 * c) * a.ldw + 8 * lc + ko, wb + dst);
+            const long xr = x_tail ? min(xr0 + 8 * c, (long)a.M - 1) : xr0 + 8 * c;
             copy_x4(xbase + xr * a.ldx + 8 * lc + ko, xb + dst);
         }
     };
@@ -115,14 +112,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_xwt(GemmArgs a) {
     const int nk = a.K / BK;
     // fragments of k16 step (ks, s2) live in set s2: af/bf[s2][block]
     v8 af[2][4], bf[2][MB];
-    auto read_frags = [&](int ks, int s2) {
+    auto read_frags = [&](int ks, int s2, int set) {
         const char* wt = gsm + (ks % STAGES) * 2 * TILE_BYTES;
         const char* xt = wt + TILE_BYTES;
         const int co = ((2 * s2 + g) ^ sw) << 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[s2][i] = *(const v8*)(wt + abase + co + 2048 * i);
+        for (int i = 0; i < 4; ++i) af[set][i] = *(const v8*)(wt + abase + co + 32 * ROW_BYTES * i);
 #pragma unroll
-        for (int j = 0; j < MB; ++j) bf[s2][j] = *(const v8*)(xt + bbase + co + 2048 * j);
+        for (int j = 0; j < MB; ++j) bf[set][j] = *(const v8*)(xt + bbase + co + 32 * ROW_BYTES * j);
     };
     auto mfmas = [&](int s2) {
 #pragma unroll
@@ -130,33 +127,29 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_xwt(GemmArgs a) {
 #pragma unroll
             for (int j = 0; j < MB; ++j) acc[i][j] = Mma16<T>::mma(af[s2][i], bf[s2][j], acc[i][j]);
     };
-#pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st)
-        if (st < nk) load_step(st, st);
-    // step 0's copies (steps 1 and 2 may still fly)
-    if (nk >= 3)
-        __builtin_amdgcn_s_waitcnt(vmcnt_enc(16));
-    else if (nk == 2)
-        __builtin_amdgcn_s_waitcnt(VMCNT_1STAGE);
-    else
-        __builtin_amdgcn_s_waitcnt(VMCNT0);
+    load_step(0, 0);
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
     __syncthreads();
-    read_frags(0, 0);
+    read_frags(0, 0, 0);
     for (int ks = 0; ks < nk; ++ks) {
-        read_frags(ks, 1);
+        // buffer (ks + 1) % 2 was last read in step ks - 1, before the barrier that ended it
+        if (ks + 1 < nk) load_step(ks + 1, (ks + 1) & 1);
+        read_frags(ks, 1, 1);
         __builtin_amdgcn_sched_barrier(0);
         mfmas(0);
         __builtin_amdgcn_sched_barrier(0);
-        // step ks + 1's copies are done (step ks + 2's may still fly); the barrier publishes every
-        // wave's, and every wave has finished reading step ks - 1's buffer, which takes step ks + 3
+        read_frags(ks, 2, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(1);
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(ks, 3, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(0);
+        __builtin_amdgcn_sched_barrier(0);
         if (ks + 1 < nk) {
-            if (ks + 2 < nk)
-                __builtin_amdgcn_s_waitcnt(VMCNT_1STAGE);
-            else
-                __builtin_amdgcn_s_waitcnt(VMCNT0);
+            __builtin_amdgcn_s_waitcnt(VMCNT0);
             __syncthreads();
-            if (ks + STAGES - 1 < nk) load_step(ks + STAGES - 1, (ks + STAGES - 1) % STAGES);
-            read_frags(ks + 1, 0);
+            read_frags(ks + 1, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
         mfmas(1);
