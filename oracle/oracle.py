@@ -598,3 +598,106 @@ def load_tiny_modernbert(root: Path):
         if m is not None:
             weights[m] = f32(v)
     return cfg, weights
+
+
+# ---------------------------------------------------------------------------
+# the typed Laya decision head (crates/huncho-backend/src/candle.rs:500-694), numpy
+# ---------------------------------------------------------------------------
+
+def layer_norm_affine(x, w, b, eps=1e-5):
+    """candle_nn::ops::layer_norm: (x - mean) / sqrt(var + eps) * w + b over the last axis, fp32."""
+    x = np.asarray(x, np.float32)
+    mean = x.mean(-1, keepdims=True, dtype=np.float32)
+    d = x - mean
+    var = (d * d).mean(-1, keepdims=True, dtype=np.float32)
+    return (d / np.sqrt(var + np.float32(eps)) * f32(w) + f32(b)).astype(np.float32)
+
+
+def gelu_erf_np(x):
+    """0.5 x (1 + erf(x / sqrt 2)), elementwise in float64, returned as fp32."""
+    from scipy.special import erf
+
+    x = np.asarray(x, np.float64)
+    return (0.5 * x * (1.0 + erf(x / math.sqrt(2.0)))).astype(np.float32)
+
+
+def laya_head(h, weights: dict, qtype: int, positions, bf16: bool = False):
+    """LayaHead::forward (candle.rs:651-694) for one sequence: h [T, d] encoder output rows;
+    z = h + type_emb[qtype]; every `head.layers.{i}` is a pre-norm (norm_first) transformer
+    encoder layer, LayaLayer::forward_queries (520-585): LayerNorm (eps 1e-5, weight and bias) ->
+    in_proj (q|k|v, bias) -> multi-head softmax attention over the whole sequence (d / 64 heads,
+    scale head_dim^-1/2) -> out_proj (bias) -> residual; LayerNorm -> linear1 (bias) -> ReLU ->
+    linear2 (bias) -> residual. The rows at `positions` then go through the scorer LayerNorm ->
+    Linear -> GELU (erf) -> Linear(-> 1). Returns the [n_positions] scores. bf16: every
+    tensor op's result rounded to bf16, as candle's bf16 tensors store them (math in fp32)."""
+    rnd = round_bf16 if bf16 else (lambda a: np.asarray(a, np.float32))
+    w = {k: rnd(f32(v)) for k, v in weights.items()}
+    z = rnd(f32(h) + w["type_emb.weight"][qtype][None, :])
+    d = z.shape[1]
+    nhead = max(d // 64, 1)
+    hd = d // nhead
+    i = 0
+    while f"head.layers.{i}.self_attn.in_proj_weight" in w:
+        p = f"head.layers.{i}."
+        xn = rnd(layer_norm_affine(z, w[p + "norm1.weight"], w[p + "norm1.bias"]))
+        qkv = rnd(rnd(xn @ w[p + "self_attn.in_proj_weight"].T) + w[p + "self_attn.in_proj_bias"])
+        q, k, v = qkv[:, :d], qkv[:, d:2 * d], qkv[:, 2 * d:]
+        out = np.empty_like(q)
+        for hh in range(nhead):
+            sl = slice(hh * hd, (hh + 1) * hd)
+            s = rnd(rnd(q[:, sl] @ k[:, sl].T) * np.float32(1.0 / math.sqrt(hd)))
+            e = np.exp(s - s.max(-1, keepdims=True))
+            pr = rnd(e / e.sum(-1, keepdims=True))
+            out[:, sl] = rnd(pr @ v[:, sl])
+        o = rnd(rnd(out @ w[p + "self_attn.out_proj.weight"].T) + w[p + "self_attn.out_proj.bias"])
+        x = rnd(z + o)
+        xn2 = rnd(layer_norm_affine(x, w[p + "norm2.weight"], w[p + "norm2.bias"]))
+        ff = rnd(np.maximum(rnd(rnd(xn2 @ w[p + "linear1.weight"].T) + w[p + "linear1.bias"]), 0.0))
+        ff2 = rnd(rnd(ff @ w[p + "linear2.weight"].T) + w[p + "linear2.bias"])
+        z = rnd(x + ff2)
+        i += 1
+    if i == 0:
+        raise ValueError("a Laya head needs at least one head layer")
+    m = z[np.asarray(positions, np.int64)]
+    y = rnd(layer_norm_affine(m, w["scorer.0.weight"], w["scorer.0.bias"]))
+    y = rnd(rnd(y @ w["scorer.1.weight"].T) + w["scorer.1.bias"])
+    y = rnd(gelu_erf_np(y))
+    y = rnd(rnd(y @ w["scorer.3.weight"].T) + w["scorer.3.bias"])
+    return y[:, 0].astype(np.float32)
+
+
+def laya_test_head(d: int, n_layers: int) -> dict:
+    """The reference's deterministic test head (crates/huncho-backend/tests/support/laya.rs:5-52):
+    one LCG stream (seed 7, x <- 1664525 x + 1013904223 mod 2^32, value (x >> 8) / 2^24 - 0.5)
+    over the tensors in insertion order; norm weights 1 + value / 8, everything else
+    value / sqrt(d); linear1 has 2 d + 1 rows, the scorer d / 2 + 1 hidden units."""
+    state = [7]
+    out = {}
+
+    def insert(key, shape, norm):
+        n = int(np.prod(shape))
+        vals = np.empty(n, np.float32)
+        s = state[0]
+        for j in range(n):
+            s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+            vals[j] = np.float32((s >> 8) / 16777216.0 - 0.5)
+        state[0] = s
+        out[key] = (np.float32(1.0) + vals / np.float32(8.0) if norm else vals / np.float32(math.sqrt(d))).reshape(shape)
+
+    insert("type_emb.weight", (3, d), False)
+    for i in range(n_layers):
+        p = f"head.layers.{i}."
+        for key, shape, norm in [
+            ("self_attn.in_proj_weight", (3 * d, d), False), ("self_attn.in_proj_bias", (3 * d,), False),
+            ("self_attn.out_proj.weight", (d, d), False), ("self_attn.out_proj.bias", (d,), False),
+            ("norm1.weight", (d,), True), ("norm1.bias", (d,), False),
+            ("norm2.weight", (d,), True), ("norm2.bias", (d,), False),
+            ("linear1.weight", (2 * d + 1, d), False), ("linear1.bias", (2 * d + 1,), False),
+            ("linear2.weight", (d, 2 * d + 1), False), ("linear2.bias", (d,), False)]:
+            insert(p + key, shape, norm)
+    for key, shape, norm in [
+        ("scorer.0.weight", (d,), True), ("scorer.0.bias", (d,), False),
+        ("scorer.1.weight", (d // 2 + 1, d), False), ("scorer.1.bias", (d // 2 + 1,), False),
+        ("scorer.3.weight", (1, d // 2 + 1), False), ("scorer.3.bias", (1,), False)]:
+        insert(key, shape, norm)
+    return out
