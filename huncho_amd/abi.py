@@ -72,6 +72,18 @@ class PrefillWork(C.Structure):
     _fields_ = [("forward_calls", C.c_uint64), ("processed_tokens", C.c_uint64), ("chunked_prefills", C.c_uint64)]
 
 
+class LayaHeadConfig(C.Structure):
+    _fields_ = [("d", I), ("n_layers", I), ("ffn", I), ("scorer_hidden", I), ("n_types", I)]
+
+
+LAYA_HEAD_LAYER_FIELDS = ["in_proj_w", "in_proj_b", "out_proj_w", "out_proj_b", "norm1_w", "norm1_b", "norm2_w",
+                          "norm2_b", "linear1_w", "linear1_b", "linear2_w", "linear2_b"]
+
+
+class LayaHeadLayerWeights(C.Structure):
+    _fields_ = [(n, vp) for n in LAYA_HEAD_LAYER_FIELDS]
+
+
 class BertLayerWeights(C.Structure):
     _fields_ = [(n, vp) for n in BERT_LAYER_FIELDS]
 
@@ -143,6 +155,11 @@ SIGNATURES = {
     "hk_bert_model_destroy": (I, [vp]),
     "hk_bert_workspace_size": (I, [vp, I, C.POINTER(SZ)]),
     "hk_bert_forward": (I, [vp, vp, vp, i32p, I, vp, SZ, vp, vp]),
+    "hk_laya_head_create": (I, [vp, I, C.POINTER(LayaHeadConfig), vp, C.POINTER(LayaHeadLayerWeights), vp, vp, vp, vp,
+                                vp, vp, C.POINTER(vp)]),
+    "hk_laya_head_destroy": (I, [vp]),
+    "hk_laya_head_workspace_size": (I, [vp, I, I, C.POINTER(SZ)]),
+    "hk_laya_head_forward": (I, [vp, vp, vp, i32p, I, i32p, vp, i32p, vp, i32p, vp, SZ, vp]),
     "hk_mean_pool_workspace_size": (I, [I, I, C.POINTER(SZ)]),
     "hk_mean_pool_head": (I, [vp, I, vp, L, vp, I, I, I, vp, vp, I, vp, vp, SZ]),
     "hk_mean_pool_head_noalloc": (I, [vp, I, vp, L, vp, I, I, I, vp, vp, I, vp]),

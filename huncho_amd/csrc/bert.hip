@@ -5,7 +5,7 @@
 //                      64, optional window |i - j| <= w (local layers), q/k/v read straight
 //                      from the fused Wqkv rows [tokens][3][heads][64]
 //   bidir_attn_f32     the same in fp32 (the reference's execution precision)
-//   layer_norm<T,VEC>  LayerNorm without bias, fp32 statistics
+//   layer_norm<T,VEC>  LayerNorm (ModernBERT's without bias; the Laya head's with), fp32 statistics
 //   geglu<T,VEC>       gelu(x1) * x2 with the exact erf GELU
 //   rope_qk<T,VEC>     NeoX rotate-half RoPE on the q and k parts of the Wqkv rows, in place
 //   mean_pool_partial<T>, mean_pool_head<T>
@@ -299,7 +299,7 @@ __device__ __forceinline__ float wave_sum(float s) {
     return s;
 }
 
-// LayerNorm without bias over rows of `width` (<= 2048): one wave per row, two passes over
+// LayerNorm (bias optional) over rows of `width` (<= 2048): one wave per row, two passes over
 // registers (mean, then the centred sum of squares), statistics in fp32. VEC: 16-byte loads
 // and stores (width a multiple of the vector, rows and weights 16-byte aligned).
 template <typename T, bool VEC>
@@ -348,12 +348,13 @@ __global__ __launch_bounds__(256) void layer_norm(LayerNormArgs a) {
 #pragma unroll
             for (int h = 0; h < N; h += 4) {
                 const f32x4 w = *(const f32x4*)(a.w + c * N + h);
+                const f32x4 bb = a.b ? *(const f32x4*)(a.b + c * N + h) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) t[h + e] = from_f<T>(((v[k][h + e] - mean) * inv) * w[e]);
+                for (int e = 0; e < 4; ++e) t[h + e] = from_f<T>(((v[k][h + e] - mean) * inv) * w[e] + bb[e]);
             }
             *(V*)(y + c * N) = t;
         } else {
-            y[c] = from_f<T>(((v[k][0] - mean) * inv) * a.w[c]);
+            y[c] = from_f<T>(((v[k][0] - mean) * inv) * a.w[c] + (a.b ? a.b[c] : 0.0f));
         }
     }
 }
@@ -554,7 +555,7 @@ extern "C" int hk_launch_layer_norm(int dtype, const hk::LayerNormArgs* a, hipSt
     if (a->rows == 0) return HK_OK;
     const int N = vec_elems(dtype);
     const bool vec = a->width % N == 0 && a->x_tok % N == 0 && a->y_tok % N == 0 && aligned16(a->x) &&
-                     aligned16(a->y) && aligned16(a->w);
+                     aligned16(a->y) && aligned16(a->w) && (!a->b || aligned16(a->b));
     HK_BERT_DISPATCH_VEC(dtype, vec, layer_norm, dim3((a->rows + 3) / 4), dim3(256), 0, stream, *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }

@@ -182,6 +182,46 @@ struct LayerNormArgs {
     int rows, width;
     void* y;
     long y_tok;
+    const float* b;  // bias [width] or null (ModernBERT's LayerNorms have none)
+};
+
+// typed Laya head (laya_head.hip)
+struct LayaTypeArgs {
+    const void* x;  // [rows][width] at x_tok
+    long x_tok;
+    const float* type_emb;  // [n_types][width]
+    const int* cu;          // [n_seqs + 1]
+    int n_seqs;
+    int qtype[64];          // per sequence
+    int rows, width;
+    void* y;
+    long y_tok;
+};
+struct LayaBiasArgs {
+    const void* x;
+    long x_tok;
+    const float* b;    // [width]
+    const void* res;   // residual rows or null
+    long res_tok;
+    int rows, width;
+    void* y;
+    long y_tok;
+};
+struct LayaGatherArgs {
+    const void* x;
+    long x_tok;
+    const int* cu;            // [n_seqs + 1] token rows
+    const int* cu_positions;  // [n_seqs + 1] into positions
+    const int* positions;     // relative to the sequence
+    int n_seqs, n_positions, width;
+    void* y;                  // [n_positions][width]
+};
+struct LayaScoreArgs {
+    const void* y;  // [n_positions][width]
+    const float* w;  // [width]
+    float b;
+    int n_positions, width;
+    float* out;
 };
 
 struct GegluArgs {
@@ -274,6 +314,10 @@ int hk_launch_lora_merge(int dtype, void* w, long rows, int cols, const float* a
                          hipStream_t st);
 int hk_launch_bidir_attention(int dtype, const hk::BertAttnArgs* a, int n_seqs, int max_len, hipStream_t stream);
 int hk_launch_layer_norm(int dtype, const hk::LayerNormArgs* a, hipStream_t stream);
+int hk_launch_laya_type_add(int dtype, const hk::LayaTypeArgs* a, hipStream_t stream);
+int hk_launch_laya_bias_act(int dtype, int act, const hk::LayaBiasArgs* a, hipStream_t stream);
+int hk_launch_laya_gather(int dtype, const hk::LayaGatherArgs* a, hipStream_t stream);
+int hk_launch_laya_score(int dtype, const hk::LayaScoreArgs* a, hipStream_t stream);
 int hk_launch_geglu(int dtype, const hk::GegluArgs* a, hipStream_t stream);
 int hk_launch_rope_qk(int dtype, const hk::RopeQkArgs* a, int n_seqs, int max_len, hipStream_t stream);
 int hk_launch_mean_pool_head(int dtype, const hk::MeanPoolArgs* a, int n_seqs, hipStream_t stream);

@@ -1,0 +1,275 @@
+// laya_head.cpp - the typed Laya decision head (LayaHead, crates/huncho-backend/src/
+// candle.rs:500-694) on the device, after the ModernBERT encoder:
+//   z = h + type_emb[qtype]
+//   per head layer (nn.TransformerEncoderLayer, norm_first, ReLU FFN; LayaLayer::forward 520-585):
+//     x = z + out_proj(attention(in_proj(LayerNorm1(z)))) ; z = x + linear2(relu(linear1(LayerNorm2(x))))
+//   scores = Linear_a->1(gelu_erf(Linear_d->a(LayerNorm(z[positions]))))
+// over an unpadded varlen batch of sequences (one qtype per sequence, readout positions per
+// sequence). Attention is the whole sequence (bidirectional), d / 64 heads of 64. The GEMMs run
+// on hipBLASLt with the bias, activation and residual in one elementwise pass each, every result
+// rounded to the activation dtype as the reference's tensors of that dtype store it. Weights are
+// held in the activation dtype (the reference's load-time conversion); biases, LayerNorm weights,
+// the type embedding and the last scorer row as fp32 copies of those rounded values. The FFN and
+// scorer widths are padded to multiples of 8 with zero rows / columns (exact: ReLU(0) =
+// GELU(0) = 0 and the padded columns of the next weight are zero).
+#include <string.h>
+
+#include <vector>
+
+#include "abi_internal.hpp"
+
+namespace {
+
+struct HeadLayer {
+    void *in_w = nullptr, *out_w = nullptr, *w1 = nullptr, *w2 = nullptr;
+    float *in_b = nullptr, *out_b = nullptr, *n1w = nullptr, *n1b = nullptr, *n2w = nullptr, *n2b = nullptr;
+    float *b1 = nullptr, *b2 = nullptr;
+};
+
+int pad8(int x) { return (x + 7) / 8 * 8; }
+
+}  // namespace
+
+struct hk_laya_head {
+    hk_ctx* ctx = nullptr;
+    int dtype = HK_BF16;
+    size_t esz = 2;
+    int d = 0, nhead = 0, n_types = 0, ffn = 0, ffn_pad = 0, a = 0, a_pad = 0;
+    std::vector<HeadLayer> layers;
+    std::vector<void*> owned;
+    float* type_emb = nullptr;
+    float *ln_w = nullptr, *ln_b = nullptr, *l1_b = nullptr, *l2_w = nullptr;
+    void* l1_w = nullptr;
+    float l2_b = 0.0f;
+};
+
+static int h_alloc(hk_laya_head* h, size_t bytes, void** out) {
+    if (hipMalloc(out, bytes) != hipSuccess) return hk_fail(h->ctx, HK_ERR_NOMEM, "head allocation of %zu bytes failed", bytes);
+    h->owned.push_back(*out);
+    return HK_OK;
+}
+
+// A device vector of n values of the activation dtype, as fp32 on the host
+static int read_vec(hk_laya_head* h, const void* src, size_t n, std::vector<float>& out) {
+    if (!src) return hk_fail(h->ctx, HK_ERR_INVALID, "missing head tensor");
+    out.resize(n);
+    if (h->dtype == HK_F32)
+        return hk_check_hip(h->ctx, hipMemcpy(out.data(), src, n * 4, hipMemcpyDeviceToHost), "head weight read");
+    std::vector<uint16_t> t(n);
+    if (int rc = hk_check_hip(h->ctx, hipMemcpy(t.data(), src, n * 2, hipMemcpyDeviceToHost), "head weight read")) return rc;
+    for (size_t i = 0; i < n; ++i) {
+        if (h->dtype == HK_F16) {
+            out[i] = hk_host_f16_to_f32(t[i]);
+        } else {
+            const uint32_t u = (uint32_t)t[i] << 16;
+            memcpy(&out[i], &u, 4);
+        }
+    }
+    return HK_OK;
+}
+
+// fp32 device copy of a device vector (n values; padded with zeros to n_pad)
+static int f32_vec(hk_laya_head* h, const void* src, size_t n, size_t n_pad, float** out) {
+    std::vector<float> v;
+    if (int rc = read_vec(h, src, n, v)) return rc;
+    v.resize(n_pad, 0.0f);
+    if (int rc = h_alloc(h, n_pad * 4, (void**)out)) return rc;
+    return hk_check_hip(h->ctx, hipMemcpy(*out, v.data(), n_pad * 4, hipMemcpyHostToDevice), "head weight upload");
+}
+
+// A [rows][cols] matrix of the activation dtype into [rows_pad][cols_pad], zero padded
+static int mat(hk_laya_head* h, const void* src, int rows, int cols, int rows_pad, int cols_pad, void** out) {
+    if (!src) return hk_fail(h->ctx, HK_ERR_INVALID, "missing head tensor");
+    const size_t e = h->esz;
+    if (int rc = h_alloc(h, (size_t)rows_pad * cols_pad * e, out)) return rc;
+    if (int rc = hk_check_hip(h->ctx, hipMemset(*out, 0, (size_t)rows_pad * cols_pad * e), "head weight clear")) return rc;
+    return hk_check_hip(h->ctx,
+                        hipMemcpy2D(*out, (size_t)cols_pad * e, src, (size_t)cols * e, (size_t)cols * e, rows,
+                                    hipMemcpyDeviceToDevice),
+                        "head weight copy");
+}
+
+extern "C" int hk_laya_head_destroy(hk_laya_head* h) {
+    if (!h) return HK_ERR_INVALID;
+    hipSetDevice(h->ctx->device);
+    hipStreamSynchronize(h->ctx->stream);
+    for (void* p : h->owned) hipFree(p);
+    delete h;
+    return HK_OK;
+}
+
+extern "C" int hk_laya_head_create(hk_ctx* ctx, int dtype, const hk_laya_head_config* cfg, const void* type_emb,
+                                   const hk_laya_head_layer_weights* layers, const void* scorer_ln_w,
+                                   const void* scorer_ln_b, const void* scorer_w1, const void* scorer_b1,
+                                   const void* scorer_w2, const void* scorer_b2, hk_laya_head** out) {
+    if (!ctx || !cfg || !layers || !out) return HK_ERR_INVALID;
+    if (dtype != HK_BF16 && dtype != HK_F16 && dtype != HK_F32) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "dtype %d", dtype);
+    if (cfg->d <= 0 || cfg->d % 64 != 0 || cfg->d > 2048)
+        return hk_fail(ctx, HK_ERR_UNSUPPORTED, "head width %d: a multiple of 64 up to 2048 (heads of 64)", cfg->d);
+    if (cfg->n_layers <= 0 || cfg->n_layers > 64 || cfg->ffn <= 0 || cfg->scorer_hidden <= 0 || cfg->n_types <= 0)
+        return hk_fail(ctx, HK_ERR_INVALID, "bad Laya head configuration");
+    hipSetDevice(ctx->device);
+    if (int rc = hk_blas_prepare(ctx)) return rc;
+    hk_laya_head* h = new hk_laya_head();
+    h->ctx = ctx;
+    h->dtype = dtype;
+    h->esz = dtype == HK_F32 ? 4 : 2;
+    h->d = cfg->d;
+    h->nhead = cfg->d / 64;
+    h->n_types = cfg->n_types;
+    h->ffn = cfg->ffn;
+    h->ffn_pad = pad8(cfg->ffn);
+    h->a = cfg->scorer_hidden;
+    h->a_pad = pad8(cfg->scorer_hidden);
+    const int d = h->d;
+    auto fail = [&](int rc) {
+        hk_laya_head_destroy(h);
+        return rc;
+    };
+    int rc = f32_vec(h, type_emb, (size_t)h->n_types * d, (size_t)h->n_types * d, &h->type_emb);
+    for (int i = 0; i < cfg->n_layers && !rc; ++i) {
+        const hk_laya_head_layer_weights& w = layers[i];
+        HeadLayer L;
+        if (!rc) rc = mat(h, w.in_proj_w, 3 * d, d, 3 * d, d, &L.in_w);
+        if (!rc) rc = f32_vec(h, w.in_proj_b, 3 * d, 3 * d, &L.in_b);
+        if (!rc) rc = mat(h, w.out_proj_w, d, d, d, d, &L.out_w);
+        if (!rc) rc = f32_vec(h, w.out_proj_b, d, d, &L.out_b);
+        if (!rc) rc = f32_vec(h, w.norm1_w, d, d, &L.n1w);
+        if (!rc) rc = f32_vec(h, w.norm1_b, d, d, &L.n1b);
+        if (!rc) rc = f32_vec(h, w.norm2_w, d, d, &L.n2w);
+        if (!rc) rc = f32_vec(h, w.norm2_b, d, d, &L.n2b);
+        if (!rc) rc = mat(h, w.linear1_w, h->ffn, d, h->ffn_pad, d, &L.w1);
+        if (!rc) rc = f32_vec(h, w.linear1_b, h->ffn, h->ffn_pad, &L.b1);
+        if (!rc) rc = mat(h, w.linear2_w, d, h->ffn, d, h->ffn_pad, &L.w2);
+        if (!rc) rc = f32_vec(h, w.linear2_b, d, d, &L.b2);
+        h->layers.push_back(L);
+    }
+    if (!rc) rc = f32_vec(h, scorer_ln_w, d, d, &h->ln_w);
+    if (!rc) rc = f32_vec(h, scorer_ln_b, d, d, &h->ln_b);
+    if (!rc) rc = mat(h, scorer_w1, h->a, d, h->a_pad, d, &h->l1_w);
+    if (!rc) rc = f32_vec(h, scorer_b1, h->a, h->a_pad, &h->l1_b);
+    if (!rc) rc = f32_vec(h, scorer_w2, h->a, h->a_pad, &h->l2_w);
+    if (!rc) {
+        std::vector<float> b2;
+        rc = read_vec(h, scorer_b2, 1, b2);
+        if (!rc) h->l2_b = b2[0];
+    }
+    if (rc) return fail(rc);
+    *out = h;
+    return HK_OK;
+}
+
+// Workspace layout (256-byte aligned pieces): z, x, xn, att [n][d]; qkv [n][3 d]; ff [n][ffn_pad];
+// m, mn [P][d]; y1 [P][a_pad]
+static size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
+static size_t head_ws(const hk_laya_head* h, int n, int P) {
+    const size_t e = h->esz;
+    return 4 * al((size_t)n * h->d * e) + al((size_t)n * 3 * h->d * e) + al((size_t)n * h->ffn_pad * e) +
+           2 * al((size_t)P * h->d * e) + al((size_t)P * h->a_pad * e);
+}
+
+extern "C" int hk_laya_head_workspace_size(hk_laya_head* h, int n_tokens, int n_positions, size_t* bytes_out) {
+    if (!h || !bytes_out || n_tokens < 0 || n_positions < 0) return HK_ERR_INVALID;
+    *bytes_out = head_ws(h, n_tokens, n_positions);
+    return HK_OK;
+}
+
+extern "C" int hk_laya_head_forward(hk_laya_head* h, const void* hidden, const int32_t* cu_dev, const int32_t* cu_host,
+                                    int n_seqs, const int32_t* qtype_host, const int32_t* cu_positions_dev,
+                                    const int32_t* cu_positions_host, const int32_t* positions_dev,
+                                    const int32_t* positions_host, void* workspace, size_t workspace_bytes,
+                                    float* scores_dev) {
+    if (!h) return HK_ERR_INVALID;
+    hk_ctx* ctx = h->ctx;
+    if (!hidden || !cu_dev || !cu_host || !qtype_host || !cu_positions_dev || !cu_positions_host || !positions_dev ||
+        !positions_host || !workspace || !scores_dev || n_seqs <= 0 || n_seqs > 64)
+        return hk_fail(ctx, HK_ERR_INVALID, "invalid Laya head arguments (1..64 sequences)");
+    if (cu_host[0] != 0 || cu_positions_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "cu arrays must start at 0");
+    // validate every sequence before any work (candle.rs:319-335)
+    int max_len = 0;
+    for (int s = 0; s < n_seqs; ++s) {
+        const int len = cu_host[s + 1] - cu_host[s];
+        if (len <= 0) return hk_fail(ctx, HK_ERR_INVALID, "sequence %d is empty", s);
+        if (len > max_len) max_len = len;
+        if (qtype_host[s] < 0 || qtype_host[s] >= h->n_types)
+            return hk_fail(ctx, HK_ERR_INVALID, "qtype %d of sequence %d outside 0..%d", qtype_host[s], s, h->n_types - 1);
+        if (cu_positions_host[s + 1] < cu_positions_host[s])
+            return hk_fail(ctx, HK_ERR_INVALID, "cu_positions must not decrease");
+        for (int p = cu_positions_host[s]; p < cu_positions_host[s + 1]; ++p)
+            if (positions_host[p] < 0 || positions_host[p] >= len)
+                return hk_fail(ctx, HK_ERR_INVALID, "position %d outside sequence %d (%d tokens)", positions_host[p], s, len);
+    }
+    const int n = cu_host[n_seqs], P = cu_positions_host[n_seqs], d = h->d;
+    if (head_ws(h, n, P) > workspace_bytes)
+        return hk_fail(ctx, HK_ERR_INVALID, "workspace too small: %zu < %zu", workspace_bytes, head_ws(h, n, P));
+    if (P == 0) return HK_OK;
+    hipSetDevice(ctx->device);
+    const int dt = h->dtype;
+    const size_t e = h->esz;
+    char* w = (char*)workspace;
+    auto take = [&](size_t bytes) {
+        char* p = w;
+        w += al(bytes);
+        return (void*)p;
+    };
+    void* z = take((size_t)n * d * e);
+    void* x = take((size_t)n * d * e);
+    void* xn = take((size_t)n * d * e);
+    void* att = take((size_t)n * d * e);
+    void* qkv = take((size_t)n * 3 * d * e);
+    void* ff = take((size_t)n * h->ffn_pad * e);
+    void* m = take((size_t)P * d * e);
+    void* mn = take((size_t)P * d * e);
+    void* y1 = take((size_t)P * h->a_pad * e);
+#define HRUN(expr)                  \
+    do {                            \
+        if (int rc_ = (expr)) return rc_; \
+    } while (0)
+    auto launch = [&](int rc, const char* what) { return rc ? hk_fail(ctx, rc, "%s launch failed", what) : HK_OK; };
+    auto bias = [&](int act, const void* src, long src_tok, const float* b, const void* res, void* dst, int rows, int width) {
+        hk::LayaBiasArgs ba{src, src_tok, b, res, (long)width, rows, width, dst, (long)width};
+        return launch(hk_launch_laya_bias_act(dt, act, &ba, ctx->stream), "bias");
+    };
+    auto norm = [&](const void* src, const float* nw, const float* nb, void* dst, int rows) {
+        hk::LayerNormArgs la{src, (long)d, nw, 1e-5f, rows, d, dst, (long)d, nb};
+        return launch(hk_launch_layer_norm(dt, &la, ctx->stream), "layer norm");
+    };
+    // z = h + type_emb[qtype]
+    hk::LayaTypeArgs ta{};
+    ta.x = hidden;
+    ta.x_tok = d;
+    ta.type_emb = h->type_emb;
+    ta.cu = cu_dev;
+    ta.n_seqs = n_seqs;
+    for (int s = 0; s < n_seqs; ++s) ta.qtype[s] = qtype_host[s];
+    ta.rows = n;
+    ta.width = d;
+    ta.y = z;
+    ta.y_tok = d;
+    HRUN(launch(hk_launch_laya_type_add(dt, &ta, ctx->stream), "type add"));
+    const float scale = 0.125f;  // head_dim 64
+    for (const HeadLayer& L : h->layers) {
+        HRUN(norm(z, L.n1w, L.n1b, xn, n));
+        HRUN(hk_gemm_xwt(ctx, dt, n, 3 * d, d, xn, d, L.in_w, d, qkv, 3 * d, nullptr, 0, 1.0f, 0.0f));
+        HRUN(bias(0, qkv, 3 * d, L.in_b, nullptr, qkv, n, 3 * d));
+        char* q = (char*)qkv;
+        HRUN(hk_bidir_attention(ctx, dt, q, 3 * d, q + (size_t)d * e, 3 * d, q + (size_t)2 * d * e, 3 * d, cu_dev, n_seqs,
+                                n, max_len, h->nhead, 64, -1, scale, att, d));
+        HRUN(hk_gemm_xwt(ctx, dt, n, d, d, att, d, L.out_w, d, xn, d, nullptr, 0, 1.0f, 0.0f));
+        HRUN(bias(0, xn, d, L.out_b, z, x, n, d));  // x = z + (out + b)
+        HRUN(norm(x, L.n2w, L.n2b, xn, n));
+        HRUN(hk_gemm_xwt(ctx, dt, n, h->ffn_pad, d, xn, d, L.w1, d, ff, h->ffn_pad, nullptr, 0, 1.0f, 0.0f));
+        HRUN(bias(1, ff, h->ffn_pad, L.b1, nullptr, ff, n, h->ffn_pad));
+        HRUN(hk_gemm_xwt(ctx, dt, n, d, h->ffn_pad, ff, h->ffn_pad, L.w2, h->ffn_pad, att, d, nullptr, 0, 1.0f, 0.0f));
+        HRUN(bias(0, att, d, L.b2, x, z, n, d));  // z = x + (ff2 + b)
+    }
+    hk::LayaGatherArgs ga{z, (long)d, cu_dev, cu_positions_dev, positions_dev, n_seqs, P, d, m};
+    HRUN(launch(hk_launch_laya_gather(dt, &ga, ctx->stream), "gather"));
+    HRUN(norm(m, h->ln_w, h->ln_b, mn, P));
+    HRUN(hk_gemm_xwt(ctx, dt, P, h->a_pad, d, mn, d, h->l1_w, d, y1, h->a_pad, nullptr, 0, 1.0f, 0.0f));
+    HRUN(bias(2, y1, h->a_pad, h->l1_b, nullptr, y1, P, h->a_pad));
+    hk::LayaScoreArgs sa{y1, h->l2_w, h->l2_b, P, h->a_pad, scores_dev};
+    HRUN(launch(hk_launch_laya_score(dt, &sa, ctx->stream), "score"));
+#undef HRUN
+    return HK_OK;
+}

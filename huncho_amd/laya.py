@@ -192,3 +192,88 @@ class LayaModel:
             cu = batch["cu_host"]
             hs = [h[cu[i]:cu[i + 1]] for i in range(len(rows))]
         return logits, hs
+
+
+# the checkpoint names of a head layer's tensors (candle.rs:611-636), by hk_laya_head_layer_weights field
+_HEAD_FIELD = {"in_proj_w": "self_attn.in_proj_weight", "in_proj_b": "self_attn.in_proj_bias",
+               "out_proj_w": "self_attn.out_proj.weight", "out_proj_b": "self_attn.out_proj.bias",
+               "norm1_w": "norm1.weight", "norm1_b": "norm1.bias", "norm2_w": "norm2.weight", "norm2_b": "norm2.bias",
+               "linear1_w": "linear1.weight", "linear1_b": "linear1.bias", "linear2_w": "linear2.weight",
+               "linear2_b": "linear2.bias"}
+
+
+class LayaHead:
+    """hk_laya_head: the typed Laya decision head (LayaHead::from_tensors / forward, candle.rs:596-694)
+    from the checkpoint's `type_emb.weight`, `head.layers.{i}.*` and `scorer.*` tensors."""
+
+    def __init__(self, ctx: abi.Context, tensors: dict, dtype: torch.dtype = torch.bfloat16, device=0):
+        if "type_emb.weight" not in tensors:
+            raise ValueError("no Laya head in these tensors (`type_emb.weight` missing)")
+        self.ctx, self.dtype = ctx, dtype
+        self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        self.hk_dtype = {torch.bfloat16: HK_BF16, torch.float16: HK_F16, torch.float32: HK_F32}[dtype]
+        staged = {k: _to_device(v, dtype, self.device) for k, v in tensors.items()
+                  if k == "type_emb.weight" or k.startswith(("head.layers.", "scorer."))}
+        n_layers = 0
+        while f"head.layers.{n_layers}.self_attn.in_proj_weight" in staged:
+            n_layers += 1
+        if n_layers == 0:
+            raise ValueError("checkpoint has a Laya head (`type_emb.weight`) but no head layers")
+        te = staged["type_emb.weight"]
+        self.d = te.shape[1]
+        cfg = abi.LayaHeadConfig(self.d, n_layers, staged["head.layers.0.linear1.weight"].shape[0],
+                                 staged["scorer.1.weight"].shape[0], te.shape[0])
+        layers = (abi.LayaHeadLayerWeights * n_layers)()
+        for i in range(n_layers):
+            for f, suffix in _HEAD_FIELD.items():
+                t = staged.get(f"head.layers.{i}.{suffix}")
+                if t is None:
+                    raise ValueError(f"Laya head tensors missing `head.layers.{i}.{suffix}`")
+                setattr(layers[i], f, t.data_ptr())
+        h = C.c_void_p()
+        torch.cuda.synchronize(self.device)
+        ctx.check(abi.lib().hk_laya_head_create(
+            ctx.h, self.hk_dtype, C.byref(cfg), te.data_ptr(), layers, staged["scorer.0.weight"].data_ptr(),
+            staged["scorer.0.bias"].data_ptr(), staged["scorer.1.weight"].data_ptr(), staged["scorer.1.bias"].data_ptr(),
+            staged["scorer.3.weight"].data_ptr(), staged["scorer.3.bias"].data_ptr(), C.byref(h)))
+        self.h = h
+        del staged
+        self._ws = None
+
+    def close(self):
+        if self.h:
+            abi.lib().hk_laya_head_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward(self, hidden_rows, qtypes, positions):
+        """hidden_rows: per sequence [len, d] (numpy or device tensors of the head dtype); qtypes: one
+        per sequence; positions[s]: indices into sequence s. Returns one fp32 score array per sequence."""
+        dev = self.device
+        rows = [torch.as_tensor(np.asarray(r, np.float32) if not torch.is_tensor(r) else r) for r in hidden_rows]
+        hidden = torch.cat([r.to(dev).to(self.dtype) for r in rows]).contiguous()
+        lengths = [r.shape[0] for r in rows]
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        cp = np.concatenate([[0], np.cumsum([len(p) for p in positions])]).astype(np.int32)
+        pos = np.concatenate([np.asarray(p, np.int32) for p in positions]).astype(np.int32) if cp[-1] else np.zeros(1, np.int32)
+        qt = np.asarray(qtypes, np.int32)
+        sz = C.c_size_t()
+        self.ctx.check(abi.lib().hk_laya_head_workspace_size(self.h, int(cu[-1]), int(cp[-1]), C.byref(sz)))
+        if self._ws is None or self._ws.numel() < sz.value:
+            self._ws = torch.empty(max(sz.value, 1), dtype=torch.uint8, device=dev)
+        cu_d, cp_d, pos_d = (torch.from_numpy(a).to(dev) for a in (cu, cp, pos))
+        scores = torch.empty(max(int(cp[-1]), 1), dtype=torch.float32, device=dev)
+        P = lambda a: a.ctypes.data_as(C.POINTER(C.c_int32))
+        self.ctx.check(abi.lib().hk_laya_head_forward(
+            self.h, hidden.data_ptr(), cu_d.data_ptr(), P(cu), len(rows), P(qt), cp_d.data_ptr(), P(cp),
+            pos_d.data_ptr(), P(pos), self._ws.data_ptr(), self._ws.numel(), scores.data_ptr()))
+        out = scores.cpu().numpy()[: int(cp[-1])]
+        faults = self.ctx.take_faults()
+        if faults:
+            raise RuntimeError(f"device faults 0x{faults:x} during the Laya head")
+        return [out[cp[i]:cp[i + 1]] for i in range(len(rows))]

@@ -440,6 +440,44 @@ int hk_bert_forward(hk_bert_model* m, const int32_t* ids_dev, const int32_t* cu_
                     const int32_t* cu_seqlens_host, int n_seqs, void* workspace_dev, size_t workspace_bytes,
                     float* logits_dev, void* hidden_out_dev);
 
+/* ---- the typed Laya decision head (LayaHead, candle.rs:500-694; built from the checkpoint's
+ * `type_emb.weight`, `head.layers.{i}.*` and `scorer.*` tensors, candle.rs:596-649) -------------
+ * z = hidden + type_emb[qtype]; each head layer is a pre-norm nn.TransformerEncoderLayer
+ * (LayerNorm eps 1e-5 with bias; in_proj q|k|v with bias; d / 64 heads of 64 over the whole
+ * sequence; out_proj with bias; residual; LayerNorm; linear1 + ReLU; linear2; residual;
+ * LayaLayer::forward 520-585); the rows at the readout positions then go through the scorer
+ * LayerNorm -> Linear(d -> a) -> GELU (erf) -> Linear(a -> 1) (660-694). */
+typedef struct hk_laya_head_config {
+    int d;              /* encoder width, a multiple of 64 up to 2048 */
+    int n_layers;       /* head layers (the reference fixture: 2) */
+    int ffn;            /* linear1 rows */
+    int scorer_hidden;  /* scorer.1 rows */
+    int n_types;        /* type_emb rows */
+} hk_laya_head_config;
+/* Device pointers in the model dtype; weights row-major [out][in], as in the checkpoint. */
+typedef struct hk_laya_head_layer_weights {
+    const void *in_proj_w, *in_proj_b, *out_proj_w, *out_proj_b;
+    const void *norm1_w, *norm1_b, *norm2_w, *norm2_b;
+    const void *linear1_w, *linear1_b, *linear2_w, *linear2_b;
+} hk_laya_head_layer_weights;
+typedef struct hk_laya_head hk_laya_head;
+/* Copies the head (the caller's buffers may be freed after). */
+int hk_laya_head_create(hk_ctx* ctx, int dtype, const hk_laya_head_config* cfg, const void* type_emb_dev,
+                        const hk_laya_head_layer_weights* layers_host, const void* scorer_ln_w_dev,
+                        const void* scorer_ln_b_dev, const void* scorer_w1_dev, const void* scorer_b1_dev,
+                        const void* scorer_w2_dev, const void* scorer_b2_dev, hk_laya_head** out);
+int hk_laya_head_destroy(hk_laya_head* h);
+int hk_laya_head_workspace_size(hk_laya_head* h, int n_tokens, int n_positions, size_t* bytes_out);
+/* LayaHead::forward for each sequence of an unpadded varlen batch (1..64 sequences): hidden
+ * [n_tokens][d] (the encoder's final-normed rows, model dtype), qtype per sequence,
+ * positions[cu_positions[s] .. cu_positions[s + 1]) relative to sequence s (host and device
+ * copies). Writes one fp32 score per position (the reference's [n, 1] output). */
+int hk_laya_head_forward(hk_laya_head* h, const void* hidden_dev, const int32_t* cu_seqlens_dev,
+                         const int32_t* cu_seqlens_host, int n_seqs, const int32_t* qtype_host,
+                         const int32_t* cu_positions_dev, const int32_t* cu_positions_host,
+                         const int32_t* positions_dev, const int32_t* positions_host, void* workspace_dev,
+                         size_t workspace_bytes, float* scores_dev);
+
 /* Mean-pooled linear head of the encoder workload over un-padded hidden rows (candle.rs:399-414
  * hands each row's own tokens to the readout; this head pools them): logits[s][o] = head_b[o] +
  * head_w[o] . mean of rows cu[s] .. cu[s + 1] - 1 of x, in fp32, each row's sum taken as up to

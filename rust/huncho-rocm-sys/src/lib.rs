@@ -130,6 +130,37 @@ pub struct hk_kev_readout {
 
 #[repr(C)]
 #[derive(Default, Clone, Copy)]
+pub struct hk_laya_head_config {
+    pub d: c_int,
+    pub n_layers: c_int,
+    pub ffn: c_int,
+    pub scorer_hidden: c_int,
+    pub n_types: c_int,
+}
+
+#[repr(C)]
+pub struct hk_laya_head_layer_weights {
+    pub in_proj_w: *const c_void,
+    pub in_proj_b: *const c_void,
+    pub out_proj_w: *const c_void,
+    pub out_proj_b: *const c_void,
+    pub norm1_w: *const c_void,
+    pub norm1_b: *const c_void,
+    pub norm2_w: *const c_void,
+    pub norm2_b: *const c_void,
+    pub linear1_w: *const c_void,
+    pub linear1_b: *const c_void,
+    pub linear2_w: *const c_void,
+    pub linear2_b: *const c_void,
+}
+
+#[repr(C)]
+pub struct hk_laya_head {
+    _private: [u8; 0],
+}
+
+#[repr(C)]
+#[derive(Default, Clone, Copy)]
 pub struct hk_prefill_work {
     pub forward_calls: u64,
     pub processed_tokens: u64,
@@ -330,6 +361,22 @@ extern "C" {
     pub fn hk_kev_cache_clear_prefixes(c: *mut hk_kev_cache) -> c_int;
     pub fn hk_kev_cache_prefix_stats(
         c: *mut hk_kev_cache, count_out: *mut c_int, bytes_out: *mut usize
+    ) -> c_int;
+    pub fn hk_laya_head_create(
+        ctx: *mut hk_ctx, dtype: c_int, cfg: *const hk_laya_head_config, type_emb_dev: *const c_void,
+        layers_host: *const hk_laya_head_layer_weights, scorer_ln_w_dev: *const c_void,
+        scorer_ln_b_dev: *const c_void, scorer_w1_dev: *const c_void, scorer_b1_dev: *const c_void,
+        scorer_w2_dev: *const c_void, scorer_b2_dev: *const c_void, out: *mut *mut hk_laya_head
+    ) -> c_int;
+    pub fn hk_laya_head_destroy(h: *mut hk_laya_head) -> c_int;
+    pub fn hk_laya_head_workspace_size(
+        h: *mut hk_laya_head, n_tokens: c_int, n_positions: c_int, bytes_out: *mut usize
+    ) -> c_int;
+    pub fn hk_laya_head_forward(
+        h: *mut hk_laya_head, hidden_dev: *const c_void, cu_seqlens_dev: *const i32,
+        cu_seqlens_host: *const i32, n_seqs: c_int, qtype_host: *const i32, cu_positions_dev: *const i32,
+        cu_positions_host: *const i32, positions_dev: *const i32, positions_host: *const i32,
+        workspace_dev: *mut c_void, workspace_bytes: usize, scores_dev: *mut f32
     ) -> c_int;
     pub fn hk_layer_norm(
         ctx: *mut hk_ctx, dtype: c_int, x_dev: *const c_void, x_tok: c_long, w_dev: *const f32,

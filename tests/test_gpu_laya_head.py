@@ -1,0 +1,127 @@
+"""The typed Laya decision head on the GPU (hk_laya_head) against the oracle (oracle.laya_head,
+itself pinned against torch's TransformerEncoderLayer in test_laya_head_oracle.py).
+
+* the reference's own test head and input (crates/huncho-backend/tests/support/laya.rs:5-52,
+  candle.rs:722-757: d 128, 2 layers, linear1 2 d + 1 rows, scorer d / 2 + 1), every qtype, the
+  reference's position lists, and a varlen batch of three sequences in one call; fp32 within 1e-4
+  of the oracle (relative to the largest score), fp16 within 5e-3 and bf16 within 5e-2 of the
+  oracle's fp32 flow;
+* a ModernBERT-base-wide head (d 768, 12 heads, linear1 2048, scorer 385) on two sequences of
+  about 300 tokens, seeded weights, the same gates;
+* bad qtypes, positions and empty sequences are rejected before any work.
+"""
+import numpy as np
+import pytest
+import torch
+
+from huncho_amd import abi
+from huncho_amd.laya import LayaHead
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GATE = {torch.float32: 1e-4, torch.float16: 5e-3, torch.bfloat16: 5e-2}
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from huncho_amd.ops import context_for_torch
+
+    c = context_for_torch(0)
+    yield c
+    c.close()
+
+
+def ref_input(n, d, salt=0):
+    return np.array([(((i + salt) * 17 % 239) - 119) / 128 for i in range(n * d)], np.float32).reshape(n, d)
+
+
+def rel(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def test_head():
+    return O.laya_test_head(128, 2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_reference_head_every_qtype(ctx, test_head, dtype):
+    head = LayaHead(ctx, test_head, dtype)
+    h = ref_input(33, 128)
+    hd = O.round_bf16(h) if dtype == torch.bfloat16 else h  # the head reads the encoder rows in its dtype
+    worst = 0.0
+    for qtype in range(3):
+        for positions in ([32, 0, 9, 0], list(range(32, -1, -1))):
+            got = head.forward([h], [qtype], [positions])[0]
+            want = O.laya_head(hd.astype(np.float32) if dtype != torch.float16 else h, test_head, qtype, positions)
+            worst = max(worst, rel(got, want))
+    head.close()
+    print(f"reference test head, {dtype}: worst relative error {worst:.2e}")
+    assert worst < GATE[dtype], worst
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_varlen_batch_in_one_call(ctx, test_head, dtype):
+    head = LayaHead(ctx, test_head, dtype)
+    rows = [ref_input(33, 128), ref_input(17, 128, 5), ref_input(50, 128, 11)]
+    qtypes = [2, 0, 1]
+    positions = [[0, 32], [16, 3, 3], list(range(0, 50, 7))]
+    got = head.forward(rows, qtypes, positions)
+    head.close()
+    for r, q, p, g in zip(rows, qtypes, positions, got):
+        want = O.laya_head(O.round_bf16(r) if dtype == torch.bfloat16 else r, test_head, q, p)
+        e = rel(g, want)
+        assert e < GATE[dtype], e
+
+
+def wide_head(seed=5):
+    d, ffn, a = 768, 2048, 385
+    rng = np.random.default_rng(seed)
+    w = {"type_emb.weight": rng.normal(0, 0.02, (3, d))}
+    for i in range(2):
+        p = f"head.layers.{i}."
+        for k, shape, norm in [("self_attn.in_proj_weight", (3 * d, d), False), ("self_attn.in_proj_bias", (3 * d,), False),
+                               ("self_attn.out_proj.weight", (d, d), False), ("self_attn.out_proj.bias", (d,), False),
+                               ("norm1.weight", (d,), True), ("norm1.bias", (d,), False),
+                               ("norm2.weight", (d,), True), ("norm2.bias", (d,), False),
+                               ("linear1.weight", (ffn, d), False), ("linear1.bias", (ffn,), False),
+                               ("linear2.weight", (d, ffn), False), ("linear2.bias", (d,), False)]:
+            w[p + k] = 1.0 + rng.normal(0, 0.05, shape) if norm else rng.normal(0, 1.0 / np.sqrt(shape[-1]), shape)
+    w.update({"scorer.0.weight": 1.0 + rng.normal(0, 0.05, (d,)), "scorer.0.bias": rng.normal(0, 0.02, (d,)),
+              "scorer.1.weight": rng.normal(0, 1 / np.sqrt(d), (a, d)), "scorer.1.bias": rng.normal(0, 0.02, (a,)),
+              "scorer.3.weight": rng.normal(0, 1 / np.sqrt(a), (1, a)), "scorer.3.bias": rng.normal(0, 0.02, (1,))})
+    return {k: np.asarray(v, np.float32) for k, v in w.items()}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_modernbert_base_wide_head(ctx, dtype):
+    w = wide_head()
+    if dtype == torch.bfloat16:
+        w = {k: O.round_bf16(v) for k, v in w.items()}  # the checkpoint's bf16 tensors
+    head = LayaHead(ctx, w, dtype)
+    rng = np.random.default_rng(9)
+    rows = [rng.normal(0, 1, (297, 768)).astype(np.float32), rng.normal(0, 1, (311, 768)).astype(np.float32)]
+    if dtype == torch.bfloat16:
+        rows = [O.round_bf16(r) for r in rows]
+    positions = [[0, 100, 296], [310, 5]]
+    got = head.forward(rows, [1, 2], positions)
+    head.close()
+    for r, q, p, g in zip(rows, [1, 2], positions, got):
+        want = O.laya_head(r, w, q, p)
+        e = rel(g, want)
+        print(f"d 768 head, {dtype}: relative error {e:.2e}")
+        assert e < GATE[dtype], e
+
+
+def test_rejects_bad_inputs(ctx, test_head):
+    head = LayaHead(ctx, test_head, torch.float32)
+    h = ref_input(10, 128)
+    with pytest.raises(abi.HkError):
+        head.forward([h], [3], [[0]])  # qtype outside 0..2
+    with pytest.raises(abi.HkError):
+        head.forward([h], [0], [[10]])  # position past the sequence
+    with pytest.raises(abi.HkError):
+        head.forward([h, h[:0]], [0, 0], [[0], []])  # empty sequence
+    assert ctx.take_faults() == 0
+    head.close()
