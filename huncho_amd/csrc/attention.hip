@@ -14,7 +14,7 @@
 //   * a workgroup runs q-blocks (n - 1 - z, z) of its sequence back to back on one tile
 //     pipeline, so every workgroup of a sequence does the same n + 1 tiles;
 //   * 4 waves x 32 query rows; S^T = K Q^T on MFMA so that each lane owns one query
-//     column and the softmax row statistics stay in-lane (one lane-swap per tile);
+//     column and the softmax row statistics stay in-lane (one v_permlane32_swap per 32 keys);
 //   * K rows are read into the MFMA A operand in a permuted order so that each lane's
 //     accumulator holds 16 consecutive keys; P then feeds P.V directly as the B operand;
 //   * K and V tiles sit row-major in double-buffered LDS with an XOR chunk swizzle; the V^T
@@ -25,6 +25,7 @@
 // Grid = (kv_heads, q-block pairs, sequences): the pairs of one (sequence, KV head) are
 // consecutive in dispatch order on one XCD and share its L2 copy of the K/V pages.
 // The fp32 kernel keeps one workgroup per q-block, grid (kv_heads, sequences, q-blocks).
+#include <type_traits>
 #include "common.hpp"
 #include "kernel_args.hpp"
 
@@ -37,6 +38,14 @@ constexpr int V_STRIDE_F32 = D + 4;
 
 // Key row loaded by accumulator row m so that lane group g, element j sees key g*16 + j.
 __device__ __forceinline__ int perm_key(int m) { return ((m >> 2) & 1) * 16 + (m >> 3) * 4 + (m & 3); }
+
+// max of lane l and lane l ^ 32: v_permlane32_swap (gfx950) of a value with itself gives the low
+// half's values in one result and the high half's in the other, in every lane
+__device__ __forceinline__ float swap_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
@@ -266,116 +275,142 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attn_16(AttnArgs a) {
         l_run = 0.0f;
     };
 
-    // one 64-key tile of the schedule: start the copies of the next tile (and the table read
-    // after it), S^T, online softmax, O^T += V^T P^T, wait for the copies, barrier
-    auto step = [&](int i) {
-        const int buf = i & 1;
-        if (i + 1 < n_sched) {  // the other buffer was last read in step i - 1
-            resolve();
-            load_tile(sched_tile(i + 1), buf ^ 1);
-            if (i + 2 < n_sched) lookup(sched_tile(i + 2));
+    // Softmax pieces of one 32-key half (accumulator s, keys n0h ..): the causal mask (MASK:
+    // only tiles that reach past the block's first query), the raw-score max of the half-wave
+    // pair, and the lazy rescale when the max grew.
+    auto half_max = [&](f32x16& sv, int n0h, auto mask_c) {
+        constexpr bool MASK = decltype(mask_c)::value;
+        float mloc = -INFINITY;
+        if (MASK && n0h + 31 > first_pos) {
+            const int lim = qpos - n0h - g * 16;  // key offset j is visible iff j <= lim
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                if (j > lim) sv[j] = -INFINITY;
+                mloc = fmaxf(mloc, sv[j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, sv[j]);
         }
+        return swap_max(mloc);
+    };
+    auto rescale = [&](float m_half) {
+        const bool grow = (m_half - m_use) * c > RESCALE_LOG2;
+        if (__any(grow)) {
+            const float m_new = grow ? m_half : m_use;
+            // lanes that keep their max keep their sums (alpha 1; also avoids -inf - -inf)
+            const float alpha = grow ? fast_exp2((m_use - m_new) * c) : 1.0f;
+            m_use = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc_o[db][j] *= alpha;
+        }
+    };
+    // probabilities of one half as the P.V operand (rounded to T), and their row sums
+    auto half_p = [&](const f32x16& sv, v8* pf) {
+        const float mc = m_use * c;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            v8 t;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) t[k] = (T)fast_exp2(fmaf(sv[h * 8 + k], c, -mc));
+            pf[h] = t;
+        }
+        const v2 one2 = {(T)1.0f, (T)1.0f};
+        float l0 = 0.0f, l1 = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int q = 0; q < 8; q += 4) {
+                l0 = dot2(v2{pf[h][q], pf[h][q + 1]}, one2, l0);
+                l1 = dot2(v2{pf[h][q + 2], pf[h][q + 3]}, one2, l1);
+            }
+        l_run += l0 + l1;
+    };
+    // O^T += V^T P^T for keys kb*32 + g*16 + h*8 + [0..7], dims db*32 + [0..31]
+    auto pv = [&](const T* Vb, int kb, int h, const v8& p) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const T* vb = Vb + vofs[db];
+            const i16x4 lo = lds_read_tr16(vb + (kb * 32 + h * 8) * KV_ROW);
+            const i16x4 hi = lds_read_tr16(vb + (kb * 32 + h * 8 + 4) * KV_ROW);
+            const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            acc_o[db] = Mma16<T>::mma(af, p, acc_o[db]);
+        }
+    };
+
+    // One 64-key tile of the schedule, ordered so that each wave has independent MFMA and
+    // VALU work side by side: the copies of the next tile and the max of half 0 beside the
+    // S^T MFMAs, the probabilities of half 0 beside the rest of half 1's S^T, the max of half 1
+    // beside half 0's P.V, and the probabilities of half 1 beside its own P.V. The copies are
+    // unconditional (the last step copies its own tile again into the free buffer) so that they
+    // share the MFMAs' basic block; the table entry of a tile is read one step before its copies.
+    auto step = [&](int i, auto mask_c) {
+        const int buf = i & 1;
         const T* Kb = lds + buf * 2 * TILE_ELEMS;
         const T* Vb = Kb + TILE_ELEMS;
-
-        // S^T = K Q^T for this wave's 32 queries: two 32-key halves. Each half then takes its
-        // own online-softmax step, so the softmax of half 0 can run while the MFMAs of half 1
-        // execute, and the softmax of half 1 while the P.V of half 0 executes.
-        // (the two accumulation chains alternate, so consecutive MFMAs are independent)
-        f32x16 s[2] = {f32x16{}, f32x16{}};
+        // the first K fragments are read before the copies are issued (the copies' inline
+        // assembly orders every LDS access around it), so their latency overlaps the copies
+        v8 kf[4];
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-                s[kb] = Mma16<T>::mma(*(const v8*)(Kb + kb * 32 * KV_ROW + koff[ks]), qf[ks], s[kb]);
+        for (int ks = 0; ks < 4; ++ks) kf[ks] = *(const v8*)(Kb + koff[ks]);
+        resolve();
+        load_tile(sched_tile(min(i + 1, n_sched - 1)), buf ^ 1);
+        lookup(sched_tile(min(i + 2, n_sched - 1)));
         const int n0 = sched_tile(i) * BN;
+        f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            // causal mask (only halves that reach past the block's first query), raw-score max
-            float mloc = -INFINITY;
-            if (n0 + kb * 32 + 31 > first_pos) {
-                const int lim = qpos - n0 - kb * 32 - g * 16;  // key offset j is visible iff j <= lim
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    if (j > lim) s[kb][j] = -INFINITY;
-                    mloc = fmaxf(mloc, s[kb][j]);
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, s[kb][j]);
-            }
-            const float m_half = wave_max32(mloc);
-            const bool grow = (m_half - m_use) * c > RESCALE_LOG2;
-            if (__any(grow)) {
-                const float m_new = grow ? m_half : m_use;
-                // lanes that keep their max keep their sums (alpha 1; also avoids -inf - -inf)
-                const float alpha = grow ? fast_exp2((m_use - m_new) * c) : 1.0f;
-                m_use = m_new;
-                l_run *= alpha;
-#pragma unroll
-                for (int db = 0; db < 4; ++db)
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) acc_o[db][j] *= alpha;
-            }
-            const float mc = m_use * c;
-            v8 pf[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                v8 t;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) t[k] = (T)fast_exp2(fmaf(s[kb][h * 8 + k], c, -mc));
-                pf[h] = t;
-            }
-            // row sums of the rounded probabilities that P.V consumes (v_dot2 against ones)
-            {
-                const v2 one2 = {(T)1.0f, (T)1.0f};
-                float l0 = 0.0f, l1 = 0.0f;
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int q = 0; q < 8; q += 4) {
-                        l0 = dot2(v2{pf[h][q], pf[h][q + 1]}, one2, l0);
-                        l1 = dot2(v2{pf[h][q + 2], pf[h][q + 3]}, one2, l1);
-                    }
-                l_run += l0 + l1;
-            }
-            // O^T += V^T P^T: keys kb*32 + g*16 + h*8 + [0..7] of dims db*32 + [0..31] (the four
-            // output blocks alternate, so consecutive MFMAs are independent)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const T* vb = Vb + vofs[db];
-                    const i16x4 lo = lds_read_tr16(vb + (kb * 32 + h * 8) * KV_ROW);
-                    const i16x4 hi = lds_read_tr16(vb + (kb * 32 + h * 8 + 4) * KV_ROW);
-                    const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                    acc_o[db] = Mma16<T>::mma(af, pf[h], acc_o[db]);
-                }
+        for (int ks = 0; ks < 8; ++ks) {
+            s0 = Mma16<T>::mma(ks < 4 ? kf[ks] : *(const v8*)(Kb + koff[ks]), qf[ks], s0);
+            if (ks & 1) s1 = Mma16<T>::mma(*(const v8*)(Kb + 32 * KV_ROW + koff[ks >> 1]), qf[ks >> 1], s1);
         }
+        rescale(half_max(s0, n0, mask_c));
+#pragma unroll
+        for (int ks = 4; ks < 8; ++ks) s1 = Mma16<T>::mma(*(const v8*)(Kb + 32 * KV_ROW + koff[ks]), qf[ks], s1);
+        v8 p0[2], p1[2];
+        half_p(s0, p0);
+        pv(Vb, 0, 0, p0[0]);
+        pv(Vb, 0, 1, p0[1]);
+        rescale(half_max(s1, n0 + 32, mask_c));
+        half_p(s1, p1);
+        pv(Vb, 1, 0, p1[0]);
+        pv(Vb, 1, 1, p1[1]);
         // this wave's copies of tile i + 1; unconditional, so that no load is pending on the
         // loop's back edge and the compiler adds no wait of its own inside the next step
         __builtin_amdgcn_s_waitcnt(VMCNT0);
         __syncthreads();
     };
+    // tiles of a block before mask_from see only keys at or before the block's first query
+    auto mask_from = [&](int qb) { return (off + qb * P + 1) / BN; };
+    std::integral_constant<bool, false> no_mask;
+    std::integral_constant<bool, true> with_mask;
 
     begin_block(qb_a);
     lookup(0);  // issued before Q, so that resolving it waits for the table read alone
     load_q(qb_a);
     resolve();
     load_tile(0, 0);
-    if (n_sched > 1) lookup(sched_tile(1));
+    lookup(sched_tile(min(1, n_sched - 1)));
     __builtin_amdgcn_s_waitcnt(VMCNT0);  // Q and this wave's copies of tile 0
     __syncthreads();
     // The two blocks run as two loops whose bodies issue only the tile and table loads:
     // Q, gate and output traffic stays between them, so the compiler's wait counting never
     // holds a tile's S^T behind the next tile's prefetch.
-    for (int i = 0; i < nt_a; ++i) step(i);
+    {
+        const int mf = min(mask_from(qb_a), nt_a);
+        for (int i = 0; i < mf; ++i) step(i, no_mask);
+        for (int i = mf; i < nt_a; ++i) step(i, with_mask);
+    }
     if (n_blocks == 2) load_q(qb_b);  // lands while block a's output is written
     finish_block(qb_a, (nt_a - 1) & 1);  // the buffer of block a's last tile is free
     if (n_blocks == 2) {
         begin_block(qb_b);
         __builtin_amdgcn_s_waitcnt(VMCNT0);  // Q of block b and block a's stores, once
-        for (int i = nt_a; i < n_sched; ++i) step(i);
+        const int mf = nt_a + min(mask_from(qb_b), n_sched - nt_a);
+        for (int i = nt_a; i < mf; ++i) step(i, no_mask);
+        for (int i = mf; i < n_sched; ++i) step(i, with_mask);
         finish_block(qb_b, 0);
     }
 }
