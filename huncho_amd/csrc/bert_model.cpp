@@ -118,6 +118,7 @@ extern "C" int hk_bert_model_create(hk_ctx* ctx, int dtype, const hk_bert_config
         return hk_fail(ctx, HK_ERR_INVALID, "invalid ModernBERT configuration");
     if (c.n_out > 0 && !head_w) return hk_fail(ctx, HK_ERR_INVALID, "missing head weight");
     hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);  // staged tensors written by queued work are complete
     if (int rc = hk_blas_prepare(ctx)) return rc;  // GEMM handle + workspace, before any forward
     hk_bert_model* m = new hk_bert_model();
     m->ctx = ctx;
@@ -155,6 +156,8 @@ extern "C" int hk_bert_model_create(hk_ctx* ctx, int dtype, const hk_bert_config
     }
     if ((rc = b_table(m, c.global_theta, &m->cos_g, &m->sin_g)) || (rc = b_table(m, c.local_theta, &m->cos_l, &m->sin_l)))
         return fail(rc);
+    hipStreamSynchronize(nullptr);  // the weight copies, on the null stream, are complete before the
+                                    // context's stream (non-blocking) uses them
     *out = m;
     return HK_OK;
 }

@@ -128,6 +128,7 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
         return hk_fail(ctx, HK_ERR_INVALID, "invalid model configuration");
     if (c.n_out > 0 && !head_w) return hk_fail(ctx, HK_ERR_INVALID, "missing decision head");
     hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);  // staged tensors written by queued work are complete
     if (int rc = hk_blas_prepare(ctx)) return rc;  // GEMM handle + workspace, before any forward
     hk_kev_model* m = new hk_kev_model();
     m->ctx = ctx;
@@ -200,6 +201,8 @@ extern "C" int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* 
         hk_rope_fill_table(c.rotary_dim, c.rope_theta, c.max_context, dtype, cs.data(), sn.data());
         if ((rc = upload_f32(m, cs, &m->rope_cos)) || (rc = upload_f32(m, sn, &m->rope_sin))) return fail(rc);
     }
+    hipStreamSynchronize(nullptr);  // the weight copies, on the null stream, are complete before the
+                                    // context's stream (non-blocking) uses them
     *out = m;
     return HK_OK;
 }

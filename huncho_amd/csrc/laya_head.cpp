@@ -109,6 +109,7 @@ extern "C" int hk_laya_head_create(hk_ctx* ctx, int dtype, const hk_laya_head_co
     if (cfg->n_layers <= 0 || cfg->n_layers > 64 || cfg->ffn <= 0 || cfg->scorer_hidden <= 0 || cfg->n_types <= 0)
         return hk_fail(ctx, HK_ERR_INVALID, "bad Laya head configuration");
     hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);  // staged tensors written by queued work are complete
     if (int rc = hk_blas_prepare(ctx)) return rc;
     hk_laya_head* h = new hk_laya_head();
     h->ctx = ctx;
@@ -155,6 +156,8 @@ extern "C" int hk_laya_head_create(hk_ctx* ctx, int dtype, const hk_laya_head_co
         if (!rc) h->l2_b = b2[0];
     }
     if (rc) return fail(rc);
+    hipStreamSynchronize(nullptr);  // the weight copies, on the null stream, are complete before the
+                                    // context's stream (non-blocking) uses them
     *out = h;
     return HK_OK;
 }

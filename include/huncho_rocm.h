@@ -254,7 +254,9 @@ int hk_lora_merge(hk_ctx* ctx, int dtype, void* w_dev, int rows, int cols, const
 
 typedef struct hk_kev_model hk_kev_model;
 
-/* Loads (copies and fuses) the weights; the caller's buffers may be freed afterwards.
+/* Loads (copies and fuses) the weights; the caller's buffers may be freed afterwards. Waits for
+ * the work queued on the context's stream first (staged tensors may come from it) and returns
+ * once the copies are complete (load time only: model and head creation block the host).
  * head_w [n_out][hidden] (model dtype), head_b [n_out] fp32 or NULL. */
 int hk_kev_model_create(hk_ctx* ctx, int dtype, const hk_kev_config* cfg, const hk_kev_layer_weights* layers_host,
                         const void* embed_dev, const void* final_norm_dev, const void* head_w_dev,
