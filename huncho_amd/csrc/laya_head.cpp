@@ -188,6 +188,8 @@ extern "C" int hk_laya_head_forward(hk_laya_head* h, const void* hidden, const i
         !positions_host || !workspace || !scores_dev || n_seqs <= 0 || n_seqs > 64)
         return hk_fail(ctx, HK_ERR_INVALID, "invalid Laya head arguments (1..64 sequences)");
     if (cu_host[0] != 0 || cu_positions_host[0] != 0) return hk_fail(ctx, HK_ERR_INVALID, "cu arrays must start at 0");
+    if (((uintptr_t)hidden | (uintptr_t)workspace) & 15)
+        return hk_fail(ctx, HK_ERR_INVALID, "hidden rows and workspace must be 16-byte aligned");
     // validate every sequence before any work (candle.rs:319-335)
     int max_len = 0;
     for (int s = 0; s < n_seqs; ++s) {

@@ -473,7 +473,9 @@ int hk_laya_head_workspace_size(hk_laya_head* h, int n_tokens, int n_positions, 
 /* LayaHead::forward for each sequence of an unpadded varlen batch (1..64 sequences): hidden
  * [n_tokens][d] (the encoder's final-normed rows, model dtype), qtype per sequence,
  * positions[cu_positions[s] .. cu_positions[s + 1]) relative to sequence s (host and device
- * copies). Writes one fp32 score per position (the reference's [n, 1] output). */
+ * copies). Writes one fp32 score per position (the reference's [n, 1] output). hidden and the
+ * workspace (hk_laya_head_workspace_size bytes) are 16-byte aligned; an unknown qtype, an empty
+ * sequence or a position outside its sequence is HK_ERR_INVALID before any work. */
 int hk_laya_head_forward(hk_laya_head* h, const void* hidden_dev, const int32_t* cu_seqlens_dev,
                          const int32_t* cu_seqlens_host, int n_seqs, const int32_t* qtype_host,
                          const int32_t* cu_positions_dev, const int32_t* cu_positions_host,
