@@ -138,6 +138,29 @@ def test_small_hybrid_fp32_probabilities(ctx):
     model.close()
 
 
+def test_max_context_row_fp32(ctx):
+    """A row of exactly max_context (8192) tokens beside a 3-token row: 512 pages in its block
+    table, 128 key tiles of attention, 128 delta-rule chunks; both rows against the fp32 oracle.
+    One token more is rejected before any work."""
+    shape = KevShape(hidden=256, n_layers=4, n_heads=2, n_kv_heads=1, intermediate=512, vocab=1000,
+                     lin_n_k_heads=2, lin_n_v_heads=2, rotary_dim=64, rope_theta=10000.0, n_out=5, max_context=8192)
+    weights = synthetic_weights(shape, SEED + 2, std=0.05)
+    rows = [abi.synth_uniform_int(SEED, 900, shape.max_context, 0, shape.vocab - 1),
+            abi.synth_uniform_int(SEED, 901, 3, 0, shape.vocab - 1)]
+    model = KevModel(ctx, shape, weights, torch.float32)
+    logits, probs = model.forward_batch(rows, temperature=1.3)
+    ref_model, head_w = oracle_model(shape, weights, bf16=False)
+    ref_logits, ref_probs = oracle_scores(ref_model, head_w, rows, 1.3)
+    dp = float(np.abs(probs - ref_probs).max())
+    dl = float(np.abs(logits - ref_logits).max() / np.abs(ref_logits).max())
+    print(f"fp32 max-context row: max |dp| = {dp:.3e}, rel dlogit = {dl:.3e}")
+    assert dp < 2e-5 and dl < 1e-4, (dp, dl)
+    with pytest.raises(abi.HkError):
+        model.forward_batch([np.concatenate([rows[0], rows[1][:1]])])
+    assert ctx.take_faults() == 0
+    model.close()
+
+
 def test_forward_rejects_out_of_vocab_before_work(ctx):
     shape = KevShape(hidden=256, n_layers=4, n_heads=2, n_kv_heads=1, intermediate=512, vocab=1000,
                      lin_n_k_heads=2, lin_n_v_heads=2, rotary_dim=64, n_out=3)
