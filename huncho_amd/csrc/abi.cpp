@@ -368,7 +368,7 @@ int hk_qk_norm_rope_kv_write_impl(hk_ctx* ctx, int dtype, const void* q_in, long
                                   int rope_max_pos, const int32_t* cu, const int32_t* ctxl, int n_seqs, int n_tokens,
                                   const int32_t* bt, int bt_stride, int num_pages, int page_size, int q_heads,
                                   int kv_heads, int head_dim, void* q_out, long q_out_tok, long q_out_head,
-                                  void* k_pool, void* v_pool) {
+                                  void* k_pool, void* v_pool, const int32_t* tok_sp) {
     if (!ctx) return HK_ERR_INVALID;
     if (int rc = check_dtype(ctx, dtype)) return rc;
     if (head_dim != 128) return hk_fail(ctx, HK_ERR_UNSUPPORTED, "head_dim %d: only 128 is implemented", head_dim);
@@ -384,7 +384,7 @@ int hk_qk_norm_rope_kv_write_impl(hk_ctx* ctx, int dtype, const void* q_in, long
     hipSetDevice(ctx->device);
     hk::KvArgs a{q_in, q_in_tok, q_in_head, k_in, k_in_tok, v_in, v_in_tok, q_norm, k_norm, eps, rope_cos, rope_sin,
                  rd, rope_max_pos, cu, ctxl, n_seqs, n_tokens, bt, bt_stride, num_pages, shift, q_heads, kv_heads,
-                 q_out, q_out_tok, q_out_head, k_pool, v_pool, ctx->fault_dev};
+                 q_out, q_out_tok, q_out_head, k_pool, v_pool, ctx->fault_dev, tok_sp};
     int rc = hk_launch_qk_norm_rope_kv_write(dtype, &a, ctx->stream);
     return rc ? hk_fail(ctx, rc, "qk_norm_rope_kv_write launch failed") : HK_OK;
 }
@@ -400,7 +400,7 @@ extern "C" int hk_qk_norm_rope_kv_write(hk_ctx* ctx, int dtype, const void* q_in
     return hk_qk_norm_rope_kv_write_impl(ctx, dtype, q_in, q_in_tok, q_in_head, k_in, k_in_tok, v_in, v_in_tok, q_norm,
                                          k_norm, eps, rope_cos, rope_sin, rd, rope_max_pos, cu, ctxl, n_seqs, n_tokens,
                                          bt, bt_stride, num_pages, page_size, q_heads, kv_heads, head_dim, q_out,
-                                         q_out_tok, q_out_head, k_pool, v_pool);
+                                         q_out_tok, q_out_head, k_pool, v_pool, nullptr);
 }
 
 extern "C" int hk_paged_kv_write(hk_ctx* ctx, int dtype, const void* k, const void* v, const int32_t* cu,
@@ -409,7 +409,7 @@ extern "C" int hk_paged_kv_write(hk_ctx* ctx, int dtype, const void* k, const vo
     return hk_qk_norm_rope_kv_write_impl(ctx, dtype, nullptr, 0, 0, k, (long)kv_heads * head_dim, v,
                                          (long)kv_heads * head_dim, nullptr, nullptr, 0.f, nullptr, nullptr, 0, 0, cu,
                                          ctxl, n_seqs, n_tokens, bt, bt_stride, num_pages, page_size, 0, kv_heads,
-                                         head_dim, nullptr, 0, 0, k_pool, v_pool);
+                                         head_dim, nullptr, 0, 0, k_pool, v_pool, nullptr);
 }
 
 extern "C" int hk_paged_prefill_attention(hk_ctx* ctx, int dtype, const void* q, long q_tok, long q_head,

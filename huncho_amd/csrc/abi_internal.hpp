@@ -36,6 +36,15 @@ uint16_t hk_host_f32_to_f16(float x);
 int hk_gemm_xwt(hk_ctx* ctx, int dtype, int n, int out, int in, const void* x, long ldx, const void* w, long ldw,
                 void* y, long ldy, const void* c, long ldc, float alpha, float beta);
 
+// hk_qk_norm_rope_kv_write with an optional per-token (sequence, position) table (int pairs,
+// hk_launch_token_seq_pos), which replaces the kernel's search of cu_seqlens
+int hk_qk_norm_rope_kv_write_impl(hk_ctx* ctx, int dtype, const void* q_in, long q_in_tok, long q_in_head,
+                                  const void* k_in, long k_in_tok, const void* v_in, long v_in_tok, const float* q_norm,
+                                  const float* k_norm, float eps, const float* rope_cos, const float* rope_sin, int rd,
+                                  int rope_max_pos, const int32_t* cu, const int32_t* ctxl, int n_seqs, int n_tokens,
+                                  const int32_t* bt, int bt_stride, int num_pages, int page_size, int q_heads,
+                                  int kv_heads, int head_dim, void* q_out, long q_out_tok, long q_out_head,
+                                  void* k_pool, void* v_pool, const int32_t* tok_sp);
 // Argument checks shared by hk_mean_pool_head and its variants (HK_OK or an error set on ctx).
 int hk_mean_pool_check(hk_ctx* ctx, int dtype, const void* x, long x_tok, const int32_t* cu, int n_seqs, int n_tokens,
                        int width, const void* head_w, int n_out, const float* logits);

@@ -99,6 +99,9 @@ struct KvArgs {
     void* k_pool;
     void* v_pool;
     int* fault;
+    // [n_tokens] (sequence, absolute position) pairs, or null: then each token's pair is found
+    // from cu_seqlens_q and context_lens
+    const int* tok_sp;
 };
 
 struct PrepArgs {
@@ -308,6 +311,10 @@ int hk_launch_final_norm_head(int dtype, const void* x, long x_tok, const int* c
                               float eps, int width, const void* head_w, const float* head_b, int n_out, float* logits,
                               void* h_out, hipStream_t st);
 int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st);
+// out[t] = (sequence of token t, its absolute position ctxl[s] - q_len + (t - q0)) as int pairs;
+// a sequence whose range lies outside [0, n_tokens) sets fault bit 1 and writes nothing
+int hk_launch_token_seq_pos(const int* cu, const int* ctxl, int n_seqs, int n_tokens, int* out, int* fault,
+                            hipStream_t st);
 int hk_launch_readout(int dtype, const hk::ReadoutArgs* a, hipStream_t st);
 int hk_launch_gemm(int dtype16, int epi, const hk::GemmArgs* a, hipStream_t stream);
 int hk_launch_lora_merge(int dtype, void* w, long rows, int cols, const float* a, const float* b, int rank, float scale,

@@ -231,6 +231,7 @@ struct Buffers {
     void *x, *h, *big, *ba, *q, *k, *v, *o, *act, *k_pool, *v_pool;
     float *g, *beta;
     int* ctx_lens;
+    int* tok_sp;  // [n][2]: each token's sequence and absolute position
     size_t pool_bytes;
 };
 
@@ -254,6 +255,7 @@ Buffers carve(const hk_kev_model* m, Workspace& ws, int n, int n_seqs, int num_p
     b.g = ws.take<float>((size_t)n * c.lin_n_v_heads);
     b.beta = ws.take<float>((size_t)n * c.lin_n_v_heads);
     b.ctx_lens = ws.take<int>((size_t)n_seqs);
+    b.tok_sp = ws.take<int>((size_t)2 * n);
     b.pool_bytes = (size_t)num_pages * c.n_kv_heads * c.page_size * c.head_dim * e;
     b.k_pool = ws.take_bytes(b.pool_bytes);
     b.v_pool = ws.take_bytes(b.pool_bytes);
@@ -403,6 +405,10 @@ int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
     } else {
         RUN(hk_launch_seq_lens(cu_dev, n_seqs, b.ctx_lens, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "seq_lens") : 0);
     }
+    // each token's sequence and position, once for all attention layers
+    RUN(hk_launch_token_seq_pos(cu_dev, ctx_lens, n_seqs, n, b.tok_sp, ctx->fault_dev, ctx->stream)
+            ? hk_fail(ctx, HK_ERR_DEVICE, "token_seq_pos launch")
+            : 0);
     int ai = 0, gi = 0;  // attention / Gated DeltaNet layer ordinals
     RUN(hk_launch_embed(dt, ids, n, m->embed, c.vocab, H, b.x, ctx->fault_dev, ctx->stream)
             ? hk_fail(ctx, HK_ERR_DEVICE, "embed launch")
@@ -446,10 +452,10 @@ int kev_forward_impl(hk_kev_model* m, const int32_t* ids, const int32_t* cu_dev,
             char* qg = (char*)b.big;
             char* kin = qg + (size_t)2 * Hq * hd * e;
             char* vin = kin + (size_t)Hkv * hd * e;
-            RUN(hk_qk_norm_rope_kv_write(ctx, dt, qg, rows, 2 * hd, kin, rows, vin, rows, L.q_norm, L.k_norm, c.eps,
-                                         m->rope_cos, m->rope_sin, c.rotary_dim, c.max_context, cu_dev, ctx_lens,
-                                         n_seqs, n, bt, bt_stride, num_pages, c.page_size, Hq, Hkv, hd, qg, rows,
-                                         2 * hd, k_pool, v_pool));
+            RUN(hk_qk_norm_rope_kv_write_impl(ctx, dt, qg, rows, 2 * hd, kin, rows, vin, rows, L.q_norm, L.k_norm,
+                                              c.eps, m->rope_cos, m->rope_sin, c.rotary_dim, c.max_context, cu_dev,
+                                              ctx_lens, n_seqs, n, bt, bt_stride, num_pages, c.page_size, Hq, Hkv, hd,
+                                              qg, rows, 2 * hd, k_pool, v_pool, b.tok_sp));
             RUN(hk_paged_prefill_attention(ctx, dt, qg, rows, 2 * hd, k_pool, v_pool, num_pages, c.page_size, bt,
                                            bt_stride, cu_dev, ctx_lens, n_seqs, n, max_len, Hq, Hkv, hd,
                                            (float)(1.0 / sqrt((double)hd)), qg + (size_t)hd * e, rows, 2 * hd, b.o,

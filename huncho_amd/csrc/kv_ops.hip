@@ -154,25 +154,37 @@ __global__ __launch_bounds__(1024) void qk_norm_rope_kv_write_vec(KvArgs a) {
         w0 = *(const f32x4*)(w + sub * 8);
         w1 = *(const f32x4*)(w + sub * 8 + 4);
     }
-    // 2. sequence and position: cu_seqlens and context_lens staged in LDS by one coalesced
-    //    load each, so the search and the lookups are LDS reads
-    __shared__ int cu_s[CU_LDS + 1], ctx_s[CU_LDS];
-    const bool staged = a.n_seqs <= CU_LDS;
-    if (staged) {
-        for (int i = threadIdx.x; i <= a.n_seqs; i += blockDim.x) {
-            cu_s[i] = a.cu_seqlens_q[i];
-            if (i < a.n_seqs) ctx_s[i] = a.context_lens[i];
+    // 2. sequence and position: one 8-byte load from the per-token table when given; else
+    //    cu_seqlens and context_lens staged in LDS by one coalesced load each, so the search and
+    //    the lookups are LDS reads
+    int s, pos;
+    if (a.tok_sp) {
+        const int2 sp = ((const int2*)a.tok_sp)[t];
+        s = sp.x;
+        pos = sp.y;
+        if ((unsigned)s >= (unsigned)a.n_seqs || pos < 0) {  // uniform across the workgroup
+            if (threadIdx.x == 0) atomicOr(a.fault, 1);
+            return;
         }
-        __syncthreads();
-    }
-    const int* cu = staged ? cu_s : a.cu_seqlens_q;
-    const int* ctxl = staged ? ctx_s : a.context_lens;
-    const int s = find_seq(cu, a.n_seqs, t);
-    const int q0 = cu[s], q_len = cu[s + 1] - q0;
-    const int pos = ctxl[s] - q_len + (t - q0);
-    if (pos < 0 || t - q0 >= q_len) {  // uniform across the workgroup
-        if (threadIdx.x == 0) atomicOr(a.fault, 1);
-        return;
+    } else {
+        __shared__ int cu_s[CU_LDS + 1], ctx_s[CU_LDS];
+        const bool staged = a.n_seqs <= CU_LDS;
+        if (staged) {
+            for (int i = threadIdx.x; i <= a.n_seqs; i += blockDim.x) {
+                cu_s[i] = a.cu_seqlens_q[i];
+                if (i < a.n_seqs) ctx_s[i] = a.context_lens[i];
+            }
+            __syncthreads();
+        }
+        const int* cu = staged ? cu_s : a.cu_seqlens_q;
+        const int* ctxl = staged ? ctx_s : a.context_lens;
+        s = find_seq(cu, a.n_seqs, t);
+        const int q0 = cu[s], q_len = cu[s + 1] - q0;
+        pos = ctxl[s] - q_len + (t - q0);
+        if (pos < 0 || t - q0 >= q_len) {  // uniform across the workgroup
+            if (threadIdx.x == 0) atomicOr(a.fault, 1);
+            return;
+        }
     }
     if (a.rope_cos && pos >= a.rope_max_pos) {
         if (threadIdx.x == 0) atomicOr(a.fault, 4);

@@ -609,11 +609,30 @@ __global__ void seq_lens_kernel(const int* cu, int n, int* out) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s < n) out[s] = cu[s + 1] - cu[s];
 }
+
+// one workgroup per sequence: (s, position) of each of its tokens, 8-byte stores
+__global__ __launch_bounds__(256) void token_seq_pos_kernel(const int* cu, const int* ctxl, int n_tokens, int* out,
+                                                            int* fault) {
+    const int s = blockIdx.x;
+    const int q0 = cu[s], q_len = cu[s + 1] - q0, off = ctxl[s] - q_len;
+    if (q0 < 0 || q_len < 0 || q0 + q_len > n_tokens) {
+        if (threadIdx.x == 0) atomicOr(fault, 1);
+        return;
+    }
+    for (int i = threadIdx.x; i < q_len; i += 256) ((int2*)out)[q0 + i] = make_int2(s, off + i);
+}
 }  // namespace hk
 
 extern "C" int hk_launch_seq_lens(const int* cu, int n, int* out, hipStream_t st) {
     if (n == 0) return HK_OK;
     hipLaunchKernelGGL(hk::seq_lens_kernel, dim3((n + 255) / 256), dim3(256), 0, st, cu, n, out);
+    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
+}
+
+extern "C" int hk_launch_token_seq_pos(const int* cu, const int* ctxl, int n_seqs, int n_tokens, int* out, int* fault,
+                                       hipStream_t st) {
+    if (n_seqs == 0 || n_tokens == 0) return HK_OK;
+    hipLaunchKernelGGL(hk::token_seq_pos_kernel, dim3(n_seqs), dim3(256), 0, st, cu, ctxl, n_tokens, out, fault);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
