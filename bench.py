@@ -14,7 +14,9 @@ sequences with seeded lengths in [256, 4096]. One step = one encoder forward of 
 
 Prints one JSON line: whole-job tokens/s, the live-measured roofline of the attention kernel
 (MFMA-bound, bf16 dense peak 2.5 PFLOP/s) and, for Kev, of the delta-rule kernel (HBM-bound,
-8 TB/s), and the CPU oracle's forward timed on this host's cores as a reported baseline.
+8 TB/s), and the CPU oracle's forward timed on this host's cores as a reported baseline. The
+default Kev run also measures the Laya workload (same steps and warmup) and adds its tokens/s and
+attention rooflines to the line as `laya` (`--no-laya` skips it).
 """
 from __future__ import annotations
 
@@ -46,6 +48,8 @@ def parse():
     p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
     p.add_argument("--kernel-iters", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-laya", action="store_true",
+                   help="kev: skip the Laya encoder measurement that the default run adds to its line")
     p.add_argument("--kernels-only", action="store_true",
                    help="time only the roofline kernels (no model; for counter collection)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -409,7 +413,8 @@ def laya_cpu_baseline(shape, weights, threads, n_rows=3, n_tokens=2048):
                               "sample": f"1 sequence x 256 tokens, 1 thread, {dt1:.2f} s"}}
 
 
-def run_laya(args, dtype):
+def laya_measure(args, dtype):
+    """The Laya encoder workload's bench line (without the CPU baseline)."""
     import numpy as np
     import torch
 
@@ -478,6 +483,12 @@ def run_laya(args, dtype):
                                      "hbm_frac": round(lo["bytes"] / lo["seconds"] / HBM_PEAK, 4)},
         "device": {"name": info.name.decode(), "cus": info.compute_units, "clock_mhz": info.clock_khz // 1000},
     }
+    model.close()
+    return line, shape, weights
+
+
+def run_laya(args, dtype):
+    line, shape, weights = laya_measure(args, dtype)
     if not args.no_cpu_baseline:
         threads = default_threads(args)
         log(f"CPU baseline with {threads} threads and 1 thread")
@@ -638,6 +649,14 @@ def run_kev(args, dtype):
         log(f"CPU baseline with {threads} threads and 1 thread")
         line["cpu_baseline"] = cpu_baseline(shape, weights, args.seq_len, threads)
         line["cpu_kernel_baselines"] = cpu_kernel_baselines(threads)
+    if not args.no_laya:
+        # the second workload (16 varlen ModernBERT-base rows, 256..4096 tokens), same steps
+        log("second workload: the Laya encoder")
+        sub = argparse.Namespace(**vars(args))
+        sub.batch = 0
+        laya, _, _ = laya_measure(sub, dtype)
+        line["laya"] = {k: laya[k] for k in ("metric", "value", "unit", "steps", "warmup", "ms_per_step", "config",
+                                             "roofline", "roofline_local_attention")}
     print(json.dumps(line), flush=True)
 
 
