@@ -113,7 +113,7 @@ def kernel_rooflines(ctx, shape, n_seqs, seq_len, dtype, iters):
     t_attn = time_launches(lambda: paged_prefill_attention(ctx, q, kp, vp, bt, cu, lens, seq_len, gate=gate,
                                                            out=out), iters, stream)
     attn_flops = 4.0 * hq * d * seq_len * (seq_len + 1) / 2 * n_seqs
-    attn_bytes = n * (2 * hq + 2 * hkv) * d * 2
+    attn_bytes = n * (3 * hq + 2 * hkv) * d * 2  # Q, K, V, O and the output gate rows
 
     # the varlen paged GQA prefill batch: 32 sequences with seeded lengths in [64, 2048], pages
     # of 16 from a seeded permutation of a 4096-page pool (the compute-bound attention shape)
@@ -631,7 +631,10 @@ def run_kev(args, dtype):
                      "peak": MFMA_PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                      "frac": round(attn_achieved * 1e12 / MFMA_PEAK_BF16, 4), "traffic": traffic_of("attention"),
                      "us_per_launch": round(a["seconds"] * 1e6, 2), "flops_per_launch": a["flops"],
-                     "hbm_frac": round(a["bytes"] / a["seconds"] / HBM_PEAK, 4)},
+                     "bytes_per_launch": a["bytes"], "hbm_frac": round(a["bytes"] / a["seconds"] / HBM_PEAK, 4),
+                     # the roofline ceiling at this launch's arithmetic intensity (FLOP per algorithmic
+                     # byte), as a share of the MFMA peak: below 1, HBM bounds the launch first
+                     "ceiling_frac": round(min(1.0, a["flops"] / a["bytes"] * HBM_PEAK / MFMA_PEAK_BF16), 4)},
         "roofline_attention_varlen": {
             "kernel": "paged_prefill_attn (32 sequences, lengths 64..2048, no gate)", "bound": "mfma",
             "achieved": round(kr["attention_varlen"]["flops"] / kr["attention_varlen"]["seconds"] / 1e12, 2),

@@ -580,15 +580,13 @@ __global__ __launch_bounds__(256, 1) void paged_prefill_attn_f32(AttnArgs a) {
 // ---------------------------------------------------------------------------
 extern "C" int hk_launch_paged_prefill_attention(int dtype, const hk::AttnArgs* args, int n_seqs,
                                                  int n_qblocks, hipStream_t stream) {
-    static bool configured = false;
-    if (!configured) {
-        if (hipFuncSetAttribute((const void*)hk::paged_prefill_attn_16<hk::bf16>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)hk::ATTN16_LDS) != hipSuccess ||
-            hipFuncSetAttribute((const void*)hk::paged_prefill_attn_16<hk::f16>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)hk::ATTN16_LDS) != hipSuccess)
-            return HK_ERR_DEVICE;
-        configured = true;
-    }
+    // set once, under C++'s thread-safe static initialisation (replicas launch from several threads)
+    static const bool configured =
+        hipFuncSetAttribute((const void*)hk::paged_prefill_attn_16<hk::bf16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)hk::ATTN16_LDS) == hipSuccess &&
+        hipFuncSetAttribute((const void*)hk::paged_prefill_attn_16<hk::f16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)hk::ATTN16_LDS) == hipSuccess;
+    if (!configured) return HK_ERR_DEVICE;
     // 16-bit: one workgroup per mirrored pair of q-blocks; fp32: one per q-block
     if (dtype == hk::DT_F32) {
         hipLaunchKernelGGL(hk::paged_prefill_attn_f32, dim3(args->kv_heads, n_seqs, n_qblocks), dim3(256), 0, stream,

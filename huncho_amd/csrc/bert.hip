@@ -510,15 +510,13 @@ extern "C" int hk_launch_bidir_attention(int dtype, const hk::BertAttnArgs* a, i
                            *a);
         return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
     }
-    static bool configured = false;
-    if (!configured) {
-        if (hipFuncSetAttribute((const void*)hk::bert::bidir_attn_16<hk::bf16>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)hk::bert::LDS16) != hipSuccess ||
-            hipFuncSetAttribute((const void*)hk::bert::bidir_attn_16<hk::f16>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)hk::bert::LDS16) != hipSuccess)
-            return HK_ERR_DEVICE;
-        configured = true;
-    }
+    // set once, under C++'s thread-safe static initialisation (replicas launch from several threads)
+    static const bool configured =
+        hipFuncSetAttribute((const void*)hk::bert::bidir_attn_16<hk::bf16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)hk::bert::LDS16) == hipSuccess &&
+        hipFuncSetAttribute((const void*)hk::bert::bidir_attn_16<hk::f16>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)hk::bert::LDS16) == hipSuccess;
+    if (!configured) return HK_ERR_DEVICE;
     hk::BertAttnArgs b = *a;
     b.qblocks = (max_len + 127) / 128;
     const long groups = (long)b.heads * n_seqs;

@@ -326,13 +326,11 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_f32(GdnArgs a) {
 extern "C" int hk_launch_gated_delta_chunked(int dtype, const hk::GdnArgs* args, int n_seqs, hipStream_t stream) {
     if (dtype != hk::DT_F32) return hk_launch_gdn16(dtype, 0, args, nullptr, n_seqs, stream);
     dim3 grid(args->H, n_seqs);
-    static bool configured = false;
-    if (!configured) {
-        if (hipFuncSetAttribute((const void*)hk::gdn_chunk_f32, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)hk::GDN_F32_LDS) != hipSuccess)
-            return HK_ERR_DEVICE;
-        configured = true;
-    }
+    // set once, under C++'s thread-safe static initialisation (replicas launch from several threads)
+    static const bool configured = hipFuncSetAttribute((const void*)hk::gdn_chunk_f32,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)hk::GDN_F32_LDS) == hipSuccess;
+    if (!configured) return HK_ERR_DEVICE;
     hipLaunchKernelGGL(hk::gdn_chunk_f32, grid, dim3(256), hk::GDN_F32_LDS, stream, *args);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }

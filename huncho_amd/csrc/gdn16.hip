@@ -662,14 +662,11 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa
 
 template <typename T, bool FUSED>
 static int launch16(const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs, hipStream_t stream) {
-    static bool configured = false;
     auto kern = hk::gdn16::gdn_chunk16<T, FUSED>;
-    if (!configured) {
-        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)hk::gdn16::LDS_BYTES) != hipSuccess)
-            return HK_ERR_DEVICE;
-        configured = true;
-    }
+    // set once, under C++'s thread-safe static initialisation (replicas launch from several threads)
+    static const bool configured = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)hk::gdn16::LDS_BYTES) == hipSuccess;
+    if (!configured) return HK_ERR_DEVICE;
     hipLaunchKernelGGL(kern, dim3(a->H, n_seqs), dim3(hk::gdn16::NTHREADS), hk::gdn16::LDS_BYTES, stream, *a, *fa);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }

@@ -204,14 +204,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_xwt(GemmArgs a) {
 
 template <typename T, int EPI>
 static int launch_gemm(const hk::GemmArgs* a, hipStream_t stream) {
-    static bool configured = false;
     auto kern = hk::gemm::gemm_xwt<T, EPI>;
-    if (!configured) {
-        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)hk::gemm::LDS_BYTES) != hipSuccess)
-            return HK_ERR_DEVICE;
-        configured = true;
-    }
+    // set once, under C++'s thread-safe static initialisation (replicas launch from several threads)
+    static const bool configured = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)hk::gemm::LDS_BYTES) == hipSuccess;
+    if (!configured) return HK_ERR_DEVICE;
     const int tiles = (a->N / hk::gemm::BN) * ((a->M + hk::gemm::BM - 1) / hk::gemm::BM);
     hipLaunchKernelGGL(kern, dim3(tiles), dim3(hk::gemm::NTHREADS), hk::gemm::LDS_BYTES, stream, *a);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
