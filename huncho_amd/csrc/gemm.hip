@@ -16,7 +16,9 @@
 // consecutive ones: outputs leave as 8-byte stores, and with the SwiGLU weight layout below a
 // lane holds each gate column and its up column.
 // K steps of 64: W and X tiles (256 rows x 128 B each, whole 128-byte lines) go from global
-// memory straight into LDS (global_load_lds_dwordx4, 8 rows per copy) through two buffers
+// memory straight into LDS (buffer_load_dwordx4 ... lds, 8 rows per copy: loop-invariant lane
+// offsets, one scalar offset per K step, no vector address arithmetic; X rows past M read as
+// zeros through the buffer's bound) through two buffers
 // (2 x 64 KB); a step's copies are issued when it starts and have the step's 64 MFMAs per wave
 // to arrive. (K steps of 32 through a 4-stage ring read half lines per row and were 5-8 %
 // slower.) A row's 16-byte chunk c sits at physical chunk c ^ ((row >> 1) & 7): the 16 rows
@@ -46,6 +48,18 @@ __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
 template <typename T> __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+// raw buffer resource (stride 0): loads at byte offsets >= bytes return zeros
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, unsigned bytes) {
+    const unsigned long long b = (unsigned long long)base;
+    return i32x4_t{__builtin_amdgcn_readfirstlane((int)(b & 0xffffffffu)), __builtin_amdgcn_readfirstlane((int)(b >> 32)),
+                   __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+// one buffer_load_dwordx4 into LDS: lane l copies 16 bytes at voff + soff to LDS byte lds + 16 l
+__device__ __forceinline__ void buf_copy_x4(i32x4_t rsrc, unsigned voff, unsigned soff, unsigned lds) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
+}
+
 template <typename T, int EPI>
 __global__ __launch_bounds__(NTHREADS, 1) void gemm_xwt(GemmArgs a) {
     typedef typename Mma16<T>::v8 v8;
@@ -56,7 +70,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_xwt(GemmArgs a) {
     // operands and addresses (otherwise they sit in VGPRs and shuttle through AGPRs as spills).
     asm volatile("" ::: "a0");
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wn = wave >> 1, wm = wave & 1;
     const int n_tiles_n = a.N / BN, n_tiles_m = (a.M + BM - 1) / BM;
     const int total = n_tiles_n * n_tiles_m;
@@ -79,21 +93,26 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_xwt(GemmArgs a) {
     // holding logical chunk (i % 8) ^ swz(row) = (i % 8) ^ (4 (c & 1) + (i / 8) / 2)
     const int crow = lane >> 3, cpc = lane & 7;
     const int lc0 = cpc ^ (crow >> 1), lc1 = cpc ^ (4 + (crow >> 1));
-    const T* const wsrc = (const T*)a.w + (long)(n0 + 64 * wave + crow) * a.ldw;
-    const long xr0 = m0 + 64 * wave + crow;
-    const bool x_tail = m0 + BM > a.M;
-    const T* const xbase = (const T*)a.x;
+    // buffer resources over this tile's 256 W rows and its X rows (rows past M read as zeros);
+    // per-lane byte offsets of the 8 copies are loop-invariant, the K step adds a scalar offset
+    const i32x4_t wrs = buffer_rsrc((const T*)a.w + (long)n0 * a.ldw, (unsigned)(256 * a.ldw * 2));
+    const i32x4_t xrs = buffer_rsrc((const T*)a.x + (long)m0 * a.ldx, (unsigned)(min(BM, a.M - m0) * a.ldx * 2));
+    unsigned wvo[8], xvo[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int lc = (c & 1) ? lc1 : lc0, r = 64 * wave + 8 * c + crow;
+        wvo[c] = (unsigned)((r * a.ldw + 8 * lc) * 2);
+        xvo[c] = (unsigned)((r * a.ldx + 8 * lc) * 2);
+    }
     const unsigned lbase = lds_address(gsm);
     auto load_step = [&](int ks, int buf) {
         const unsigned wb = lbase + buf * 2 * TILE_BYTES, xb = wb + TILE_BYTES;
-        const long ko = (long)ks * BK;
+        const unsigned so = (unsigned)ks * (BK * 2);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            const int lc = (c & 1) ? lc1 : lc0;
             const unsigned dst = (unsigned)((64 * wave + 8 * c) * ROW_BYTES);
-            copy_x4(wsrc + (long)(8 * c) * a.ldw + 8 * lc + ko, wb + dst);
-            const long xr = x_tail ? min(xr0 + 8 * c, (long)a.M - 1) : xr0 + 8 * c;
-            copy_x4(xbase + xr * a.ldx + 8 * lc + ko, xb + dst);
+            buf_copy_x4(wrs, wvo[c], so, wb + dst);
+            buf_copy_x4(xrs, xvo[c], so, xb + dst);
         }
     };
 
