@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
     p.add_argument("--kernel-iters", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--fork-probe", action="store_true",
+                   help="time attention on a suffix batch over a shared prefix, and on private prefix copies")
     p.add_argument("--no-laya", action="store_true",
                    help="kev: skip the Laya encoder measurement that the default run adds to its line")
     p.add_argument("--kernels-only", action="store_true",
@@ -223,6 +225,69 @@ def timed(fn):
     t0 = time.perf_counter()
     fn()
     return time.perf_counter() - t0
+
+
+def fork_probe(iters):
+    """A suffix batch over one shared prefix (the reference's attention_suffix_batch case,
+    kv_pages.rs:180-296): 8 rows whose block tables point at the same 32 prefix pages (512 tokens)
+    plus 2 private pages each for a 24-token suffix, against the same batch with a private copy
+    of the prefix per row. Times both launches; under `rocprofv3 --pmc FETCH_SIZE` the two
+    dispatches give the HBM bytes each reads."""
+    import numpy as np
+    import torch
+
+    from huncho_amd import abi
+    from huncho_amd.kev import KevShape
+    from huncho_amd.ops import context_for_torch, paged_prefill_attention
+
+    shape = KevShape()
+    hq, hkv, d, P = shape.n_heads, shape.n_kv_heads, shape.head_dim, shape.page_size
+    rows, prefix, suffix = 8, 512, 24
+    ctx_len = prefix + suffix
+    pp, sp = prefix // P, (suffix + P - 1) // P
+    dev = torch.device("cuda", 0)
+    ctx = context_for_torch(0)
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    n_pages = rows * (pp + sp)
+    perm = abi.synth_permutation(SEED, 17, n_pages)
+    kp = torch.randn((n_pages, hkv, P, d), generator=g, device=dev).to(torch.bfloat16)
+    vp = torch.randn((n_pages, hkv, P, d), generator=g, device=dev).to(torch.bfloat16)
+    shared = np.zeros((rows, pp + sp), np.int32)
+    private = np.zeros((rows, pp + sp), np.int32)
+    for r in range(rows):
+        shared[r, :pp] = perm[:pp]  # every row reads the same prefix pages
+        shared[r, pp:] = perm[rows * pp + r * sp: rows * pp + (r + 1) * sp]
+        private[r] = perm[r * (pp + sp): (r + 1) * (pp + sp)]
+    # the private batch holds the same prefix values in its own pages
+    src = torch.from_numpy(shared.reshape(-1).astype(np.int64)).to(dev)
+    dst = torch.from_numpy(private.reshape(-1).astype(np.int64)).to(dev)
+    kp2, vp2 = kp.clone(), vp.clone()
+    kp2[dst] = kp[src]
+    vp2[dst] = vp[src]
+    n = rows * suffix
+    qg = torch.randn((n, hq, 2 * d), generator=g, device=dev).to(torch.bfloat16)
+    q, gate = qg[:, :, :d], qg[:, :, d:]
+    cu = torch.arange(0, n + 1, suffix, dtype=torch.int32, device=dev)
+    lens = torch.full((rows,), ctx_len, dtype=torch.int32, device=dev)
+    o1 = torch.empty((n, hq, d), dtype=torch.bfloat16, device=dev)
+    o2 = torch.empty_like(o1)
+    bt1 = torch.from_numpy(shared).to(dev)
+    bt2 = torch.from_numpy(private).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    t1 = time_launches(lambda: paged_prefill_attention(ctx, q, kp, vp, bt1, cu, lens, suffix, gate=gate, out=o1),
+                       iters, stream)
+    t2 = time_launches(lambda: paged_prefill_attention(ctx, q, kp2, vp2, bt2, cu, lens, suffix, gate=gate, out=o2),
+                       iters, stream)
+    torch.cuda.synchronize()
+    page_bytes = hkv * P * d * 2 * 2  # K and V of one page, all KV heads
+    line = {"probe": "suffix batch over a shared prefix", "rows": rows, "prefix_tokens": prefix,
+            "suffix_tokens": suffix, "identical_outputs": bool(torch.equal(o1, o2)),
+            "shared_us": round(t1 * 1e6, 2), "private_us": round(t2 * 1e6, 2),
+            "kv_bytes_unique_shared": (pp + rows * sp) * page_bytes,
+            "kv_bytes_unique_private": rows * (pp + sp) * page_bytes,
+            "q_gate_o_bytes": n * hq * d * 2 * 3}
+    ctx.close()
+    print(json.dumps(line), flush=True)
 
 
 def cpu_baseline(shape, weights, seq_len, threads, n_seqs=12):
@@ -513,6 +578,9 @@ def main():
         log(f"copied {src.numel() * 4} bytes 3 times")
         return
     dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    if args.fork_probe:
+        fork_probe(args.kernel_iters)
+        return
     if args.kernels_only:
         from huncho_amd.ops import context_for_torch
 
