@@ -63,6 +63,22 @@ def test_store_and_residual(ctx, dtype, rows, n, k):
     assert torch.equal(r2, y2)
 
 
+@pytest.mark.parametrize("rows,n,k", [(8269, 2048, 256), (25500, 768, 128)])
+def test_more_tiles_than_workgroups(ctx, rows, n, k):
+    """One workgroup per CU walks several 256x256 tiles (264 and 300 tiles: a second tile for
+    some workgroups, a tile count that is and one that is not a multiple of 8, ragged last rows)."""
+    dtype = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(rows + n)
+    x = (torch.randn((rows, k), generator=g, device="cuda") * 0.5).to(dtype)
+    w = (torch.randn((n, k), generator=g, device="cuda") * 0.05).to(dtype)
+    ref = x.double() @ w.double().T
+    y = linear(ctx, x, w)
+    assert within_ulp(y, ref.to(dtype), dtype, 1, k), float((y.double() - ref).abs().max())
+    r = torch.randn((rows, n), generator=g, device="cuda").to(dtype)
+    y2 = linear(ctx, x, w, epi=1, c=r)
+    assert within_ulp(y2, (ref + r.double()).to(dtype), dtype, 1, k)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_swiglu_epilogue(ctx, dtype):
     rows, inter, k = 777, 384, 256
