@@ -39,8 +39,9 @@ struct Plan {
 };
 
 // Solution indices pinned per (dtype, out, n, in, C operand) at the Kev-shaped 64 x 512 token
-// batch, measured on MI355X (gfx950) with ROCm 7.2's hipBLASLt by timing every supported
-// solution (hk_ctx_set_gemm_autotune) and keeping the fastest.
+// batch and the ModernBERT-base-shaped 16-row batch (40,910 tokens), measured on MI355X (gfx950)
+// with ROCm 7.2's hipBLASLt by timing every supported solution (hk_ctx_set_gemm_autotune) and
+// keeping the fastest.
 struct Pinned {
     int dtype, out, n, in, has_c, index;
 };
@@ -54,6 +55,10 @@ const Pinned kPinned[] = {
     {HK_F16, 32, 32768, 1024, 0, 625072},    {HK_F16, 1024, 32768, 2048, 1, 625107},
     {HK_F16, 1024, 32768, 3584, 1, 624960},  {HK_F16, 6144, 32768, 1024, 0, 625108},
     {HK_F16, 7168, 32768, 1024, 0, 625108},  {HK_F16, 8192, 32768, 1024, 0, 625108},
+    // bf16 ModernBERT-base: Wqkv and Wi (GeGLU) 768 -> 2304, attention Wo (+ residual),
+    // MLP Wo 1152 -> 768 (+ residual); 2.5 % of the encoder step over the heuristic's choices
+    {HK_BF16, 2304, 40910, 768, 0, 618611},  {HK_BF16, 768, 40910, 768, 1, 618611},
+    {HK_BF16, 768, 40910, 1152, 1, 618612},
 };
 
 typedef std::tuple<int, int, int, int, long, long, long, long, int> Key;
