@@ -38,6 +38,14 @@ __device__ __forceinline__ int vswz(int r) { return ((r & 3) << 1) | ((r >> 4) &
 __device__ __forceinline__ int k_off(int r, int c) { return r * D + 8 * (c ^ kswz(r)); }
 __device__ __forceinline__ int v_off(int r, int c) { return r * D + 8 * (c ^ vswz(r)); }
 
+// NeoX rotate-half pair (x_i, x_{i+32}) at one position, in fp32, each result rounded to T; the
+// same code in rope_qk and in the attention kernel's fused q rotation, so both round alike
+template <typename T>
+__device__ __forceinline__ void rope_pair(float a1, float a2, float c, float s, T& r1, T& r2) {
+    r1 = from_f<T>(a1 * c - a2 * s);
+    r2 = from_f<T>(a2 * c + a1 * s);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
     typedef typename Mma16<T>::v8 v8;
@@ -69,6 +77,28 @@ __global__ __launch_bounds__(256, 2) void bidir_attn_16(BertAttnArgs a) {
         const T* qp = (const T*)a.q + (long)(t0 + (q_valid ? p : 0)) * a.q_tok + (long)h * D;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qf[ks] = q_valid ? *(const v8*)(qp + ks * 16 + g * 8) : v8{};
+    }
+    if (a.rope_cos) {
+        // NeoX rotate-half RoPE of this lane's query row as it is loaded (the model's q RoPE;
+        // rope_qk then rotates k only): dims 16 ks + 8 g + e, ks = 0, 1, pair with the dims 32
+        // higher, which the same lane holds in qf[ks + 2]
+        if (q_valid && p >= a.rope_max_pos) atomicOr(a.fault, 4);
+        const int pr = min(q_valid ? p : 0, a.rope_max_pos - 1);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const float* cs = a.rope_cos + (long)pr * 32 + ks * 16 + g * 8;
+            const float* sn = a.rope_sin + (long)pr * 32 + ks * 16 + g * 8;
+            const f32x4 c0 = *(const f32x4*)cs, c1 = *(const f32x4*)(cs + 4);
+            const f32x4 s0 = *(const f32x4*)sn, s1 = *(const f32x4*)(sn + 4);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                T r1, r2;
+                rope_pair<T>((float)qf[ks][e], (float)qf[ks + 2][e], e < 4 ? c0[e] : c1[e - 4], e < 4 ? s0[e] : s1[e - 4],
+                             r1, r2);
+                qf[ks][e] = r1;
+                qf[ks + 2][e] = r2;
+            }
+        }
     }
     // keys any query of the block may see
     const int blk_lo = qb * 128, blk_hi = min(L, qb * 128 + 128) - 1;
@@ -407,10 +437,10 @@ __global__ __launch_bounds__(256) void rope_qk(RopeQkArgs a) {
         if (threadIdx.x == 0) atomicOr(a.fault, 4);
         return;
     }
-    const int per_tok = 2 * a.heads * UPH;
+    const int per_tok = (a.k_only ? 1 : 2) * a.heads * UPH;
     for (int u = threadIdx.x; u < rows * per_tok; u += blockDim.x) {
         const int pp = p0 + u / per_tok, w = u % per_tok;
-        const int hh = w / UPH, i0 = (w % UPH) * N;
+        const int hh = (a.k_only ? a.heads : 0) + w / UPH, i0 = (w % UPH) * N;
         T* xh = (T*)a.x + (long)(t0 + pp) * a.x_tok + hh * 64 + i0;
         const float* cs = a.cos + (long)pp * 32 + i0;
         const float* sn = a.sin + (long)pp * 32 + i0;
@@ -421,18 +451,20 @@ __global__ __launch_bounds__(256) void rope_qk(RopeQkArgs a) {
                 const f32x4 c = *(const f32x4*)(cs + h), sv = *(const f32x4*)(sn + h);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float a1 = (float)x1[h + e], a2 = (float)x2[h + e];
-                    r1[h + e] = from_f<T>(a1 * c[e] - a2 * sv[e]);
-                    r2[h + e] = from_f<T>(a2 * c[e] + a1 * sv[e]);
+                    T t1, t2;
+                    rope_pair<T>((float)x1[h + e], (float)x2[h + e], c[e], sv[e], t1, t2);
+                    r1[h + e] = t1;
+                    r2[h + e] = t2;
                 }
             }
             *(V*)xh = r1;
             *(V*)(xh + 32) = r2;
         } else {
             const float c = cs[0], sv = sn[0];
-            const float x1 = to_f(xh[0]), x2 = to_f(xh[32]);
-            xh[0] = from_f<T>(x1 * c - x2 * sv);
-            xh[32] = from_f<T>(x2 * c + x1 * sv);
+            T t1, t2;
+            rope_pair<T>(to_f(xh[0]), to_f(xh[32]), c, sv, t1, t2);
+            xh[0] = t1;
+            xh[32] = t2;
         }
     }
 }

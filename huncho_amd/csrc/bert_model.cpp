@@ -244,12 +244,21 @@ extern "C" int hk_bert_forward(hk_bert_model* m, const int32_t* ids, const int32
             src = b.x;
         }
         BRUN(hk_gemm_xwt(ctx, dt, n, 3 * H, H, src, H, L.wqkv, H, b.qkv, 3 * H, nullptr, 0, 1.0f, 0.0f));
-        hk::RopeQkArgs ra{b.qkv, 3L * H, global ? m->cos_g : m->cos_l, global ? m->sin_g : m->sin_l, c.max_context, nh,
-                          cu_dev, n_seqs, n, ctx->fault_dev};
+        // 16-bit: the attention kernel rotates q as it loads it, so rope_qk rotates k only
+        const bool q_in_attn = dt != HK_F32;
+        const float* rcos = global ? m->cos_g : m->cos_l;
+        const float* rsin = global ? m->sin_g : m->sin_l;
+        hk::RopeQkArgs ra{b.qkv, 3L * H, rcos, rsin, c.max_context, nh, cu_dev, n_seqs, n, ctx->fault_dev,
+                          q_in_attn ? 1 : 0};
         BRUN(hk_launch_rope_qk(dt, &ra, n_seqs, max_len, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "rope launch") : 0);
         char* q = (char*)b.qkv;
         hk::BertAttnArgs aa{q, 3L * H, q + (size_t)H * e, 3L * H, q + (size_t)2 * H * e, 3L * H, b.att, (long)H,
                             cu_dev, n_seqs, n, nh, global ? -1 : c.local_window / 2, scale_log2, ctx->fault_dev};
+        if (q_in_attn) {
+            aa.rope_cos = rcos;
+            aa.rope_sin = rsin;
+            aa.rope_max_pos = c.max_context;
+        }
         BRUN(hk_launch_bidir_attention(dt, &aa, n_seqs, max_len, ctx->stream) ? hk_fail(ctx, HK_ERR_DEVICE, "attention launch")
                                                                                : 0);
         BRUN(hk_gemm_xwt(ctx, dt, n, H, H, b.att, H, L.wo, H, b.h, H, b.h, H, 1.0f, 1.0f));

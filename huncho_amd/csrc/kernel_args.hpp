@@ -175,6 +175,11 @@ struct BertAttnArgs {
     float scale_log2;  // softmax scale * log2(e)
     int* fault;
     int qblocks;  // query blocks per (sequence, head) in the 16-bit grid (set by the launcher)
+    // optional NeoX RoPE of q applied as the 16-bit kernel loads it ([max_pos][32] tables;
+    // null: q is used as given)
+    const float* rope_cos;
+    const float* rope_sin;
+    int rope_max_pos;
 };
 
 struct LayerNormArgs {
@@ -244,6 +249,7 @@ struct RopeQkArgs {
     const int* cu;
     int n_seqs, n_tokens;
     int* fault;
+    int k_only;  // rotate only the k part (q is rotated by the attention kernel as it loads it)
 };
 
 // Mean-pool partial sums per sequence (slot rows of MeanPoolArgs::pool).
