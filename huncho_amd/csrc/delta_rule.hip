@@ -22,7 +22,7 @@
 // instead of transposing the data. Inputs stream from HBM once: q, k, v, g, beta in, o out.
 //
 // This file holds the fp32 variant (v_mfma_f32_32x32x2_f32, the fp32 model path); the 16-bit
-// variants and the fused Gated DeltaNet layer kernel live in gdn16.hip.
+// variants and the fused Gated DeltaNet layer kernel live in gdn16_kernel.hpp.
 #include "common.hpp"
 #include "kernel_args.hpp"
 

@@ -1,682 +1,15 @@
-// gdn16.hip - chunked gated delta rule for 16-bit activations (bf16 / fp16) on gfx950, with
-// an optional fused Gated DeltaNet prologue and epilogue.
-//
-// Recurrence (crates/huncho-backend/src/delta_cpu.rs:95-131, qwen3_5.rs:950-987), per token t:
-//   S <- S exp(g_t); delta_t = beta_t (v_t - S^T k_t); S <- S + k_t delta_t^T; o_t = S^T q_t
-// evaluated in the equal chunked form (chunk 64, G = inclusive cumsum of g in the chunk):
-//   A = strict_lower(beta_t exp(G_t - G_s) k_t.k_s),  T = (I + A)^-1
-//   delta = T [beta (V - exp(G) K S0)],  O = exp(G) Q S0 + lower(exp(G_t - G_s) q_t.k_s) delta
-//   S1 = exp(G_last) S0 + K^T [exp(G_last - G) delta]
-// Only decay ratios exp(G_t - G_s) with t >= s (each <= 1) are used.
-//
-// Two modes (template FUSED):
-//   standalone  q, k [tokens][k_heads][128], v [tokens][heads][128], g, beta fp32 -> o
-//   fused       the Gated DeltaNet layer body of LinearAttn::forward (qwen3_5.rs:846-940)
-//               straight from the fused in_proj output rows [q | k | v | z | b | a]:
-//               causal depthwise conv (K = 4, ascending taps, conv_cpu.rs:34-48) + SiLU,
-//               l2norm of q and k, q * 128^-1/2, beta = sigmoid(b),
-//               g = -exp(A_log) softplus(a + dt_bias), the recurrence, then the gated
-//               RMSNorm rms(o) * w * silu(z) (193-201) -> out_proj input
-// so one kernel streams each layer's q|k|v|z|b|a once and writes one output row per token.
-//
-// Work split: one workgroup of 4 waves (256 threads) per (sequence, value head), two
-// workgroups per CU (79,360 B of LDS each, <= 256 registers per lane), so 2 waves share each
-// SIMD. Wave w owns value columns 32w..32w+31 of the fp32 state S [128 x 128] as two 16-column
-// tiles, held for the whole sequence in sixteen 16x16 MFMA accumulators (v_mfma_f32_16x16x32_f16
-// for both activation dtypes; lane l: column l % 16, rows 4 (l / 16) + r). Intermediates (K S,
-// R, delta) stay in accumulator layout and feed the next product as its B operand: each
-// product's reduction index is permuted to the
-// accumulator's row order (element e of lane group q <-> index 32 s + 4 q + e, or
-// 32 s + 16 + 4 q + e - 4 for e >= 4), and the A operands are read from LDS in that order.
-//
-// Chunk pipeline:
-//   P0  global -> LDS: q, k, v rows (fused: all four waves run the conv, SiLU and l2norm,
-//       4 rows of each tensor per 16-lane group); wave 3: g scan and beta
-//   P1  16x16 tiles of K K^T and Q K^T -> A (fp32, masked, decayed) and Aqk (16-bit);
-//       every wave: K S0, Q S0 for its columns -> R = beta (V - e^G K S0), e^G Q S0
-//   P2  the four 16x16 diagonal blocks of T = (I + A)^-1 in place (waves 0-3)
-//   P3  delta = T R by block forward substitution, O = e^G Q S0 + Aqk delta (staged in LDS
-//       over V), S update with the K^T operand read through transposing LDS reads
-//   P4  O (or the gated-normed O) -> HBM with 16-byte stores
-#include "common.hpp"
-#include "kernel_args.hpp"
+// gdn16.hip - the fused Gated DeltaNet layer instantiations of gdn_chunk16 (the kernel is in
+// gdn16_kernel.hpp) and the 16-bit delta-rule launcher. The standalone recurrence is
+// instantiated in gdn16_standalone.hip, which the build compiles with its own machine
+// scheduling strategy.
+#include "gdn16_kernel.hpp"
 
-namespace hk {
-namespace gdn16 {
-
-template <typename T> struct M16;
-template <> struct M16<bf16> {
-    typedef bf16x8 v8;
-    typedef bf16x4 v4;
-    typedef bf16x2 v2;
-    static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ f32x4 mma16(v4 a, v4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c,
-                                                         0, 0, 0);
-    }
-};
-template <> struct M16<f16> {
-    typedef f16x8 v8;
-    typedef f16x4 v4;
-    typedef f16x2 v2;
-    static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ f32x4 mma16(v4 a, v4 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-    }
-};
-
-template <typename T> __device__ __forceinline__ float f(T x) { return (float)x; }
-template <typename T> __device__ __forceinline__ float rnd(float x) { return (float)(T)x; }
-
-// a.x b.x + a.y b.y as one VOP3P instruction with an inline zero accumulator (the builtin's
-// accumulating VOP2 form first copies the zero into its destination register)
-__device__ __forceinline__ float dot2_0(bf16x2 a, bf16x2 b) {
-    float d;
-    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
-    return d;
-}
-__device__ __forceinline__ float dot2_0(f16x2 a, f16x2 b) {
-    float d;
-    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
-    return d;
-}
-// The two halves of a packed 16-bit pair in fp32 (bf16: a shift and a mask). The empty asm
-// hides the pair's origin, or the compiler rebuilds each half from its own single conversion.
-__device__ __forceinline__ unsigned opaque(bf16x2 p) {
-    unsigned u = __builtin_bit_cast(unsigned, p);
-    asm("" : "+v"(u));
-    return u;
-}
-__device__ __forceinline__ float lo_f(bf16x2 p) { return __builtin_bit_cast(float, opaque(p) << 16); }
-__device__ __forceinline__ float hi_f(bf16x2 p) { return __builtin_bit_cast(float, opaque(p) & 0xffff0000u); }
-__device__ __forceinline__ float lo_f(f16x2 p) { return (float)p[0]; }
-__device__ __forceinline__ float hi_f(f16x2 p) { return (float)p[1]; }
-// (a, b) rounded to T (one packed conversion), then held as an fp16 pair: the fp16 MFMA operand
-// of two values stored in the activation dtype (bf16 values in range are exact in fp16)
-__device__ __forceinline__ f16x2 to_ct(bf16x2 p) { return f16x2{(f16)lo_f(p), (f16)hi_f(p)}; }
-__device__ __forceinline__ f16x2 to_ct(f16x2 p) { return p; }
-template <typename T> __device__ __forceinline__ f16x2 rnd_ct(float a, float b) {
-    return to_ct(typename M16<T>::v2{(T)a, (T)b});
-}
-
-constexpr int CH = 64, DK = 128, DV = 128, NTHREADS = 256;
-constexpr int RS = DK + 8;  // row stride (elements) of the Q / K / V tiles [64][136]
-constexpr int AS = CH + 4;  // fp32 row stride of A / T [64][68]
-constexpr int TS = CH + 8;  // row stride of Aqk [64][72]
-// Q, K, V [64][136] each, A, Aqk, g scan, beta: 79,360 B (two workgroups fit a CU's 160 KiB)
-constexpr size_t LDS_BYTES = 3 * CH * RS * 2 + CH * AS * 4 + CH * TS * 2 + 2 * CH * 4;
-
-// Element offset of column x of row r in a Q / K / V tile. The 16-byte row padding moves each
-// row 4 banks on, so 16-byte reads of 16 consecutive rows are conflict-free; and every
-// unrolled access is one per-lane base plus an instruction offset.
-__device__ __forceinline__ int el(int r, int x) { return r * RS + x; }
-
-__device__ __forceinline__ float silu(float x) { return fast_silu(x); }
-
-__device__ __forceinline__ float wave_incl_scan(float x, int lane) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        float y = __shfl_up(x, d);
-        if (lane >= d) x += y;
-    }
-    return x;
-}
-
-// In place, the inverses T_bb = (I + A_bb)^-1 of the four 16x16 diagonal blocks of the
-// strictly lower A [64][AS], by forward substitution on waves 0-3 (wave w: block w, lane j:
-// column j). The strictly lower part of each solved block keeps its zeros above the diagonal.
-// Kept out of line: inlined, its unrolled row loads would be hoisted together and spill the
-// caller.
-__device__ __attribute__((noinline)) void solve_diagonal_blocks(float* Am, int wave, int lane) {
-    if (wave >= 4) return;
-    const int b = wave * 16, j = lane & 15;
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float* row = Am + (b + i) * AS + b;
-        float a0 = (i == j) ? 1.0f : 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll
-        for (int k = 0; k + 3 < i; k += 4) {
-            f32x4 rv = *(const f32x4*)(row + k);
-            a0 -= rv[0] * x[k];
-            a1 -= rv[1] * x[k + 1];
-            a2 -= rv[2] * x[k + 2];
-            a3 -= rv[3] * x[k + 3];
-        }
-#pragma unroll
-        for (int k = i & ~3; k < i; ++k) a0 -= row[k] * x[k];
-        x[i] = (a0 + a1) + (a2 + a3);
-    }
-    if (lane < 16) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) Am[(b + i) * AS + b + j] = x[i];
-    }
-}
-
-// Two runs of four 16-bit elements of a Q / K row: columns x0 .. x0 + 3 and x0 + 16 .. + 19
-// (the permuted reduction order of one 32-wide k-step).
-template <typename T>
-__device__ __forceinline__ typename M16<T>::v8 ld_pair(const T* tile, int r, int x0) {
-    typedef typename M16<T>::v4 v4;
-    const v4 lo = *(const v4*)(tile + el(r, x0));
-    const v4 hi = *(const v4*)(tile + el(r, x0 + 16));
-    return typename M16<T>::v8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-// The same two runs from a plain row-major row (Aqk)
-template <typename T>
-__device__ __forceinline__ typename M16<T>::v8 ld_pair_plain(const T* row, int x0) {
-    typedef typename M16<T>::v4 v4;
-    const v4 lo = *(const v4*)(row + x0);
-    const v4 hi = *(const v4*)(row + x0 + 16);
-    return typename M16<T>::v8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-// Accumulator tiles a (elements 0-3) and b (4-7) as one 16-bit B operand
-template <typename T>
-__device__ __forceinline__ typename M16<T>::v8 pack2(f32x4 a, f32x4 b) {
-    return typename M16<T>::v8{(T)a[0], (T)a[1], (T)a[2], (T)a[3], (T)b[0], (T)b[1], (T)b[2], (T)b[3]};
-}
-template <typename T>
-__device__ __forceinline__ typename M16<T>::v4 pack1(f32x4 a) {
-    return typename M16<T>::v4{(T)a[0], (T)a[1], (T)a[2], (T)a[3]};
-}
-// Four fp32 elements of A / T (row r, columns c .. c + 3) as a 16-bit operand, optionally negated
-template <typename T, bool NEG>
-__device__ __forceinline__ typename M16<T>::v4 ld_a4(const float* Am, int r, int c) {
-    const f32x4 x = *(const f32x4*)(Am + r * AS + c);
-    return NEG ? typename M16<T>::v4{(T)-x[0], (T)-x[1], (T)-x[2], (T)-x[3]}
-               : typename M16<T>::v4{(T)x[0], (T)x[1], (T)x[2], (T)x[3]};
-}
-
-template <typename T, bool FUSED>
-__global__ __launch_bounds__(256, 2) void gdn_chunk16(GdnArgs a, GdnFusedArgs fa) {
-    // MFMA operands and LDS tiles are fp16 (CT) for both activation dtypes: bf16 activations
-    // are exact in fp16 (inside its range), and every intermediate rounded to an operand (R, A,
-    // T, delta, the state S, Aqk) keeps 11 significant bits instead of bf16's 8. The reference
-    // runs this recurrence in fp32 (delta_cpu.rs:95-131); its activation-dtype storage points
-    // (the conv output, beta, the recurrence output) are rounded to T, and the normalised q and
-    // k, which it keeps in fp32, only to the fp16 operand (fused mode; standalone mode takes q
-    // and k in T).
-    typedef f16 CT;
-    typedef typename M16<CT>::v8 v8;
-    typedef typename M16<CT>::v4 v4;
-    typedef typename M16<T>::v8 tv8;
-    typedef typename M16<T>::v2 tv2;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    CT* Qs = (CT*)smem;                   // [64][RS]
-    CT* Ks = Qs + CH * RS;                // [64][RS]
-    CT* Vs = Ks + CH * RS;                // [64][RS]; O staging in P3
-    float* Am = (float*)(Vs + CH * RS);   // [64][AS]: A, then the diagonal blocks of T
-    CT* Aq = (CT*)(Am + CH * AS);         // [64][TS]
-    float* Gs = (float*)(Aq + CH * TS);
-    float* Bs = Gs + CH;
-
-    const int h = blockIdx.x, seq = blockIdx.y, H = a.H;
-    const int t0 = a.cu_seqlens[seq];
-    const int Tn = a.cu_seqlens[seq + 1] - t0;
-    if (t0 < 0 || Tn < 0 || t0 + Tn > a.n_tokens) {
-        if (threadIdx.x == 0) atomicOr(a.fault, 1);
-        return;
-    }
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int kh = h / a.qk_rep;
-    // this sequence's state rows and conv rows (per-row pointer tables or contiguous arrays)
-    const float* const s0 = a.init_rows ? a.init_rows[seq]
-                                        : (a.initial_state ? a.initial_state + (long)seq * H * DK * DV : nullptr);
-    float* const s1 = a.final_rows ? a.final_rows[seq]
-                                   : (a.final_state ? a.final_state + (long)seq * H * DK * DV : nullptr);
-    const T* const hist = !FUSED ? nullptr
-                          : fa.hist_rows ? (const T*)fa.hist_rows[seq]
-                                         : (fa.hist ? (const T*)fa.hist + (long)seq * fa.conv_dim * 3 : nullptr);
-    T* const tail = !FUSED ? nullptr
-                    : fa.tail_rows ? (T*)fa.tail_rows[seq]
-                                   : (fa.tail_out ? (T*)fa.tail_out + (long)seq * fa.conv_dim * 3 : nullptr);
-    const long sbase = (long)h * DK * DV;
-
-    // state: column tile cw (value columns 32 wave + 16 cw + l % 16), row tile rb (dk rows
-    // 16 rb + 4 (l / 16) + r)
-    f32x4 S[2][8];
-    if (s0) {
-        const float* sp = s0 + sbase + (long)(4 * (lane >> 4)) * DV + 32 * wave + (lane & 15);
-#pragma unroll
-        for (int cw = 0; cw < 2; ++cw)
-#pragma unroll
-            for (int rb = 0; rb < 8; ++rb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) S[cw][rb][r] = sp[(16 * rb + r) * DV + 16 * cw];
-    } else {
-#pragma unroll
-        for (int cw = 0; cw < 2; ++cw)
-#pragma unroll
-            for (int rb = 0; rb < 8; ++rb) S[cw][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    // conv-tail lanes (waves 0-2): tensor wave (q, k, v), channels 8 j .. + 7 of the head;
-    // mixed column mcol + 8 j
-    const long mcol = (long)kh * 128 + wave * (long)fa.Hk * 128 + (wave == 2 ? (long)(h - kh) * 128 : 0);
-
-    bool range_bad = false;  // a non-finite output row (fp16 operand range exceeded)
-    for (int c0 = 0; c0 < Tn; c0 += CH) {
-        const int Lc = min(CH, Tn - c0);
-        // lane indices re-formed every chunk, so the compiler builds the per-lane LDS
-        // addresses here instead of holding dozens of them across the loop
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const int q4 = ln >> 4, j = ln & 15;
-        __syncthreads();
-        // ---------------- P0: inputs -> LDS ----------------
-        if (FUSED) {
-            // 16 lane groups (4 per wave) x 4 rows of each of q, k and v: group G = 4 wave + q4
-            // takes chunk rows 4 G .. 4 G + 3 of every tensor, so all four waves share the conv,
-            // SiLU and l2norm evenly. Each tensor's 4 conv outputs come from a 7-row window of raw
-            // conv inputs (sequence positions c0 + 4 G - 3 ..). Positions past the sequence end
-            // are loaded clamped: they only reach rows past the end, whose beta is 0 and whose
-            // outputs are not stored. Positions before the start are the conv history or 0.
-            const int r0 = 4 * (4 * wave + q4);
-            auto tcol = [&](int tsr) {  // mixed column of this lane's channels in tensor tsr
-                return (tsr == 2 ? 2 * (long)fa.Hk * 128 + (long)h * 128 : (long)tsr * fa.Hk * 128 + (long)kh * 128) +
-                       8 * j;
-            };
-            // all three windows are loaded before the first conv, so the chunk waits for one
-            // memory round trip
-            // Addresses: a wave-uniform base per tensor (this sequence's first row, the head's
-            // columns) plus one 32-bit byte offset per row shared by the three tensors (the host
-            // keeps n_tokens * mixed_tok * sizeof(T) below 2^32 and the row stride below 2^24)
-            tv8 raw[3][7];
-            {
-                const char* const mb = (const char*)fa.mixed + (long)t0 * fa.mixed_tok * (long)sizeof(T);
-                const char* const base[3] = {mb + (long)kh * 128 * sizeof(T),
-                                             mb + ((long)fa.Hk + kh) * 128 * sizeof(T),
-                                             mb + (2L * fa.Hk + h) * 128 * sizeof(T)};
-                const unsigned row_b = (unsigned)(fa.mixed_tok * sizeof(T));
-#pragma unroll
-                for (int i = 0; i < 7; ++i) {
-                    const int p = c0 + r0 - 3 + i;
-                    const unsigned pc = (unsigned)(p < 0 ? 0 : (p >= Tn ? Tn - 1 : p));
-                    const unsigned off = __umul24(pc, row_b) + 16u * j;
-#pragma unroll
-                    for (int tsr = 0; tsr < 3; ++tsr) raw[tsr][i] = *(const tv8*)(base[tsr] + off);
-                }
-            }
-            if (c0 + r0 == 0) {  // windows start 3 positions before the sequence
-#pragma unroll
-                for (int tsr = 0; tsr < 3; ++tsr) {
-                    if (hist) {
-                        const T* hb = hist + tcol(tsr) * 3;
-#pragma unroll
-                        for (int i = 0; i < 3; ++i)
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) raw[tsr][i][e] = hb[e * 3 + i];
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 3; ++i) raw[tsr][i] = tv8{};
-                    }
-                }
-            }
-#pragma unroll
-            for (int tsr = 0; tsr < 3; ++tsr) {
-                const long mct = tcol(tsr);
-                CT* dst = tsr == 0 ? Qs : tsr == 1 ? Ks : Vs;
-                // taps (0, 1) and (2, 3) of each channel as 16-bit pairs (the weights are the
-                // model dtype's values, exact in T)
-                tv2 w01[8], w23[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const f32x4 w4 = *(const f32x4*)(fa.conv_w + (mct + e) * 4);
-                    w01[e] = tv2{(T)w4[0], (T)w4[1]};
-                    w23[e] = tv2{(T)w4[2], (T)w4[3]};
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float y[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float acc = dot2(w23[e], tv2{raw[tsr][i + 2][e], raw[tsr][i + 3][e]},
-                                               dot2_0(w01[e], tv2{raw[tsr][i][e], raw[tsr][i + 1][e]}));
-                        y[e] = silu(acc);
-                    }
-                    // the conv output is stored in T (qwen3_5.rs:843), held exactly in CT
-                    f16x2 o[4];
-                    if (tsr < 2) {  // conv output stored in the activation dtype, then l2norm over
-                                    // the head's 128 channels (16 lanes); q also takes the scale
-                        tv2 p[4];
-#pragma unroll
-                        for (int m = 0; m < 4; ++m) p[m] = tv2{(T)y[2 * m], (T)y[2 * m + 1]};
-                        float ss = dot2_0(p[0], p[0]);
-#pragma unroll
-                        for (int m = 1; m < 4; ++m) ss = dot2(p[m], p[m], ss);
-                        ss = sum16(ss);
-                        const float inv = fast_rsqrt(ss + 1e-6f) * (tsr == 0 ? fa.scale : 1.0f);
-                        // the normalised q and k stay fp32 in the reference (l2norm returns
-                        // fp32, qwen3_5.rs:204-210, 923-924): rounded only to the fp16 operand
-#pragma unroll
-                        for (int m = 0; m < 4; ++m) o[m] = f16x2{(f16)(lo_f(p[m]) * inv), (f16)(hi_f(p[m]) * inv)};
-                    } else {
-#pragma unroll
-                        for (int m = 0; m < 4; ++m) o[m] = rnd_ct<T>(y[2 * m], y[2 * m + 1]);
-                    }
-                    *(v8*)(dst + el(r0 + i, 8 * j)) = __builtin_bit_cast(v8, o);
-                }
-            }
-        } else {
-            // 3 tensors x 64 rows x 16 chunks = 12 chunks per lane; 16 lanes per row
-            tv8 x[12];
-#pragma unroll
-            for (int i = 0; i < 12; ++i) {
-                const int tsr = i >> 2, r = 16 * (i & 3) + (tid >> 4);
-                const T* src = tsr == 0 ? (const T*)a.q + (long)kh * DK
-                             : tsr == 1 ? (const T*)a.k + (long)kh * DK : (const T*)a.v + (long)h * DV;
-                const long tok = tsr == 0 ? a.q_tok : tsr == 1 ? a.k_tok : a.v_tok;
-                x[i] = *(const tv8*)(src + (long)(t0 + c0 + (r < Lc ? r : Lc - 1)) * tok + 8 * j);
-                if (r >= Lc) x[i] = tv8{};
-            }
-#pragma unroll
-            for (int i = 0; i < 12; ++i) {
-                const int tsr = i >> 2, r = 16 * (i & 3) + (tid >> 4);
-                CT* dst = tsr == 0 ? Qs : tsr == 1 ? Ks : Vs;
-                v8 c;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) c[e] = (CT)f(x[i][e]);
-                *(v8*)(dst + el(r, 8 * j)) = c;
-            }
-        }
-        if (wave == 3) {  // g (inclusive scan over the chunk) and beta
-            float gv = 0.0f, bv = 0.0f;
-            if (lane < Lc) {
-                const long tt = t0 + c0 + lane;
-                if (FUSED) {
-                    const T* row = (const T*)fa.ba + tt * fa.ba_tok;
-                    const float b = f(row[fa.b_col + h]);
-                    const float av = f(row[fa.a_col + h]);
-                    bv = rnd<T>(fast_sigmoid(b));
-                    gv = fa.base_g[h] * __logf(__expf(av + fa.dt_bias[h]) + 1.0f);
-                } else {
-                    gv = a.g[tt * a.gb_tok + h];
-                    bv = a.beta[tt * a.gb_tok + h];
-                }
-            }
-            Gs[lane] = wave_incl_scan(gv, lane);
-            Bs[lane] = bv;
-        }
-        __syncthreads();
-        // ---------------- P1: A, Aqk tiles; K S0, Q S0 ----------------
-        // lower tile pairs p = (ti, si), si <= ti: wave w takes pairs w, w + 4, w + 8; upper tiles
-        // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3) of A and Aqk are zeroed, wave w taking w and w + 4.
-        // The products are formed transposed (K_s as the A operand): lane (q4, j) holds keys
-        // s = 16 si + 4 q4 + r of query / key row t = 16 ti + j, four consecutive columns of
-        // row t of A and Aqk, written as one vector each.
-        for (int p = wave; p < 10; p += 4) {
-            const int ti = p < 1 ? 0 : p < 3 ? 1 : p < 6 ? 2 : 3;
-            const int si = p - (ti * (ti + 1)) / 2;
-            f32x4 kk = f32x4{0.f, 0.f, 0.f, 0.f}, qk = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const v8 ka = *(const v8*)(Ks + el(16 * si + j, 32 * ks + 8 * q4));
-                kk = M16<CT>::mma(ka, *(const v8*)(Ks + el(16 * ti + j, 32 * ks + 8 * q4)), kk);
-                qk = M16<CT>::mma(ka, *(const v8*)(Qs + el(16 * ti + j, 32 * ks + 8 * q4)), qk);
-            }
-            const int t = 16 * ti + j, s4 = 16 * si + 4 * q4;
-            const float gt = Gs[t], bt = Bs[t];
-            const f32x4 gs = *(const f32x4*)(Gs + s4);
-            f32x4 av, qv;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int s = s4 + r;
-                // exp(G_t - G_s) may overflow above the diagonal; the selects drop it there
-                const float ex = __expf(gt - gs[r]);
-                const float dec = s <= t ? ex : 0.0f;
-                av[r] = s < t ? bt * dec * kk[r] : 0.0f;
-                qv[r] = dec * qk[r];
-            }
-            *(f32x4*)(Am + t * AS + s4) = av;
-            *(v4*)(Aq + t * TS + s4) = pack1<CT>(qv);
-        }
-        for (int u = wave; u < 6; u += 4) {
-            const int ti = u < 3 ? 0 : u < 5 ? 1 : 2;
-            const int si = u < 3 ? u + 1 : u < 5 ? u - 1 : 3;
-            const int t = 16 * ti + j, s4 = 16 * si + 4 * q4;
-            *(f32x4*)(Am + t * AS + s4) = f32x4{0.f, 0.f, 0.f, 0.f};
-            *(v4*)(Aq + t * TS + s4) = v4{};
-        }
-        // per token tile tt and column tile cw: R = beta (V - e^G K S0) and, transposed (lane
-        // (q4, j): value columns 16 cw + 4 q4 + r of token 16 tt + j), Og = e^G Q S0
-        f32x4 R[2][4], Og[2][4];
-        {
-            v8 Sb[2][4];  // S as the B operand of K S0 / Q S0 (k-step s: dk 32 s ..)
-#pragma unroll
-            for (int cw = 0; cw < 2; ++cw)
-#pragma unroll
-                for (int s = 0; s < 4; ++s) Sb[cw][s] = pack2<CT>(S[cw][2 * s], S[cw][2 * s + 1]);
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                f32x4 ksa[2], qsa[2];
-#pragma unroll
-                for (int cw = 0; cw < 2; ++cw) ksa[cw] = qsa[cw] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const v8 kop = ld_pair<CT>(Ks, 16 * tt + j, 32 * s + 4 * q4);
-                    const v8 qop = ld_pair<CT>(Qs, 16 * tt + j, 32 * s + 4 * q4);
-#pragma unroll
-                    for (int cw = 0; cw < 2; ++cw) {
-                        ksa[cw] = M16<CT>::mma(kop, Sb[cw][s], ksa[cw]);
-                        qsa[cw] = M16<CT>::mma(Sb[cw][s], qop, qsa[cw]);  // (Q S0)^T
-                    }
-                }
-                const f32x4 gt = *(const f32x4*)(Gs + 16 * tt + 4 * q4);
-                const f32x4 bt = *(const f32x4*)(Bs + 16 * tt + 4 * q4);
-                const float egj = __expf(Gs[16 * tt + j]);  // e^G of the token of (Q S0)^T
-#pragma unroll
-                for (int cw = 0; cw < 2; ++cw) {
-                    // V[16 tt + 4 q4 + r][32 wave + 16 cw + j] through a transposing read: source
-                    // lane j addresses row 16 tt + 4 q4 + j / 4, columns 32 wave + 16 cw + 4 (j % 4) ..
-                    const i16x4 vr =
-                        lds_read_tr16(Vs + el(16 * tt + 4 * q4 + (j >> 2), 32 * wave + 16 * cw + 4 * (j & 3)));
-                    const v4 vv = __builtin_bit_cast(v4, vr);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float eg = __expf(gt[r]);
-                        // R rounded to CT: it is a 16-bit MFMA operand
-                        R[cw][tt][r] = rnd<CT>(bt[r] * (f(vv[r]) - eg * ksa[cw][r]));
-                        Og[cw][tt][r] = egj * qsa[cw][r];
-                    }
-                }
-            }
-        }
-        __syncthreads();
-        // ---------------- P2: diagonal blocks of T = (I + A)^-1 ----------------
-        solve_diagonal_blocks(Am, wave, lane);
-        __syncthreads();
-        // ---------------- P3: delta, O, state ----------------
-        // delta = T R by block forward substitution over 16-token blocks (T_ii solved above,
-        // A_ij the strictly lower blocks): delta_i = T_ii (R_i - sum_{j<i} A_ij delta_j); and
-        // O_i = e^G Q S0 + sum_{j<=i} Aqk_ij delta_j, on 16x16x16 products whose B operand is a
-        // delta tile in its accumulator layout
-        f32x4 dl[2][4];
-        v4 dbk[2][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f32x4 x[2] = {R[0][i], R[1][i]};
-#pragma unroll
-            for (int jj = 0; jj < i; ++jj) {
-                const v4 na = ld_a4<CT, true>(Am, 16 * i + j, 16 * jj + 4 * q4);
-#pragma unroll
-                for (int cw = 0; cw < 2; ++cw) x[cw] = M16<CT>::mma16(na, dbk[cw][jj], x[cw]);
-            }
-            const v4 ti_ = ld_a4<CT, false>(Am, 16 * i + j, 16 * i + 4 * q4);
-#pragma unroll
-            for (int cw = 0; cw < 2; ++cw) {
-                dl[cw][i] = M16<CT>::mma16(ti_, pack1<CT>(x[cw]), f32x4{0.f, 0.f, 0.f, 0.f});
-                dbk[cw][i] = pack1<CT>(dl[cw][i]);
-            }
-#pragma unroll
-            for (int jj = 0; jj <= i; ++jj) {
-                const v4 aq = *(const v4*)(Aq + (16 * i + j) * TS + 16 * jj + 4 * q4);
-                // (Aqk_ij delta_j)^T = delta_j^T Aqk_ij^T: the delta tile in accumulator layout is
-                // the A operand delta_j^T, the row-major Aqk read the B operand Aqk_ij^T
-#pragma unroll
-                for (int cw = 0; cw < 2; ++cw) Og[cw][i] = M16<CT>::mma16(dbk[cw][jj], aq, Og[cw][i]);
-            }
-        }
-        // O staged over V (dead since P1): four consecutive columns of one token row per lane,
-        // at the reference's output rounding (T), held exactly in CT
-        CT* Os = Vs;
-#pragma unroll
-        for (int cw = 0; cw < 2; ++cw)
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const f16x2 lo = rnd_ct<T>(Og[cw][tt][0], Og[cw][tt][1]), hi = rnd_ct<T>(Og[cw][tt][2], Og[cw][tt][3]);
-                *(v4*)(Os + el(16 * tt + j, 32 * wave + 16 * cw + 4 * q4)) = v4{lo[0], lo[1], hi[0], hi[1]};
-            }
-        const float glast = Gs[CH - 1];
-        const float eglast = __expf(glast);
-        v8 Db[2][2];
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            const f32x4 gt = *(const f32x4*)(Gs + 16 * tt + 4 * q4);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float d = __expf(glast - gt[r]);
-                dl[0][tt][r] *= d;
-                dl[1][tt][r] *= d;
-            }
-        }
-#pragma unroll
-        for (int cw = 0; cw < 2; ++cw) {
-            Db[cw][0] = pack2<CT>(dl[cw][0], dl[cw][1]);
-            Db[cw][1] = pack2<CT>(dl[cw][2], dl[cw][3]);
-        }
-        // S = e^{G_last} S + K^T (e^{G_last - G} delta). The A operand K^T[dk][token] comes
-        // from transposing reads: source lane j addresses K row 32 ks + 4 q4 + j / 4 (+ 16
-        // for elements 4-7), columns 16 rb + 4 (j % 4) .. + 3
-#pragma unroll
-        for (int cw = 0; cw < 2; ++cw)
-#pragma unroll
-            for (int rb = 0; rb < 8; ++rb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) S[cw][rb][r] *= eglast;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int rb = 0; rb < 8; ++rb) {
-                const int kr = 32 * ks + 4 * q4 + (j >> 2);
-                const i16x4 lo = lds_read_tr16(Ks + el(kr, 16 * rb + 4 * (j & 3)));
-                const i16x4 hi = lds_read_tr16(Ks + el(kr + 16, 16 * rb + 4 * (j & 3)));
-                const v8 af = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-                for (int cw = 0; cw < 2; ++cw) S[cw][rb] = M16<CT>::mma(af, Db[cw][ks], S[cw][rb]);
-            }
-        // P4 operands that do not depend on O: the gate norm_w * silu(z) of this thread's rows,
-        // computed before the barrier (rows past the end read a clamped row and are not stored)
-        const int rsub = tid & 15, rrow = tid >> 4;  // 16 lanes per row, 16 rows per pass
-        float gz[4][8];
-        if (FUSED) {
-            tv8 zv[4];
-            const char* const zb = (const char*)fa.z + ((long)t0 * fa.z_tok + (long)h * DV) * (long)sizeof(T);
-#pragma unroll
-            for (int pass = 0; pass < 4; ++pass) {
-                const unsigned tt = (unsigned)(c0 + min(pass * 16 + rrow, Lc - 1));
-                zv[pass] = *(const tv8*)(zb + (__umul24(tt, (unsigned)(fa.z_tok * sizeof(T))) + 16u * rsub));
-            }
-#pragma unroll
-            for (int pass = 0; pass < 4; ++pass)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) gz[pass][e] = fa.norm_w[8 * rsub + e] * silu(f(zv[pass][e]));
-        }
-        __syncthreads();
-        // ---------------- P4: O -> HBM (gated RMSNorm when fused) ----------------
-        char* const ob = (char*)a.o + ((long)t0 * a.o_tok + (long)h * DV) * (long)sizeof(T);
-#pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-            const int r = pass * 16 + rrow;
-            const v8 ov = *(const v8*)(Os + el(r, 8 * rsub));
-            const long tt = t0 + c0 + r;
-            if (FUSED) {
-                float x[8], ss = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    x[e] = f(ov[e]);
-                    ss += x[e] * x[e];
-                }
-                ss = sum16(ss);
-                // a 16-bit operand out of fp16 range makes the row non-finite
-                if (r < Lc && !(ss < __builtin_inff())) range_bad = true;
-                const float inv = fast_rsqrt(ss * (1.0f / 128.0f) + fa.eps);
-                tv8 y;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) y[e] = (T)((x[e] * inv) * gz[pass][e]);
-                if (r < Lc) *(tv8*)(ob + (__umul24((unsigned)(c0 + r), (unsigned)(a.o_tok * sizeof(T))) + 16u * rsub)) = y;
-            } else if (r < Lc) {
-                tv8 y;
-                float ss = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    y[e] = (T)f(ov[e]);  // exact: ov holds T values
-                    ss += f(ov[e]) * f(ov[e]);
-                }
-                if (!(ss < __builtin_inff())) range_bad = true;
-                *(tv8*)((T*)a.o + tt * a.o_tok + (long)h * DV + 8 * rsub) = y;
-            }
-        }
-    }
-    if (range_bad) atomicOr(a.fault, FAULT_RANGE);
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    if (s1) {
-        float* sp = s1 + sbase + (long)(4 * (ln >> 4)) * DV + 32 * wave + (ln & 15);
-#pragma unroll
-        for (int cw = 0; cw < 2; ++cw)
-#pragma unroll
-            for (int rb = 0; rb < 8; ++rb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) sp[(16 * rb + r) * DV + 16 * cw] = S[cw][rb][r];
-    }
-    const long mc = mcol + 8 * (ln & 15);
-    if (FUSED && tail && wave < 3 && (ln >> 4) == 0) {
-        // cache tail: the last 3 raw conv inputs of [history, sequence]; wave ts writes the
-        // channels of q, k or v (16 lanes x 8 channels)
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            const int p = Tn - 3 + i;
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = 0.0f;
-            if (p >= 0) {
-                tv8 x = *(const tv8*)((const T*)fa.mixed + (long)(t0 + p) * fa.mixed_tok + mc);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = f(x[e]);
-            } else if (hist) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = f(hist[((long)mc + e) * 3 + (p + 3)]);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) tail[((long)mc + e) * 3 + i] = (T)v[e];
-        }
-    }
-}
-
-}  // namespace gdn16
-}  // namespace hk
-
-template <typename T, bool FUSED>
-static int launch16(const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs, hipStream_t stream) {
-    auto kern = hk::gdn16::gdn_chunk16<T, FUSED>;
-    // set once, under C++'s thread-safe static initialisation (replicas launch from several threads)
-    static const bool configured = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       (int)hk::gdn16::LDS_BYTES) == hipSuccess;
-    if (!configured) return HK_ERR_DEVICE;
-    hipLaunchKernelGGL(kern, dim3(a->H, n_seqs), dim3(hk::gdn16::NTHREADS), hk::gdn16::LDS_BYTES, stream, *a, *fa);
-    return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
-}
+int hk_launch_gdn16_standalone(int dtype16, const hk::GdnArgs* a, int n_seqs, hipStream_t stream);
 
 // dtype16: 1 = bf16, 2 = fp16
 extern "C" int hk_launch_gdn16(int dtype16, int fused, const hk::GdnArgs* a, const hk::GdnFusedArgs* fa, int n_seqs,
                                hipStream_t stream) {
-    hk::GdnFusedArgs none{};
-    if (!fa) fa = &none;
-    if (dtype16 == 1)
-        return fused ? launch16<hk::bf16, true>(a, fa, n_seqs, stream) : launch16<hk::bf16, false>(a, fa, n_seqs, stream);
-    return fused ? launch16<hk::f16, true>(a, fa, n_seqs, stream) : launch16<hk::f16, false>(a, fa, n_seqs, stream);
+    if (!fused) return hk_launch_gdn16_standalone(dtype16, a, n_seqs, stream);
+    if (!fa) return HK_ERR_INVALID;
+    return dtype16 == 1 ? launch16<hk::bf16, true>(a, fa, n_seqs, stream) : launch16<hk::f16, true>(a, fa, n_seqs, stream);
 }
