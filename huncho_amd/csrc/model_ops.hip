@@ -374,47 +374,64 @@ __global__ __launch_bounds__(256) void swiglu_x8(SwigluArgs a) {
     }
 }
 
+// Four tokens per 256-thread workgroup, one wave per token; rows move as 16-byte vectors when
+// the row size and both bases allow it.
 template <typename T>
-__global__ void embed_gather(const int* ids, int n, const void* table, int vocab, int width, void* out, int* fault) {
-    const int t = blockIdx.x;
+__global__ __launch_bounds__(256) void embed_gather(const int* ids, int n, const void* table, int vocab, int width,
+                                                    void* out, int* fault) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (t >= n) return;
     const int id = ids[t];
     if (id < 0 || id >= vocab) {
-        if (threadIdx.x == 0) atomicOr(fault, 8);
+        if (lane == 0) atomicOr(fault, 8);
         return;
     }
     const T* src = (const T*)table + (long)id * width;
     T* dst = (T*)out + (long)t * width;
-    for (int i = threadIdx.x; i < width; i += blockDim.x) dst[i] = src[i];
+    const long bytes = (long)width * (long)sizeof(T);
+    if (bytes % 16 == 0 && ((uintptr_t)table & 15) == 0 && ((uintptr_t)out & 15) == 0) {
+        const int nv = (int)(bytes / 16);
+        for (int i = lane; i < nv; i += 64) ((uint4*)dst)[i] = ((const uint4*)src)[i];
+    } else {
+        for (int i = lane; i < width; i += 64) dst[i] = src[i];
+    }
 }
 
-// One workgroup (one wave) per sequence: final RMSNorm of the last token, rounded to T,
-// then logits[c] = sum_i h[i] * W[c][i] (+ b[c]) in fp32.
+// One 256-thread workgroup per sequence: final RMSNorm of the last token (rounded to T, as the
+// reference stores the hidden row), then logits[c] = sum_i h[i] * W[c][i] (+ b[c]) in fp32, wave w
+// taking outputs w, w + 4, ...; the normalised row is staged in LDS once.
 template <typename T>
-__global__ void final_norm_head(const void* x, long x_tok, const int* cu, const float* w_eff, float eps, int width,
-                                const void* head_w, const float* head_b, int n_out, float* logits, void* h_out) {
-    const int s = blockIdx.x, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void final_norm_head(const void* x, long x_tok, const int* cu, const float* w_eff,
+                                                       float eps, int width, const void* head_w, const float* head_b,
+                                                       int n_out, float* logits, void* h_out) {
+    extern __shared__ float hrow[];  // [width], then the sum of squares
+    float* red = hrow + width;
+    const int s = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int t = cu[s + 1] - 1;
     const T* xr = (const T*)x + (long)t * x_tok;
-    float ss = 0.0f;
-    for (int i = lane; i < width; i += 64) {
-        float v = to_f(xr[i]);
-        ss += v * v;
-    }
-    ss = wsum(ss);
-    const float denom = sqrtf(ss / (float)width + eps);
-    for (int c = 0; c < n_out; ++c) {
-        float acc = 0.0f;
+    if (wave == 0) {  // the sum of squares in one wave, in the same order as the logits' sums
+        float ss = 0.0f;
         for (int i = lane; i < width; i += 64) {
-            float hv = rndt<T>((to_f(xr[i]) / denom) * w_eff[i]);
-            acc += hv * to_f(((const T*)head_w)[(long)c * width + i]);
+            const float v = to_f(xr[i]);
+            ss += v * v;
         }
+        ss = wsum(ss);
+        if (lane == 0) red[0] = ss;
+    }
+    __syncthreads();
+    const float denom = sqrtf(red[0] / (float)width + eps);
+    for (int i = tid; i < width; i += 256) {
+        const float hv = rndt<T>((to_f(xr[i]) / denom) * w_eff[i]);
+        hrow[i] = hv;
+        if (h_out) ((T*)h_out)[(long)s * width + i] = from_f<T>(hv);
+    }
+    __syncthreads();
+    for (int c = wave; c < n_out; c += 4) {
+        float acc = 0.0f;
+        for (int i = lane; i < width; i += 64) acc += hrow[i] * to_f(((const T*)head_w)[(long)c * width + i]);
         acc = wsum(acc);
         if (lane == 0) logits[(long)s * n_out + c] = head_b ? acc + head_b[c] : acc;
     }
-    if (h_out)
-        for (int i = lane; i < width; i += 64)
-            ((T*)h_out)[(long)s * width + i] = from_f<T>((to_f(xr[i]) / denom) * w_eff[i]);
 }
 
 }  // namespace hk
@@ -429,6 +446,16 @@ using namespace hk;
             hipLaunchKernelGGL(KERNEL<f16>, GRID, BLOCK, 0, st, __VA_ARGS__);   \
         else                                                                    \
             hipLaunchKernelGGL(KERNEL<float>, GRID, BLOCK, 0, st, __VA_ARGS__); \
+    } while (0)
+
+#define HK_DISPATCH3_LDS(KERNEL, GRID, BLOCK, LDS, ...)                          \
+    do {                                                                          \
+        if (dtype == DT_BF16)                                                     \
+            hipLaunchKernelGGL(KERNEL<bf16>, GRID, BLOCK, LDS, st, __VA_ARGS__);  \
+        else if (dtype == DT_F16)                                                 \
+            hipLaunchKernelGGL(KERNEL<f16>, GRID, BLOCK, LDS, st, __VA_ARGS__);   \
+        else                                                                      \
+            hipLaunchKernelGGL(KERNEL<float>, GRID, BLOCK, LDS, st, __VA_ARGS__); \
     } while (0)
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -505,7 +532,7 @@ extern "C" int hk_launch_swiglu(int dtype, const SwigluArgs* a, hipStream_t st) 
 extern "C" int hk_launch_embed(int dtype, const int* ids, int n, const void* table, int vocab, int width, void* out,
                                int* fault, hipStream_t st) {
     if (n == 0) return HK_OK;
-    HK_DISPATCH3(embed_gather, dim3(n), dim3(128), ids, n, table, vocab, width, out, fault);
+    HK_DISPATCH3(embed_gather, dim3((n + 3) / 4), dim3(256), ids, n, table, vocab, width, out, fault);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
@@ -513,8 +540,10 @@ extern "C" int hk_launch_final_norm_head(int dtype, const void* x, long x_tok, c
                                          const float* w_eff, float eps, int width, const void* head_w,
                                          const float* head_b, int n_out, float* logits, void* h_out, hipStream_t st) {
     if (n_seqs == 0) return HK_OK;
-    HK_DISPATCH3(final_norm_head, dim3(n_seqs), dim3(64), x, x_tok, cu, w_eff, eps, width, head_w, head_b, n_out,
-                 logits, h_out);
+    const size_t lds = ((size_t)width + 4) * sizeof(float);
+    if (lds > 64 * 1024) return HK_ERR_UNSUPPORTED;
+    HK_DISPATCH3_LDS(final_norm_head, dim3(n_seqs), dim3(256), lds, x, x_tok, cu, w_eff, eps, width, head_w, head_b,
+                     n_out, logits, h_out);
     return hipGetLastError() == hipSuccess ? HK_OK : HK_ERR_DEVICE;
 }
 
