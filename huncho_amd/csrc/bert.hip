@@ -486,6 +486,30 @@ __global__ __launch_bounds__(256) void mean_pool_partial(MeanPoolArgs a) {
     if (j >= P) return;
     const long ta = t0 + (long)L * j / P, tb = t0 + (long)L * (j + 1) / P;
     const T* x = (const T*)a.x;
+    float* const out = a.pool + ((long)seq * POOL_PARTS + j) * a.width;
+    if (sizeof(T) == 2 && a.width % 8 == 0 && a.width <= 1024 && a.x_tok % 8 == 0 && ((uintptr_t)x & 15) == 0) {
+        // 16-byte rows: thread c8 sums columns 8 c8 .. 8 c8 + 7 over the range's even rows and
+        // thread c8 + 128 over its odd rows (eight independent sums each); the two halves are
+        // added through LDS
+        __shared__ float half1[1024];
+        const int groups = a.width / 8, c8 = threadIdx.x & 127, parity = threadIdx.x >> 7;
+        float acc[8] = {};
+        if (c8 < groups && parity < 2) {
+            for (long t = ta + parity; t < tb; t += 2) {
+                const typename Vec16<T>::type v = *(const typename Vec16<T>::type*)(x + t * a.x_tok + 8 * c8);
+#pragma unroll
+                for (int e = 0; e < Vec16<T>::N; ++e) acc[e] += to_f(v[e]);
+            }
+            if (parity == 1)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) half1[8 * c8 + e] = acc[e];
+        }
+        __syncthreads();
+        if (c8 < groups && parity == 0)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) out[8 * c8 + e] = acc[e] + half1[8 * c8 + e];
+        return;
+    }
     for (int i = threadIdx.x; i < a.width; i += blockDim.x) {
         float s0 = 0.0f, s1 = 0.0f;
         long t = ta;
@@ -494,7 +518,7 @@ __global__ __launch_bounds__(256) void mean_pool_partial(MeanPoolArgs a) {
             s1 += to_f(x[(t + 1) * a.x_tok + i]);
         }
         if (t < tb) s0 += to_f(x[t * a.x_tok + i]);
-        a.pool[((long)seq * POOL_PARTS + j) * a.width + i] = s0 + s1;
+        out[i] = s0 + s1;
     }
 }
 
