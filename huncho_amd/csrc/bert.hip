@@ -531,9 +531,19 @@ __global__ __launch_bounds__(256) void mean_pool_head(MeanPoolArgs a) {
     const int t0 = a.cu[seq], L = a.cu[seq + 1] - t0;
     if (t0 < 0 || L <= 0 || t0 + L > a.n_tokens) return;  // reported by pass 1
     const int P = min(POOL_PARTS, L);
+    const float* const part = a.pool + (long)seq * POOL_PARTS * a.width;
     for (int i = threadIdx.x; i < a.width; i += blockDim.x) {
+        // parts added in index order; eight loads are issued ahead of their adds
         float s = 0.0f;
-        for (int j = 0; j < P; ++j) s += a.pool[((long)seq * POOL_PARTS + j) * a.width + i];
+        int j = 0;
+        for (; j + 8 <= P; j += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = part[(long)(j + k) * a.width + i];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s += v[k];
+        }
+        for (; j < P; ++j) s += part[(long)j * a.width + i];
         pooled[i] = s / (float)L;
     }
     __syncthreads();
